@@ -1,0 +1,208 @@
+"""bench.py -- the dit-step on one MI355X: ms per step at 1024px bf16, and the MFMA roofline.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--resolution 1024] [--no-cpu]
+
+One step is one PixArt-Sigma dit-step forward (28 blocks, hidden 1152, 16 heads x 72, MLP 4608)
+at batch 2 (classifier-free guidance) over a 128x128x4 latent (4096 image tokens) and a
+300-token caption of width 4096, through the library's fused engine (bh_dit_forward). Weights
+(~N(0, 0.02)), latent and caption (~N(0, 1)) are seeded synthetic bf16, resident in HBM before
+the timed region. K steps are timed between two HIP events on the engine's stream, bracketed by
+device synchronisation.
+
+The JSON line also carries:
+  roofline      the dominant kernel (largest share of step time): algorithmic FLOP per launch
+                over its average launch duration, timed live with HIP events around each of its
+                launches in the timed region, against the 2.5166 PFLOP/s dense bf16 MFMA peak;
+  step          the whole step's algorithmic FLOP (the reference's accounting,
+                eval/burnscore/geometry.py:275-367) over the measured step time, same peak;
+  kernels       per-class time of one separately profiled step (not the timed region);
+  cpu_baseline  the stock oracle's dit-step on this host's cores, on a bounded sample: the
+                prologue plus one and two blocks at the same 1024px shape, extrapolated to 28
+                blocks by the per-block time (the graph is a fixed prologue, 28 identical blocks
+                and a head).
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "dit-step ms @1024px bf16 (1 GPU) + % of MI355X bf16 MFMA roofline"
+PEAK_BF16_TFLOPS = 2516.6          # 256 CU x 4096 FLOP/clk x 2.4 GHz, dense
+PEAK_HBM_GBS = 8000.0
+REFERENCE_5090_MS = 97.85          # eval/cells/BG-1/reference.json:28 (RTX 5090, cuda impl)
+HW = {512: 64, 1024: 128, 2048: 256}
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def parse() -> argparse.Namespace:
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=3)
+    p.add_argument("--resolution", type=int, default=1024, choices=sorted(HW))
+    p.add_argument("--caption-len", type=int, default=300)
+    p.add_argument("--batch", type=int, default=2)
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    p.add_argument("--cpu-threads", type=int, default=0)
+    return p.parse_args()
+
+
+def cpu_baseline(wl, threads: int) -> dict:
+    """The stock oracle on this host: prologue + 1 block and prologue + 2 blocks, timed."""
+    import numpy as np
+    import oracle
+    from burnisher_amd.workload import config_struct
+
+    cfg = config_struct(wl.cfg)
+    w, keep = wl.weight_struct(wl.top, wl.blocks)
+    out = np.zeros((wl.batch, wl.cfg["out_channels"], wl.latent_hw, wl.latent_hw), np.uint16)
+    times = {}
+    for layers in (1, 2):
+        t0 = time.perf_counter()
+        oracle.call(oracle.stock(), "stock_dit_forward", ctypes.byref(cfg), ctypes.byref(w),
+                    wl.batch, wl.latent_hw, wl.caption_len, wl.latent.ctypes.data, wl.timestep,
+                    wl.caption.ctypes.data, wl.mask.ctypes.data, 0, out.ctypes.data, threads,
+                    layers)
+        times[layers] = time.perf_counter() - t0
+        log(f"cpu baseline: prologue + {layers} block(s) in {times[layers]:.2f} s")
+    per_block = times[2] - times[1]
+    fixed = times[1] - per_block
+    step_s = fixed + wl.cfg["num_layers"] * per_block
+    return {"value": round(step_s * 1e3, 1), "unit": "ms", "cores": threads, "kind": "port",
+            "sample": (f"stock oracle (oracle/stock.cpp) dit-step at the same 1024px B=2 shape, "
+                       f"run with 1 and with 2 of the 28 blocks ({times[1]:.1f} s, "
+                       f"{times[2]:.1f} s); step = prologue/head + 28 x per-block time")}
+
+
+def main() -> int:
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
+              "(the dit-step would shard on the CFG batch, see DESIGN.md)", file=sys.stderr)
+        return 2
+    import numpy as np
+    import torch
+
+    import burnisher_amd as bh
+    from burnisher_amd.workload import PIXART_SIGMA, config_struct, dit_step_flops, make_workload
+
+    bh.check(bh.lib().bh_init(0), "bh_init")
+    hw = HW[args.resolution]
+    log(f"generating the {args.resolution}px workload (seeded synthetic bf16)")
+    wl = make_workload(PIXART_SIGMA, batch=args.batch, latent_hw=hw, caption_len=args.caption_len)
+    top, blocks, latent, caption, mask = wl.to_device()
+    cfg = config_struct(wl.cfg)
+    w, keep = wl.weight_struct(top, blocks)
+    handle = ctypes.c_void_p()
+    bh.call("bh_dit_create", ctypes.byref(cfg), ctypes.byref(w), wl.batch, hw, wl.caption_len,
+            bh.DIT_FUSED, ctypes.byref(handle))
+    out = torch.zeros((wl.batch, cfg.out_channels, hw, hw), dtype=torch.bfloat16, device="cuda")
+    stream = torch.cuda.Stream()
+    sp = stream.cuda_stream
+
+    def step():
+        bh.call("bh_dit_forward", handle, latent.data_ptr(), wl.timestep, caption.data_ptr(),
+                mask.data_ptr(), bh.F32, out.data_ptr(), sp)
+
+    flops = dit_step_flops(wl.cfg, batch=wl.batch, latent_hw=hw, caption_len=wl.caption_len)
+    with torch.cuda.stream(stream):
+        for _ in range(max(1, args.warmup)):
+            step()
+    torch.cuda.synchronize()
+    log("warmup done")
+
+    # one profiled step, every class, for the breakdown and to name the dominant kernel
+    classes = {name: i for i, name in enumerate(bh.KERNEL_CLASSES)}
+    bh.call("bh_profile_enable", (1 << len(classes)) - 1)
+    with torch.cuda.stream(stream):
+        step()
+    torch.cuda.synchronize()
+    breakdown = {}
+    for name, i in classes.items():
+        ms, n, work = ctypes.c_double(), ctypes.c_int64(), ctypes.c_double()
+        bh.call("bh_profile_read", i, ctypes.byref(ms), ctypes.byref(n), ctypes.byref(work))
+        if n.value:
+            breakdown[name] = {"ms": round(ms.value, 4), "launches": n.value, "work": work.value}
+    bh.call("bh_profile_enable", 0)
+    exclusive = ["attention_self", "attention_cross", "gemm_ff0", "gemm_ff2", "gemm_qkv", "norm"]
+    dominant = max((c for c in exclusive if c in breakdown), key=lambda c: breakdown[c]["ms"])
+    log(f"profiled step: {json.dumps(breakdown)}; dominant kernel {dominant}")
+
+    # the timed region: K steps, HIP events around the dominant kernel's launches
+    bh.call("bh_profile_enable", 1 << classes[dominant])
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    with torch.cuda.stream(stream):
+        start.record(stream)
+        for _ in range(args.steps):
+            step()
+        stop.record(stream)
+    torch.cuda.synchronize()
+    total_ms = start.elapsed_time(stop)
+    ms_per_step = total_ms / args.steps
+    dms, dn, dwork = ctypes.c_double(), ctypes.c_int64(), ctypes.c_double()
+    bh.call("bh_profile_read", classes[dominant], ctypes.byref(dms), ctypes.byref(dn), ctypes.byref(dwork))
+    bh.call("bh_profile_enable", 0)
+    avg_launch_ms = dms.value / max(1, dn.value)
+    work_per_launch = dwork.value / max(1, dn.value)
+    achieved = work_per_launch / (avg_launch_ms * 1e-3) / 1e12
+    log(f"timed {args.steps} steps: {ms_per_step:.3f} ms/step; {dominant}: {dn.value} launches, "
+        f"{avg_launch_ms * 1e3:.1f} us avg, {achieved:.1f} TFLOP/s")
+
+    # parity sanity on the timed output: finite and not constant
+    res = out.float()
+    assert torch.isfinite(res).all() and res.std() > 1e-3, "degenerate dit-step output"
+
+    step_tflops = flops["total"] / (ms_per_step * 1e-3) / 1e12
+    line = {
+        "metric": METRIC,
+        "value": round(ms_per_step, 4),
+        "unit": "ms",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": round(ms_per_step / REFERENCE_5090_MS, 4) if args.resolution == 1024 else None,
+        "vs_baseline_basis": "value / 97.85 ms, the reference's published dit-step at this config "
+                             "on an RTX 5090 (eval/cells/BG-1/reference.json:28); lower is better",
+        "dtype": "bf16",
+        "data": "synthetic: seeded N(0,0.02) bf16 weights, N(0,1) latent and caption, timestep 500",
+        "config": {"workload": f"PixArt-Sigma dit-step {args.resolution}px, batch 2 (CFG), "
+                               f"caption {wl.caption_len}, 28 blocks",
+                   "resolution": args.resolution, "latent": [wl.batch, 4, hw, hw],
+                   "tokens": wl.tokens, "batch": wl.batch, "caption_len": wl.caption_len,
+                   "layers": wl.cfg["num_layers"], "engine": "bh_dit_forward (fused plan)"},
+        "roofline": {"bound": "mfma", "kernel": dominant,
+                     "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                     "avg_launch_us": round(avg_launch_ms * 1e3, 2), "launches": dn.value,
+                     "flop_per_launch": work_per_launch},
+        "step": {"flop": flops["total"], "tflops": round(step_tflops, 2),
+                 "mfma_frac": round(step_tflops / PEAK_BF16_TFLOPS, 4),
+                 "ceiling_ms": round(flops["total"] / (PEAK_BF16_TFLOPS * 1e12) * 1e3, 3)},
+        "kernels": breakdown,
+    }
+    bh.lib().bh_dit_destroy(handle)
+    if not args.no_cpu:
+        threads = args.cpu_threads or min(16, os.cpu_count() or 1)
+        log(f"cpu baseline on {threads} threads")
+        line["cpu_baseline"] = cpu_baseline(wl, threads)
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

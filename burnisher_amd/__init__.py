@@ -1,0 +1,149 @@
+"""burnisher_amd -- Python access to libburnisher_hip.so, the gfx950 dit-step library.
+
+The library's C ABI (include/burnisher_hip.h) is the product boundary; this module only loads
+it with ctypes and wraps each entry point so that a failing status raises `BurnisherError` with
+the library's message. Device memory and streams come from PyTorch (tensors are passed by
+`data_ptr()`); PyTorch computes nothing here.
+
+If the library is missing this module raises on first use -- there is no CPU fallback.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+LIB_PATH = PKG / "lib" / "libburnisher_hip.so"
+
+F32, BF16 = 0, 1
+EPI_NONE, EPI_GELU, EPI_SILU, EPI_GELU_GATED = 0, 1, 2, 3
+DIT_FUSED, DIT_OPWISE = 0, 1
+(K_GEMM, K_GEMV, K_ATTN_SELF, K_ATTN_CROSS, K_NORM, K_ELEMENTWISE, K_GEMM_FF0, K_GEMM_FF2,
+ K_GEMM_QKV) = range(9)
+KERNEL_CLASSES = ["gemm", "gemv", "attention_self", "attention_cross", "norm", "elementwise",
+                  "gemm_ff0", "gemm_ff2", "gemm_qkv"]
+
+
+class BurnisherError(RuntimeError):
+    pass
+
+
+# ---- C structs (include/burnisher_hip.h) --------------------------------------------------
+
+class GemmFused(ctypes.Structure):
+    _fields_ = [("epilogue", ctypes.c_int), ("round_mid", ctypes.c_int),
+                ("row_add", ctypes.c_void_p), ("row_add_period", ctypes.c_int64),
+                ("residual", ctypes.c_void_p), ("gate", ctypes.c_void_p),
+                ("gate_rows", ctypes.c_int64), ("ld_out", ctypes.c_int64)]
+
+
+class DitConfig(ctypes.Structure):
+    _fields_ = [("num_layers", ctypes.c_int), ("num_heads", ctypes.c_int),
+                ("head_dim", ctypes.c_int), ("patch_size", ctypes.c_int),
+                ("in_channels", ctypes.c_int), ("out_channels", ctypes.c_int),
+                ("caption_channels", ctypes.c_int), ("sample_size", ctypes.c_int),
+                ("mlp_ratio", ctypes.c_double), ("eps", ctypes.c_double)]
+
+
+BLOCK_FIELDS = ["scale_shift_table",
+                "attn1_q_w", "attn1_q_b", "attn1_k_w", "attn1_k_b", "attn1_v_w", "attn1_v_b",
+                "attn1_o_w", "attn1_o_b",
+                "attn2_q_w", "attn2_q_b", "attn2_k_w", "attn2_k_b", "attn2_v_w", "attn2_v_b",
+                "attn2_o_w", "attn2_o_b",
+                "ff0_w", "ff0_b", "ff2_w", "ff2_b"]
+TOP_FIELDS = ["pos_embed_w", "pos_embed_b", "t_emb1_w", "t_emb1_b", "t_emb2_w", "t_emb2_b",
+              "adaln_w", "adaln_b", "cap1_w", "cap1_b", "cap2_w", "cap2_b", "out_table",
+              "proj_out_w", "proj_out_b"]
+
+
+class DitBlockWeights(ctypes.Structure):
+    _fields_ = [(f, ctypes.c_void_p) for f in BLOCK_FIELDS]
+
+
+class DitWeights(ctypes.Structure):
+    _fields_ = [(f, ctypes.c_void_p) for f in TOP_FIELDS] + [
+        ("blocks", ctypes.POINTER(DitBlockWeights))]
+
+
+# ---- loading -------------------------------------------------------------------------------
+
+_lib = None
+
+_V, _I, _I64, _F, _D = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_float, ctypes.c_double
+SIGNATURES = {
+    "bh_abi_version": ([], _I),
+    "bh_build_info": ([], ctypes.c_char_p),
+    "bh_last_error": ([], ctypes.c_char_p),
+    "bh_init": ([_I], _I),
+    "bh_synchronize": ([_V], _I),
+    "bh_gemm": ([_V, _V, _V, _V, _I64, _I64, _I64, _I, _I, _I, _V], _I),
+    "bh_gemm_fused_run": ([_V, _V, _V, _V, _I64, _I64, _I64, ctypes.POINTER(GemmFused), _V], _I),
+    "bh_attention": ([_V, _V, _V, _V, _I64, _I64, _I64, _I64, _I64, _F, _V, _V, _I, _I, _V], _I),
+    "bh_attention_strided": ([_V, _I64, _V, _V, _I64, _V, _I64, _I64, _I64, _I64, _I64, _I64, _F,
+                              _V, _I, _I, _V], _I),
+    "bh_norm": ([_V, _V, _V, _V, _I64, _I64, _F, _I, _I64, _I64, _I, _V], _I),
+    "bh_modulate": ([_V, _V, _V, _V, _I64, _I64, _I64, _V, _V, _I, _V], _I),
+    "bh_activation": ([_V, _V, _I64, _I, _V, _I, _V], _I),
+    "bh_add": ([_V, _V, _V, _I64, _I64, _F, _I, _I, _V], _I),
+    "bh_chunk": ([_V, _V, _V, _I64, _I64, _I64, _I64, _I64, _I, _V], _I),
+    "bh_patch": ([_V, _V, _I64, _I64, _I64, _I64, _I, _I, _V], _I),
+    "bh_norm_modulate": ([_V, _V, _I64, _I64, _I64, _V, _I64, _I64, _V, _I64, _I64, _I64, _F, _V],
+                         _I),
+    "bh_dit_create": ([ctypes.POINTER(DitConfig), ctypes.POINTER(DitWeights), _I64, _I64, _I64, _I,
+                       ctypes.POINTER(_V)], _I),
+    "bh_dit_forward": ([_V, _V, _D, _V, _V, _I, _V, _V], _I),
+    "bh_dit_workspace_bytes": ([_V], _I64),
+    "bh_dit_destroy": ([_V], None),
+    "bh_profile_enable": ([_I], _I),
+    "bh_profile_read": ([_I, ctypes.POINTER(_D), ctypes.POINTER(_I64), ctypes.POINTER(_D)], _I),
+    "bh_fill_normal_bf16": ([_V, _I64, ctypes.c_uint64, ctypes.c_char_p, _F], _I),
+}
+
+
+def lib() -> ctypes.CDLL:
+    """The loaded library. Raises if it has not been built (python -m burnisher_amd.build)."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise BurnisherError(
+                f"{LIB_PATH} is missing: build it with `python -m burnisher_amd.build` "
+                "(there is no CPU fallback for the hip-gfx950 path)")
+        handle = ctypes.CDLL(str(LIB_PATH), mode=os.RTLD_NOW | os.RTLD_LOCAL)
+        for name, (args, ret) in SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.argtypes = args
+            fn.restype = ret
+        _lib = handle
+    return _lib
+
+
+def check(status: int, what: str = "") -> None:
+    if status != 0:
+        msg = lib().bh_last_error().decode(errors="replace")
+        raise BurnisherError(f"{what}: {msg}" if what else msg)
+
+
+def call(name: str, *args):
+    """Calls entry point `name`; a nonzero status raises BurnisherError with its message."""
+    status = getattr(lib(), name)(*args)
+    check(status, name)
+
+
+def ptr(t) -> int | None:
+    """Device (or host) address of a torch tensor, None for None."""
+    return None if t is None else t.data_ptr()
+
+
+def stream_ptr(stream=None) -> int | None:
+    import torch
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return s.cuda_stream
+
+
+def fill_normal_bf16(n: int, name: str, seed: int, std: float):
+    """n draws of N(0, std^2) as a uint16 numpy array of bf16 bits (host), keyed by name."""
+    import numpy as np
+    out = np.empty(n, dtype=np.uint16)
+    call("bh_fill_normal_bf16", out.ctypes.data, n, seed, name.encode(), std)
+    return out

@@ -1,0 +1,190 @@
+// Internal declarations shared by the HIP kernels and the C-ABI layer of libburnisher_hip.so.
+//
+// Numerics contract (the reference oracle, src/cpu/ops_cpu.cpp and src/core/tensor.cpp:85-96):
+// every op reads bf16 as float exactly, computes in fp32 and rounds once per stored element with
+// round-to-nearest-even. Elementwise kernels here use non-contracting fp32 operations
+// (__fadd_rn/__fmul_rn) wherever the oracle does a separate multiply and add, so they reproduce
+// the oracle bit for bit; only the GEMM and attention reductions differ in summation order.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <stdexcept>
+#include <string>
+
+namespace bh {
+
+using bf16_t = uint16_t;
+
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_t;
+typedef __attribute__((__vector_size__(4 * sizeof(__bf16)))) __bf16 bf16x4_t;
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4_t;
+
+// ---- bf16 storage ---------------------------------------------------------------------------
+
+__host__ __device__ inline float bf2f(bf16_t v) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    return __uint_as_float(static_cast<uint32_t>(v) << 16);
+#else
+    uint32_t u = static_cast<uint32_t>(v) << 16;
+    float f;
+    __builtin_memcpy(&f, &u, 4);
+    return f;
+#endif
+}
+
+// Round-to-nearest-even, NaN kept NaN (dtype.h:64-72 semantics).
+__host__ __device__ inline bf16_t f2bf(float f) {
+    uint32_t u;
+#if defined(__HIP_DEVICE_COMPILE__)
+    u = __float_as_uint(f);
+#else
+    __builtin_memcpy(&u, &f, 4);
+#endif
+    if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<bf16_t>((u >> 16) | 0x0040u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return static_cast<bf16_t>(u >> 16);
+}
+
+// What a store through the tensor dtype does to a float.
+__host__ __device__ inline float round_bf16(float f) { return bf2f(f2bf(f)); }
+
+// ---- errors ---------------------------------------------------------------------------------
+
+struct Error : std::runtime_error {
+    using std::runtime_error::runtime_error;
+};
+
+inline void hip_check(hipError_t e, const char* what) {
+    if (e != hipSuccess) throw Error(std::string("hip: ") + what + ": " + hipGetErrorString(e));
+}
+
+// Checked after every launch: an asynchronous launch failure otherwise surfaces as a wrong
+// number in a later op.
+inline void launch_check(const char* what) {
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        throw Error(std::string("hip: ") + what + " launch: " + hipGetErrorString(e));
+    }
+}
+
+inline void require(bool ok, const std::string& msg) {
+    if (!ok) throw Error(msg);
+}
+
+// The C boundary: the message of the last failing call on this host thread (capi.cpp).
+void set_last_error(const std::string& msg);
+
+// Runs `fn`, turning an exception into status 1 plus a message for bh_last_error().
+template <typename Fn>
+int guarded(Fn&& fn) {
+    try {
+        fn();
+        set_last_error("");
+        return 0;
+    } catch (const std::exception& e) {
+        set_last_error(e.what());
+        return 1;
+    } catch (...) {
+        set_last_error("unknown error");
+        return 1;
+    }
+}
+
+// ---- launch profiler (capi.cpp) -------------------------------------------------------------
+
+enum KernelClass {
+    K_GEMM = 0,
+    K_GEMV = 1,
+    K_ATTN_SELF = 2,
+    K_ATTN_CROSS = 3,
+    K_NORM = 4,
+    K_ELEMENTWISE = 5,
+    K_GEMM_FF0 = 6,
+    K_GEMM_FF2 = 7,
+    K_GEMM_QKV = 8,
+    K_COUNT = 9
+};
+
+// RAII bracket: records a start event on construction and a stop event on destruction, on
+// `stream`, when profiling is enabled; a no-op otherwise. `work` is the algorithmic FLOP (or
+// bytes) of the launch. `also` is a second class credited with the same interval (-1: none).
+struct ProfileScope {
+    ProfileScope(int cls, hipStream_t stream, double work, int also = -1);
+    ~ProfileScope();
+    int cls_, also_;
+    hipStream_t stream_;
+    double work_;
+    int slot_ = -1;
+};
+
+// Engine hint: which engine GEMM is running, so its launch is also credited to a sub-class.
+void set_gemm_subclass(int cls);
+int gemm_subclass();
+
+// ---- kernel launchers (one per .hip file) ---------------------------------------------------
+
+struct GemmEpilogue {
+    int act = 0;               // 0 none, 1 gelu-tanh, 2 silu
+    bool round_mid = false;    // round epilogue(acc+bias) to bf16 before row_add/residual
+    const bf16_t* row_add = nullptr;
+    int64_t row_add_period = 1;
+    const bf16_t* residual = nullptr;
+    const bf16_t* gate = nullptr;
+    int64_t gate_rows = 1;
+    int64_t ld_out = 0;        // 0 means n
+};
+
+// bf16 out[m, n] = A[m, k] . B[n, k]^T (+bias) with `ep`. Picks the MFMA tile kernel, the
+// small-M kernel or the reference-order kernel by shape.
+void launch_gemm_bf16(const bf16_t* a, const bf16_t* b, const bf16_t* bias, bf16_t* out,
+                      int64_t m, int64_t n, int64_t k, const GemmEpilogue& ep, hipStream_t s);
+// Any dtype / layout, reference summation order: one thread per output (tests, fp32, [K,N] B).
+void launch_gemm_generic(const void* a, const void* b, const void* bias, void* out, int64_t m,
+                         int64_t n, int64_t k, bool b_transposed, int act, bool f32,
+                         hipStream_t s);
+
+struct AttnShape {
+    int64_t batch, heads, q_len, kv_len, head_dim;
+    int64_t ld_q, ld_kv, ld_o;  // row strides in elements
+    float scale;                // resolved (never 0)
+};
+void launch_attention_bf16(const bf16_t* q, const bf16_t* k, const bf16_t* v, bf16_t* out,
+                           const AttnShape& sh, const void* key_mask, bool mask_f32,
+                           hipStream_t s);
+// Reference-order attention (one thread per query row), any dtype, additive bias supported.
+void launch_attention_generic(const void* q, const void* k, const void* v, void* out,
+                              const AttnShape& sh, const void* bias, const void* key_mask,
+                              bool mask_f32, bool f32, hipStream_t s);
+
+void launch_norm(const void* x, const void* weight, const void* bias, void* out, int64_t rows,
+                 int64_t cols, float eps, bool rms, bool f32, hipStream_t s);
+void launch_norm_modulate(const bf16_t* x, const bf16_t* mod, int64_t mod_chunks,
+                          int64_t shift_chunk, int64_t scale_chunk, const bf16_t* table,
+                          int64_t shift_row, int64_t scale_row, bf16_t* out, int64_t batch,
+                          int64_t tokens, int64_t channels, float eps, hipStream_t s);
+// Same, reading precomputed (already rounded) shift/scale rows of [batch, channels].
+void launch_norm_modulate_pre(const bf16_t* x, const bf16_t* shift, const bf16_t* scale,
+                              bf16_t* out, int64_t batch, int64_t tokens, int64_t channels,
+                              float eps, hipStream_t s);
+void launch_modulate(const void* x, const void* scale, const void* shift, void* out,
+                     int64_t batch, int64_t tokens, int64_t channels, const void* residual,
+                     const void* gate, bool f32, hipStream_t s);
+void launch_activation(const void* x, void* out, int64_t numel, int kind, const void* gate,
+                       bool f32, hipStream_t s);
+void launch_add(const void* a, const void* b, void* out, int64_t outer, int64_t inner,
+                float scale, bool broadcast_b, bool f32, hipStream_t s);
+void launch_chunk(const void* mod, const void* table, void* out, int64_t batch, int64_t channels,
+                  int64_t chunks, int64_t chunk, int64_t table_chunk, bool f32, hipStream_t s);
+// Every chunk of every layer at once: out[l][c6][b][ch] = mod[b, c6*ch_n + ch] + tables[l][c6, ch]
+// where tables is `layers` pointers to [6, channels] tables.
+void launch_chunk_all(const bf16_t* mod, const bf16_t* const* tables_dev, bf16_t* out,
+                      int64_t layers, int64_t batch, int64_t channels, hipStream_t s);
+void launch_patch(const void* in, void* out, int64_t batch, int64_t channels, int64_t grid,
+                  int64_t patch, bool inverse, bool f32, hipStream_t s);
+// Cos-first sinusoidal timestep embedding, fp64, rounded to bf16, broadcast to `batch` rows
+// (weights.cpp:107-121 and the host broadcast at pixart_dit.cpp:156-160).
+void launch_timestep_embedding(double t, int dim, int64_t batch, bf16_t* out, hipStream_t s);
+
+}  // namespace bh

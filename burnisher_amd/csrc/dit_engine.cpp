@@ -1,0 +1,502 @@
+// The dit-step engine: PixArt-Sigma's denoiser forward (reference: src/models/pixart_dit.cpp:
+// 112-304) on one MI355X.
+//
+// Two plans over the same kernels:
+//
+//   BH_DIT_FUSED   the MI355X plan. Per layer it launches 10 kernels instead of the
+//                  reference's 22: LayerNorm+chunk+modulate as one row kernel; Q,K,V as one
+//                  [M, 3d] GEMM (the attention reads the three column blocks in place through
+//                  row strides); the gated residuals and the cross-attention residual inside the
+//                  out-projection GEMM epilogues; every layer's caption K/V projection -- which
+//                  depends only on the caption -- hoisted into one [Mcap, L*2d] GEMM before the
+//                  block loop; every layer's six adaLN chunks formed by one kernel up front. The
+//                  result equals the reference op sequence with every intermediate rounded where
+//                  the reference stores it (the fused epilogues round the GEMM output first), so
+//                  fusion itself changes no bits; only GEMM/attention summation order does.
+//
+//   BH_DIT_OPWISE  the reference graph op by op through the per-op C entry points, exactly the
+//                  calls a reference `register_impl` adapter would receive: the drop-in path.
+//
+// Everything is allocated at create time (zero-filled, as the reference device allocator hands
+// out memory); forward allocates nothing and never synchronises the host. The timestep
+// embedding is computed on the device from the scalar timestep, so no upload happens per step.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstring>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "../../include/burnisher_hip.h"
+#include "common.h"
+
+namespace bh {
+namespace {
+
+struct DevBuf {
+    void* p = nullptr;
+    size_t bytes = 0;
+    DevBuf() = default;
+    explicit DevBuf(size_t n) : bytes(n) {
+        hip_check(hipMalloc(&p, n ? n : 1), "hipMalloc");
+        hip_check(hipMemset(p, 0, n ? n : 1), "hipMemset");
+    }
+    DevBuf(const DevBuf&) = delete;
+    DevBuf& operator=(const DevBuf&) = delete;
+    DevBuf(DevBuf&& o) noexcept : p(o.p), bytes(o.bytes) { o.p = nullptr; o.bytes = 0; }
+    DevBuf& operator=(DevBuf&& o) noexcept {
+        if (this != &o) {
+            reset();
+            p = o.p;
+            bytes = o.bytes;
+            o.p = nullptr;
+            o.bytes = 0;
+        }
+        return *this;
+    }
+    ~DevBuf() { reset(); }
+    void reset() {
+        if (p) (void)hipFree(p);
+        p = nullptr;
+        bytes = 0;
+    }
+    bf16_t* bf() const { return static_cast<bf16_t*>(p); }
+};
+
+// 2-D sin/cos position table [grid*grid, dim] in fp64 (pixart_dit.cpp:32-77): each 1-D
+// half is SIN first then COS over frequencies 1/10000^(i/half); the first half of the channels
+// is driven by the column (x) coordinate, the second by the row (y); the coordinate along an
+// axis is i / (grid / base) / interpolation_scale.
+std::vector<double> position_table(int dim, int grid, int base, double interp) {
+    std::vector<double> axis(grid);
+    for (int i = 0; i < grid; ++i) {
+        axis[i] = static_cast<double>(i) / (static_cast<double>(grid) / base) / interp;
+    }
+    const int half_dim = dim / 2;       // channels per axis
+    const int quarter = half_dim / 2;   // sin (or cos) channels per axis
+    std::vector<double> omega(quarter);
+    for (int i = 0; i < quarter; ++i) {
+        omega[i] = 1.0 / std::pow(10000.0, static_cast<double>(i) / quarter);
+    }
+    std::vector<double> out(static_cast<size_t>(grid) * grid * dim);
+    for (int r = 0; r < grid; ++r) {
+        for (int c = 0; c < grid; ++c) {
+            double* row = &out[(static_cast<size_t>(r) * grid + c) * dim];
+            for (int i = 0; i < quarter; ++i) {
+                const double ax = axis[c] * omega[i];
+                const double ay = axis[r] * omega[i];
+                row[i] = std::sin(ax);
+                row[quarter + i] = std::cos(ax);
+                row[half_dim + i] = std::sin(ay);
+                row[half_dim + quarter + i] = std::cos(ay);
+            }
+        }
+    }
+    return out;
+}
+
+}  // namespace
+}  // namespace bh
+
+using namespace bh;
+
+struct bh_dit {
+    bh_dit_config cfg{};
+    bh_dit_weights w{};
+    std::vector<bh_dit_block_weights> blocks;
+    int mode = BH_DIT_FUSED;
+    int64_t B = 0, latent = 0, cap_len = 0, grid = 0, N = 0, M = 0, Mcap = 0, d = 0, dff = 0;
+    int64_t patch_in = 0, patch_out = 0;
+
+    DevBuf pos_table, patches, x, normed, modded, q, k, v, qkv, ctx, proj, q2, kc, vc, ff0;
+    DevBuf temb, h_t, emb_t, silu_t, modulation, cap_h, cap, kv_all, chunks, tables_dev;
+    DevBuf shift, scale, gate, zero, tokens;
+    DevBuf w_qkv, b_qkv, w_kv, b_kv;   // repacked weights (fused plan)
+    int64_t workspace = 0;
+
+    DevBuf make(int64_t elems) {
+        workspace += elems * 2;
+        return DevBuf(static_cast<size_t>(elems) * 2);
+    }
+};
+
+namespace {
+
+void check_weights(const bh_dit_config& c, const bh_dit_weights& w) {
+    const void* top[] = {w.pos_embed_w, w.pos_embed_b, w.t_emb1_w, w.t_emb1_b, w.t_emb2_w,
+                         w.t_emb2_b,    w.adaln_w,     w.adaln_b,  w.cap1_w,   w.cap1_b,
+                         w.cap2_w,      w.cap2_b,      w.out_table, w.proj_out_w, w.proj_out_b};
+    for (const void* p : top) {
+        require(p != nullptr, "dit: a model weight pointer is null. A model that ran with a missing "
+                              "weight would produce a plausible image from wrong numbers.");
+    }
+    require(w.blocks != nullptr, "dit: null block weight table");
+    for (int l = 0; l < c.num_layers; ++l) {
+        const bh_dit_block_weights& b = w.blocks[l];
+        const void* ps[] = {b.scale_shift_table, b.attn1_q_w, b.attn1_q_b, b.attn1_k_w, b.attn1_k_b,
+                            b.attn1_v_w, b.attn1_v_b, b.attn1_o_w, b.attn1_o_b, b.attn2_q_w,
+                            b.attn2_q_b, b.attn2_k_w, b.attn2_k_b, b.attn2_v_w, b.attn2_v_b,
+                            b.attn2_o_w, b.attn2_o_b, b.ff0_w, b.ff0_b, b.ff2_w, b.ff2_b};
+        for (const void* p : ps) {
+            require(p != nullptr, "dit: transformer_blocks." + std::to_string(l) +
+                                      " has a null weight pointer");
+        }
+    }
+}
+
+void d2d(void* dst, const void* src, size_t bytes, hipStream_t s) {
+    hip_check(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, s), "hipMemcpyAsync");
+}
+
+void ok(int status) {
+    if (status != 0) throw Error(bh_last_error());
+}
+
+// The reference graph, op by op through the C entry points (pixart_dit.cpp:132-303).
+void forward_opwise(bh_dit& e, const void* latent, double t, const void* caption,
+                    const void* mask, int mask_dtype, void* out, hipStream_t s) {
+    const auto& c = e.cfg;
+    const int64_t B = e.B, N = e.N, M = e.M, d = e.d, P = c.patch_size;
+    const int BF = BH_BF16;
+    void* st = s;
+    ok(bh_patch(latent, e.patches.p, B, c.in_channels, e.grid, P, 0, BF, st));
+    ok(bh_gemm(e.patches.p, e.w.pos_embed_w, e.w.pos_embed_b, e.x.p, M, d, e.patch_in, 1,
+               BH_EPI_NONE, BF, st));
+    ok(bh_add(e.x.p, e.pos_table.p, e.x.p, B, N * d, 1.0f, 1, BF, st));
+
+    {
+        ProfileScope ps(K_ELEMENTWISE, s, 0.0);
+        launch_timestep_embedding(t, 256, B, e.temb.bf(), s);
+    }
+    ok(bh_gemm(e.temb.p, e.w.t_emb1_w, e.w.t_emb1_b, e.h_t.p, B, d, 256, 1, BH_EPI_SILU, BF, st));
+    ok(bh_gemm(e.h_t.p, e.w.t_emb2_w, e.w.t_emb2_b, e.emb_t.p, B, d, d, 1, BH_EPI_NONE, BF, st));
+    ok(bh_activation(e.emb_t.p, e.silu_t.p, B * d, BH_EPI_SILU, nullptr, BF, st));
+    ok(bh_gemm(e.silu_t.p, e.w.adaln_w, e.w.adaln_b, e.modulation.p, B, 6 * d, d, 1, BH_EPI_NONE,
+               BF, st));
+
+    ok(bh_gemm(caption, e.w.cap1_w, e.w.cap1_b, e.cap_h.p, e.Mcap, d, c.caption_channels, 1,
+               BH_EPI_GELU, BF, st));
+    ok(bh_gemm(e.cap_h.p, e.w.cap2_w, e.w.cap2_b, e.cap.p, e.Mcap, d, d, 1, BH_EPI_NONE, BF, st));
+
+    const float eps = static_cast<float>(c.eps);
+    for (int l = 0; l < c.num_layers; ++l) {
+        const bh_dit_block_weights& bw = e.blocks[l];
+        const void* table = bw.scale_shift_table;
+        ok(bh_norm(e.x.p, nullptr, nullptr, e.normed.p, M, d, eps, 0, 0, 0, BF, st));
+        ok(bh_chunk(e.modulation.p, table, e.shift.p, B, d, 6, 0, 0, BF, st));
+        ok(bh_chunk(e.modulation.p, table, e.scale.p, B, d, 6, 1, 1, BF, st));
+        ok(bh_chunk(e.modulation.p, table, e.gate.p, B, d, 6, 2, 2, BF, st));
+        ok(bh_modulate(e.normed.p, e.scale.p, e.shift.p, e.modded.p, B, N, d, nullptr, nullptr, BF,
+                       st));
+        ok(bh_gemm(e.modded.p, bw.attn1_q_w, bw.attn1_q_b, e.q.p, M, d, d, 1, BH_EPI_NONE, BF, st));
+        ok(bh_gemm(e.modded.p, bw.attn1_k_w, bw.attn1_k_b, e.k.p, M, d, d, 1, BH_EPI_NONE, BF, st));
+        ok(bh_gemm(e.modded.p, bw.attn1_v_w, bw.attn1_v_b, e.v.p, M, d, d, 1, BH_EPI_NONE, BF, st));
+        ok(bh_attention(e.q.p, e.k.p, e.v.p, e.ctx.p, B, c.num_heads, N, N, c.head_dim, 0.0f,
+                        nullptr, nullptr, BF, BF, st));
+        ok(bh_gemm(e.ctx.p, bw.attn1_o_w, bw.attn1_o_b, e.proj.p, M, d, d, 1, BH_EPI_NONE, BF, st));
+        ok(bh_modulate(e.proj.p, e.zero.p, e.zero.p, e.x.p, B, N, d, e.x.p, e.gate.p, BF, st));
+
+        ok(bh_gemm(e.x.p, bw.attn2_q_w, bw.attn2_q_b, e.q.p, M, d, d, 1, BH_EPI_NONE, BF, st));
+        ok(bh_gemm(e.cap.p, bw.attn2_k_w, bw.attn2_k_b, e.kc.p, e.Mcap, d, d, 1, BH_EPI_NONE, BF, st));
+        ok(bh_gemm(e.cap.p, bw.attn2_v_w, bw.attn2_v_b, e.vc.p, e.Mcap, d, d, 1, BH_EPI_NONE, BF, st));
+        ok(bh_attention(e.q.p, e.kc.p, e.vc.p, e.ctx.p, B, c.num_heads, N, e.cap_len, c.head_dim,
+                        0.0f, nullptr, mask, mask_dtype, BF, st));
+        ok(bh_gemm(e.ctx.p, bw.attn2_o_w, bw.attn2_o_b, e.proj.p, M, d, d, 1, BH_EPI_NONE, BF, st));
+        ok(bh_add(e.x.p, e.proj.p, e.x.p, M, d, 1.0f, 0, BF, st));
+
+        ok(bh_norm(e.x.p, nullptr, nullptr, e.normed.p, M, d, eps, 0, 0, 0, BF, st));
+        ok(bh_chunk(e.modulation.p, table, e.shift.p, B, d, 6, 3, 3, BF, st));
+        ok(bh_chunk(e.modulation.p, table, e.scale.p, B, d, 6, 4, 4, BF, st));
+        ok(bh_chunk(e.modulation.p, table, e.gate.p, B, d, 6, 5, 5, BF, st));
+        ok(bh_modulate(e.normed.p, e.scale.p, e.shift.p, e.modded.p, B, N, d, nullptr, nullptr, BF,
+                       st));
+        ok(bh_gemm(e.modded.p, bw.ff0_w, bw.ff0_b, e.ff0.p, M, e.dff, d, 1, BH_EPI_GELU, BF, st));
+        ok(bh_gemm(e.ff0.p, bw.ff2_w, bw.ff2_b, e.proj.p, M, d, e.dff, 1, BH_EPI_NONE, BF, st));
+        ok(bh_modulate(e.proj.p, e.zero.p, e.zero.p, e.x.p, B, N, d, e.x.p, e.gate.p, BF, st));
+    }
+
+    ok(bh_chunk(e.emb_t.p, e.w.out_table, e.shift.p, B, d, 1, 0, 0, BF, st));
+    ok(bh_chunk(e.emb_t.p, e.w.out_table, e.scale.p, B, d, 1, 0, 1, BF, st));
+    ok(bh_norm(e.x.p, nullptr, nullptr, e.normed.p, M, d, eps, 0, 0, 0, BF, st));
+    ok(bh_modulate(e.normed.p, e.scale.p, e.shift.p, e.modded.p, B, N, d, nullptr, nullptr, BF, st));
+    ok(bh_gemm(e.modded.p, e.w.proj_out_w, e.w.proj_out_b, e.tokens.p, M, e.patch_out, d, 1,
+               BH_EPI_NONE, BF, st));
+    ok(bh_patch(e.tokens.p, out, B, c.out_channels, e.grid, P, 1, BF, st));
+}
+
+struct SubclassScope {
+    explicit SubclassScope(int cls) { set_gemm_subclass(cls); }
+    ~SubclassScope() { set_gemm_subclass(-1); }
+};
+
+void gemm(const bf16_t* a, const void* w, const void* b, bf16_t* out, int64_t m, int64_t n,
+          int64_t k, const GemmEpilogue& ep, hipStream_t s) {
+    launch_gemm_bf16(a, static_cast<const bf16_t*>(w), static_cast<const bf16_t*>(b), out, m, n, k,
+                     ep, s);
+}
+
+// The MI355X plan.
+void forward_fused(bh_dit& e, const void* latent, double t, const void* caption, const void* mask,
+                   int mask_dtype, void* out, hipStream_t s) {
+    const auto& c = e.cfg;
+    const int64_t B = e.B, N = e.N, M = e.M, d = e.d, P = c.patch_size, L = c.num_layers;
+    const int64_t H = c.num_heads, Dh = c.head_dim;
+    const float eps = static_cast<float>(c.eps);
+    const GemmEpilogue plain;
+
+    {
+        ProfileScope ps(K_ELEMENTWISE, s, 4.0 * e.B * e.N * e.patch_in);
+        launch_patch(latent, e.patches.p, B, c.in_channels, e.grid, P, false, false, s);
+    }
+    {   // patch embedding, then + position table (AddArgs broadcast over the batch)
+        GemmEpilogue ep;
+        ep.round_mid = true;
+        ep.row_add = e.pos_table.bf();
+        ep.row_add_period = N;
+        gemm(e.patches.bf(), e.w.pos_embed_w, e.w.pos_embed_b, e.x.bf(), M, d, e.patch_in, ep, s);
+    }
+    {   // adaLN-single: one modulation vector per step
+        {
+            ProfileScope ps(K_ELEMENTWISE, s, 2.0 * B * 256);
+            launch_timestep_embedding(t, 256, B, e.temb.bf(), s);
+        }
+        GemmEpilogue silu;
+        silu.act = 2;
+        gemm(e.temb.bf(), e.w.t_emb1_w, e.w.t_emb1_b, e.h_t.bf(), B, d, 256, silu, s);
+        gemm(e.h_t.bf(), e.w.t_emb2_w, e.w.t_emb2_b, e.emb_t.bf(), B, d, d, plain, s);
+        {
+            ProfileScope ps(K_ELEMENTWISE, s, 4.0 * B * d);
+            launch_activation(e.emb_t.p, e.silu_t.p, B * d, 2, nullptr, false, s);
+        }
+        gemm(e.silu_t.bf(), e.w.adaln_w, e.w.adaln_b, e.modulation.bf(), B, 6 * d, d, plain, s);
+    }
+    {   // caption projection, then every layer's cross-attention K and V in one GEMM
+        GemmEpilogue gelu;
+        gelu.act = 1;
+        gemm(static_cast<const bf16_t*>(caption), e.w.cap1_w, e.w.cap1_b, e.cap_h.bf(), e.Mcap, d,
+             c.caption_channels, gelu, s);
+        gemm(e.cap_h.bf(), e.w.cap2_w, e.w.cap2_b, e.cap.bf(), e.Mcap, d, d, plain, s);
+        gemm(e.cap.bf(), e.w_kv.p, e.b_kv.p, e.kv_all.bf(), e.Mcap, L * 2 * d, d, plain, s);
+    }
+    {
+        ProfileScope ps(K_ELEMENTWISE, s, 2.0 * (B * 6 * d + L * 6 * d + L * 6 * B * d));
+        launch_chunk_all(e.modulation.bf(), static_cast<const bf16_t* const*>(e.tables_dev.p),
+                         e.chunks.bf(), L, B, d, s);
+    }
+    const float scale = 1.0f / std::sqrt(static_cast<float>(Dh));
+    const bool mask_f32 = mask_dtype == BH_F32;
+    for (int64_t l = 0; l < L; ++l) {
+        const bh_dit_block_weights& bw = e.blocks[l];
+        const bf16_t* ch = e.chunks.bf() + l * 6 * B * d;   // [6][B][d]
+        const bf16_t* shift_msa = ch, *scale_msa = ch + B * d, *gate_msa = ch + 2 * B * d;
+        const bf16_t* shift_mlp = ch + 3 * B * d, *scale_mlp = ch + 4 * B * d;
+        const bf16_t* gate_mlp = ch + 5 * B * d;
+        const bf16_t* wqkv = e.w_qkv.bf() + l * 3 * d * d;
+        const bf16_t* bqkv = e.b_qkv.bf() + l * 3 * d;
+
+        // 1. self-attention
+        {
+            ProfileScope ps(K_NORM, s, 4.0 * M * d);
+            launch_norm_modulate_pre(e.x.bf(), shift_msa, scale_msa, e.modded.bf(), B, N, d, eps, s);
+        }
+        {
+            SubclassScope sc(K_GEMM_QKV);
+            gemm(e.modded.bf(), wqkv, bqkv, e.qkv.bf(), M, 3 * d, d, plain, s);
+        }
+        launch_attention_bf16(e.qkv.bf(), e.qkv.bf() + d, e.qkv.bf() + 2 * d, e.ctx.bf(),
+                              AttnShape{B, H, N, N, Dh, 3 * d, 3 * d, d, scale}, nullptr, false, s);
+        {
+            GemmEpilogue ep;
+            ep.round_mid = true;
+            ep.residual = e.x.bf();
+            ep.gate = gate_msa;
+            ep.gate_rows = N;
+            gemm(e.ctx.bf(), bw.attn1_o_w, bw.attn1_o_b, e.x.bf(), M, d, d, ep, s);
+        }
+        // 2. cross-attention (no norm before it: pixart_dit.cpp:251-253)
+        gemm(e.x.bf(), bw.attn2_q_w, bw.attn2_q_b, e.q2.bf(), M, d, d, plain, s);
+        launch_attention_bf16(e.q2.bf(), e.kv_all.bf() + l * 2 * d, e.kv_all.bf() + l * 2 * d + d,
+                              e.ctx.bf(), AttnShape{B, H, N, e.cap_len, Dh, d, L * 2 * d, d, scale},
+                              mask, mask_f32, s);
+        {
+            GemmEpilogue ep;
+            ep.round_mid = true;
+            ep.residual = e.x.bf();
+            gemm(e.ctx.bf(), bw.attn2_o_w, bw.attn2_o_b, e.x.bf(), M, d, d, ep, s);
+        }
+        // 3. feed-forward
+        {
+            ProfileScope ps(K_NORM, s, 4.0 * M * d);
+            launch_norm_modulate_pre(e.x.bf(), shift_mlp, scale_mlp, e.modded.bf(), B, N, d, eps, s);
+        }
+        {
+            SubclassScope sc(K_GEMM_FF0);
+            GemmEpilogue gelu;
+            gelu.act = 1;
+            gemm(e.modded.bf(), bw.ff0_w, bw.ff0_b, e.ff0.bf(), M, e.dff, d, gelu, s);
+        }
+        {
+            SubclassScope sc(K_GEMM_FF2);
+            GemmEpilogue ep;
+            ep.round_mid = true;
+            ep.residual = e.x.bf();
+            ep.gate = gate_mlp;
+            ep.gate_rows = N;
+            gemm(e.ff0.bf(), bw.ff2_w, bw.ff2_b, e.x.bf(), M, d, e.dff, ep, s);
+        }
+    }
+
+    // output head: shift = emb_t + table[0], scale = emb_t + table[1] (pixart_dit.cpp:287-294)
+    {
+        ProfileScope ps(K_ELEMENTWISE, s, 6.0 * B * d);
+        launch_chunk(e.emb_t.p, e.w.out_table, e.shift.p, B, d, 1, 0, 0, false, s);
+        launch_chunk(e.emb_t.p, e.w.out_table, e.scale.p, B, d, 1, 0, 1, false, s);
+    }
+    {
+        ProfileScope ps(K_NORM, s, 4.0 * M * d);
+        launch_norm_modulate_pre(e.x.bf(), e.shift.bf(), e.scale.bf(), e.modded.bf(), B, N, d, eps, s);
+    }
+    gemm(e.modded.bf(), e.w.proj_out_w, e.w.proj_out_b, e.tokens.bf(), M, e.patch_out, d, plain, s);
+    {
+        ProfileScope ps(K_ELEMENTWISE, s, 4.0 * M * e.patch_out);
+        launch_patch(e.tokens.p, out, B, c.out_channels, e.grid, P, true, false, s);
+    }
+}
+
+}  // namespace
+
+extern "C" {
+
+int bh_dit_create(const bh_dit_config* cfg, const bh_dit_weights* w, int64_t batch,
+                  int64_t latent_hw, int64_t caption_len, int mode, bh_dit** out) {
+    return guarded([&] {
+        require(cfg && w && out, "dit_create: null argument");
+        *out = nullptr;
+        const bh_dit_config& c = *cfg;
+        require(c.num_layers > 0 && c.num_heads > 0 && c.head_dim > 0 && c.patch_size > 0 &&
+                    c.in_channels > 0 && c.out_channels > 0 && c.caption_channels > 0 &&
+                    c.sample_size > 0,
+                "dit_create: every config field must be positive");
+        require(batch > 0 && caption_len > 0, "dit_create: batch and caption_len must be positive");
+        require(latent_hw > 0 && latent_hw % c.patch_size == 0,
+                "dit_create: latent size " + std::to_string(latent_hw) +
+                    " is not divisible by the patch size");
+        require(mode == BH_DIT_FUSED || mode == BH_DIT_OPWISE, "dit_create: unknown mode");
+        check_weights(c, *w);
+
+        auto e = std::make_unique<bh_dit>();
+        e->cfg = c;
+        e->w = *w;
+        e->blocks.assign(w->blocks, w->blocks + c.num_layers);
+        e->w.blocks = nullptr;
+        e->mode = mode;
+        e->B = batch;
+        e->latent = latent_hw;
+        e->cap_len = caption_len;
+        e->grid = latent_hw / c.patch_size;
+        e->N = e->grid * e->grid;
+        e->M = batch * e->N;
+        e->Mcap = batch * caption_len;
+        e->d = static_cast<int64_t>(c.num_heads) * c.head_dim;
+        e->dff = static_cast<int64_t>(static_cast<double>(e->d) * c.mlp_ratio);
+        e->patch_in = static_cast<int64_t>(c.in_channels) * c.patch_size * c.patch_size;
+        e->patch_out = static_cast<int64_t>(c.out_channels) * c.patch_size * c.patch_size;
+        const int64_t M = e->M, d = e->d, L = c.num_layers, B = batch;
+
+        // position table: fp64 on the host, stored as bf16 once (pixart_dit.cpp:88-105)
+        {
+            const int base = c.sample_size / c.patch_size;
+            const std::vector<double> pe =
+                position_table(static_cast<int>(d), static_cast<int>(e->grid), base, 2.0);
+            std::vector<bf16_t> host(pe.size());
+            for (size_t i = 0; i < pe.size(); ++i) host[i] = f2bf(static_cast<float>(pe[i]));
+            e->pos_table = e->make(static_cast<int64_t>(host.size()));
+            hip_check(hipMemcpy(e->pos_table.p, host.data(), host.size() * 2, hipMemcpyHostToDevice),
+                      "hipMemcpy");
+        }
+        e->patches = e->make(M * e->patch_in);
+        e->x = e->make(M * d);
+        e->modded = e->make(M * d);
+        e->ctx = e->make(M * d);
+        e->ff0 = e->make(M * e->dff);
+        e->temb = e->make(B * 256);
+        e->h_t = e->make(B * d);
+        e->emb_t = e->make(B * d);
+        e->silu_t = e->make(B * d);
+        e->modulation = e->make(B * 6 * d);
+        e->cap_h = e->make(e->Mcap * d);
+        e->cap = e->make(e->Mcap * d);
+        e->shift = e->make(B * d);
+        e->scale = e->make(B * d);
+        e->tokens = e->make(M * e->patch_out);
+        if (mode == BH_DIT_OPWISE) {
+            e->normed = e->make(M * d);
+            e->q = e->make(M * d);
+            e->k = e->make(M * d);
+            e->v = e->make(M * d);
+            e->proj = e->make(M * d);
+            e->kc = e->make(e->Mcap * d);
+            e->vc = e->make(e->Mcap * d);
+            e->gate = e->make(B * d);
+            e->zero = e->make(B * d);
+        } else {
+            e->qkv = e->make(M * 3 * d);
+            e->q2 = e->make(M * d);
+            e->kv_all = e->make(e->Mcap * L * 2 * d);
+            e->chunks = e->make(L * 6 * B * d);
+            e->w_qkv = e->make(L * 3 * d * d);
+            e->b_qkv = e->make(L * 3 * d);
+            e->w_kv = e->make(L * 2 * d * d);
+            e->b_kv = e->make(L * 2 * d);
+            const size_t wb = static_cast<size_t>(d * d) * 2, bb = static_cast<size_t>(d) * 2;
+            std::vector<const bf16_t*> tables(L);
+            for (int64_t l = 0; l < L; ++l) {
+                const bh_dit_block_weights& bw = e->blocks[l];
+                char* wq = static_cast<char*>(e->w_qkv.p) + l * 3 * wb;
+                char* bq = static_cast<char*>(e->b_qkv.p) + l * 3 * bb;
+                d2d(wq, bw.attn1_q_w, wb, nullptr);
+                d2d(wq + wb, bw.attn1_k_w, wb, nullptr);
+                d2d(wq + 2 * wb, bw.attn1_v_w, wb, nullptr);
+                d2d(bq, bw.attn1_q_b, bb, nullptr);
+                d2d(bq + bb, bw.attn1_k_b, bb, nullptr);
+                d2d(bq + 2 * bb, bw.attn1_v_b, bb, nullptr);
+                char* wk = static_cast<char*>(e->w_kv.p) + l * 2 * wb;
+                char* bk = static_cast<char*>(e->b_kv.p) + l * 2 * bb;
+                d2d(wk, bw.attn2_k_w, wb, nullptr);
+                d2d(wk + wb, bw.attn2_v_w, wb, nullptr);
+                d2d(bk, bw.attn2_k_b, bb, nullptr);
+                d2d(bk + bb, bw.attn2_v_b, bb, nullptr);
+                tables[l] = static_cast<const bf16_t*>(bw.scale_shift_table);
+            }
+            e->tables_dev = DevBuf(sizeof(void*) * L);
+            e->workspace += static_cast<int64_t>(sizeof(void*) * L);
+            hip_check(hipMemcpy(e->tables_dev.p, tables.data(), sizeof(void*) * L,
+                                hipMemcpyHostToDevice),
+                      "hipMemcpy");
+        }
+        hip_check(hipDeviceSynchronize(), "hipDeviceSynchronize");
+        *out = e.release();
+    });
+}
+
+int bh_dit_forward(bh_dit* e, const void* latent, double timestep, const void* caption,
+                   const void* caption_mask, int mask_dtype, void* out, void* stream) {
+    return guarded([&] {
+        require(e != nullptr, "dit_forward: null engine");
+        require(latent && caption && caption_mask && out, "dit_forward: null tensor pointer");
+        require(mask_dtype == BH_F32 || mask_dtype == BH_BF16, "dit_forward: mask dtype");
+        hipStream_t s = static_cast<hipStream_t>(stream);
+        if (e->mode == BH_DIT_OPWISE) {
+            forward_opwise(*e, latent, timestep, caption, caption_mask, mask_dtype, out, s);
+        } else {
+            forward_fused(*e, latent, timestep, caption, caption_mask, mask_dtype, out, s);
+        }
+    });
+}
+
+int64_t bh_dit_workspace_bytes(const bh_dit* e) { return e ? e->workspace : 0; }
+
+void bh_dit_destroy(bh_dit* e) { delete e; }
+
+}  // extern "C"

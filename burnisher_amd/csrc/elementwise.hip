@@ -1,0 +1,522 @@
+// Bandwidth-bound kernels of the dit-step: LayerNorm (and LayerNorm fused with the adaLN
+// chunk + modulation), modulate with gated residual, add, chunk, activation, patchify and the
+// timestep embedding.
+//
+// Each one reproduces the reference oracle's arithmetic exactly (src/cpu/ops_cpu.cpp:186-349):
+// the same fp64 LayerNorm statistics, the same separate fp32 multiplies and adds (written with
+// __fmul_rn/__fadd_rn so the compiler cannot contract them into FMAs, which the host oracle
+// never forms), one bf16 rounding per stored element. Only the order of the fp64 row sums
+// differs, which in fp64 changes the float statistics essentially never.
+//
+// Layout: one 64-lane wave per row for the row kernels (a DiT row is 1152 bf16 = 2304 B, read
+// with 16-byte loads); grid-stride 8-element vectors for the elementwise kernels.
+#include "common.h"
+
+#include <cmath>
+
+namespace bh {
+namespace {
+
+constexpr int kWave = 64;
+
+template <typename T> struct Io;
+template <> struct Io<float> {
+    static __device__ __forceinline__ float ld(const float* p, int64_t i) { return p[i]; }
+    static __device__ __forceinline__ void st(float* p, int64_t i, float v) { p[i] = v; }
+};
+template <> struct Io<bf16_t> {
+    static __device__ __forceinline__ float ld(const bf16_t* p, int64_t i) { return bf2f(p[i]); }
+    static __device__ __forceinline__ void st(bf16_t* p, int64_t i, float v) { p[i] = f2bf(v); }
+};
+
+__device__ __forceinline__ double wave_sum(double v) {
+#pragma unroll
+    for (int o = kWave / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+    return v;
+}
+
+// 8 bf16 <-> 8 floats through one 16-byte access.
+struct V8 {
+    float f[8];
+};
+__device__ __forceinline__ V8 load8(const bf16_t* p) {
+    const uint4 raw = *reinterpret_cast<const uint4*>(p);
+    V8 r;
+    const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        r.f[2 * i] = __uint_as_float(w[i] << 16);
+        r.f[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+    }
+    return r;
+}
+__device__ __forceinline__ void store8(bf16_t* p, const V8& v) {
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        w[i] = static_cast<uint32_t>(f2bf(v.f[2 * i])) |
+               (static_cast<uint32_t>(f2bf(v.f[2 * i + 1])) << 16);
+    }
+    *reinterpret_cast<uint4*>(p) = make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+// ---- LayerNorm / RMSNorm, generic (the NormArgs op) -----------------------------------------
+
+// One wave per row. Values are re-read from global memory for each pass (the row is L1/L2
+// resident), which keeps the kernel valid for any `cols`.
+template <typename T>
+__global__ void __launch_bounds__(256) k_norm(const T* __restrict__ x, const T* __restrict__ w,
+                                              const T* __restrict__ b, T* __restrict__ out,
+                                              int64_t rows, int64_t cols, float eps, bool rms) {
+    const int lane = threadIdx.x % kWave;
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * (blockDim.x / kWave) + threadIdx.x / kWave;
+    if (row >= rows) return;
+    const T* xr = x + row * cols;
+    double mean = 0.0;
+    if (!rms) {
+        double s = 0.0;
+        for (int64_t i = lane; i < cols; i += kWave) s += static_cast<double>(Io<T>::ld(xr, i));
+        mean = wave_sum(s) / static_cast<double>(cols);
+    }
+    double var = 0.0;
+    for (int64_t i = lane; i < cols; i += kWave) {
+        const double d = static_cast<double>(Io<T>::ld(xr, i)) - mean;
+        var += d * d;
+    }
+    var = wave_sum(var) / static_cast<double>(cols);
+    const float inv = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(static_cast<float>(var), eps)));
+    const float fmean = static_cast<float>(mean);
+    for (int64_t i = lane; i < cols; i += kWave) {
+        float v = __fmul_rn(__fsub_rn(Io<T>::ld(xr, i), fmean), inv);
+        if (w) v = __fmul_rn(v, Io<T>::ld(w, i));
+        if (b) v = __fadd_rn(v, Io<T>::ld(b, i));
+        Io<T>::st(out + row * cols, i, v);
+    }
+}
+
+// ---- LayerNorm fused with the adaLN chunk and modulation (the hot row kernel) ---------------
+
+// Row statistics exactly as the oracle forms them: fp64 mean, fp64 sum of squared deviations,
+// then float inverse standard deviation.
+template <int NV>
+__device__ __forceinline__ void row_stats(const V8 (&v)[NV], int nvec, int lane, int64_t cols,
+                                          float eps, float* fmean, float* inv) {
+    double s = 0.0;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        if (lane + j * kWave < nvec) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) s += static_cast<double>(v[j].f[e]);
+        }
+    }
+    const double mean = wave_sum(s) / static_cast<double>(cols);
+    double q = 0.0;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        if (lane + j * kWave < nvec) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const double d = static_cast<double>(v[j].f[e]) - mean;
+                q += d * d;
+            }
+        }
+    }
+    const double var = wave_sum(q) / static_cast<double>(cols);
+    *inv = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(static_cast<float>(var), eps)));
+    *fmean = static_cast<float>(mean);
+}
+
+// shift/scale either precomputed ([batch, C] rows, already rounded) or formed here from the
+// modulation vector and the table, rounded as the chunk op stores them.
+template <int NV, bool PRE>
+__global__ void __launch_bounds__(256) k_norm_modulate(
+    const bf16_t* __restrict__ x, const bf16_t* __restrict__ mod, int64_t mod_stride,
+    const bf16_t* __restrict__ shift_src, const bf16_t* __restrict__ scale_src,
+    const bf16_t* __restrict__ shift_tab, const bf16_t* __restrict__ scale_tab,
+    bf16_t* __restrict__ out, int64_t rows, int64_t tokens, int64_t cols, float eps) {
+    const int lane = threadIdx.x % kWave;
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * (blockDim.x / kWave) + threadIdx.x / kWave;
+    if (row >= rows) return;
+    const int nvec = static_cast<int>(cols / 8);
+    const bf16_t* xr = x + row * cols;
+    V8 v[NV];
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const int vi = lane + j * kWave;
+        if (vi < nvec) v[j] = load8(xr + vi * 8);
+    }
+    float fmean, inv;
+    row_stats<NV>(v, nvec, lane, cols, eps, &fmean, &inv);
+    const int64_t b = row / tokens;
+    bf16_t* orow = out + row * cols;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const int vi = lane + j * kWave;
+        if (vi >= nvec) continue;
+        V8 sh, sc;
+        if (PRE) {
+            sh = load8(shift_src + b * cols + vi * 8);
+            sc = load8(scale_src + b * cols + vi * 8);
+        } else {
+            const V8 ms = load8(mod + b * mod_stride + (shift_src - mod) + vi * 8);
+            const V8 mc = load8(mod + b * mod_stride + (scale_src - mod) + vi * 8);
+            const V8 ts = load8(shift_tab + vi * 8);
+            const V8 tc = load8(scale_tab + vi * 8);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                sh.f[e] = round_bf16(__fadd_rn(ms.f[e], ts.f[e]));
+                sc.f[e] = round_bf16(__fadd_rn(mc.f[e], tc.f[e]));
+            }
+        }
+        V8 o;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            // normed is stored (rounded) by the norm op before modulate reads it.
+            const float nrm = round_bf16(__fmul_rn(__fsub_rn(v[j].f[e], fmean), inv));
+            o.f[e] = __fadd_rn(__fmul_rn(nrm, __fadd_rn(1.0f, sc.f[e])), sh.f[e]);
+        }
+        store8(orow + vi * 8, o);
+    }
+}
+
+// ---- modulate (ModulateArgs) ----------------------------------------------------------------
+
+template <typename T>
+__global__ void __launch_bounds__(256) k_modulate(const T* __restrict__ x, const T* __restrict__ scale,
+                                                  const T* __restrict__ shift, T* out, int64_t n,
+                                                  int64_t tokens, int64_t channels,
+                                                  const T* residual, const T* __restrict__ gate) {
+    for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < n;
+         i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+        const int64_t c = i % channels;
+        const int64_t bc = (i / (tokens * channels)) * channels + c;
+        float v = Io<T>::ld(x, i);
+        v = __fadd_rn(__fmul_rn(v, __fadd_rn(1.0f, Io<T>::ld(scale, bc))), Io<T>::ld(shift, bc));
+        if (gate) v = __fmul_rn(v, Io<T>::ld(gate, bc));
+        if (residual) v = __fadd_rn(v, Io<T>::ld(residual, i));
+        Io<T>::st(out, i, v);
+    }
+}
+
+// bf16, channels % 8 == 0: 8 elements of one (b, token) row per thread.
+__global__ void __launch_bounds__(256) k_modulate_v8(const bf16_t* __restrict__ x,
+                                                     const bf16_t* __restrict__ scale,
+                                                     const bf16_t* __restrict__ shift, bf16_t* out,
+                                                     int64_t nvec, int64_t tokens, int64_t channels,
+                                                     const bf16_t* residual,
+                                                     const bf16_t* __restrict__ gate) {
+    const int64_t cv = channels / 8;
+    for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < nvec;
+         i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+        const int64_t c = (i % cv) * 8;
+        const int64_t bc = (i / (tokens * cv)) * channels + c;
+        const V8 xv = load8(x + i * 8), sc = load8(scale + bc), sh = load8(shift + bc);
+        V8 g, r, o;
+        if (gate) g = load8(gate + bc);
+        if (residual) r = load8(residual + i * 8);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            float v = __fadd_rn(__fmul_rn(xv.f[e], __fadd_rn(1.0f, sc.f[e])), sh.f[e]);
+            if (gate) v = __fmul_rn(v, g.f[e]);
+            if (residual) v = __fadd_rn(v, r.f[e]);
+            o.f[e] = v;
+        }
+        store8(out + i * 8, o);
+    }
+}
+
+// ---- add, chunk, activation -----------------------------------------------------------------
+
+template <typename T>
+__global__ void __launch_bounds__(256) k_add(const T* a, const T* __restrict__ b, T* out,
+                                             int64_t n, int64_t inner, float scale,
+                                             bool broadcast) {
+    for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < n;
+         i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+        const int64_t bi = broadcast ? (i % inner) : i;
+        Io<T>::st(out, i, __fadd_rn(Io<T>::ld(a, i), __fmul_rn(scale, Io<T>::ld(b, bi))));
+    }
+}
+
+template <typename T>
+__global__ void k_chunk(const T* __restrict__ mod, const T* __restrict__ table, T* __restrict__ out,
+                        int64_t batch, int64_t channels, int64_t chunks, int64_t chunk,
+                        int64_t trow) {
+    const int64_t n = batch * channels;
+    for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < n;
+         i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+        const int64_t b = i / channels, c = i % channels;
+        Io<T>::st(out, i, __fadd_rn(Io<T>::ld(mod, b * chunks * channels + chunk * channels + c),
+                                    Io<T>::ld(table, trow * channels + c)));
+    }
+}
+
+__global__ void k_chunk_all(const bf16_t* __restrict__ mod, const bf16_t* const* __restrict__ tables,
+                            bf16_t* __restrict__ out, int64_t layers, int64_t batch,
+                            int64_t channels) {
+    const int64_t per_layer = 6 * batch * channels;
+    const int64_t n = layers * per_layer;
+    for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < n;
+         i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+        const int64_t l = i / per_layer, r = i % per_layer;
+        const int64_t k = r / (batch * channels), b = (r / channels) % batch, c = r % channels;
+        const float v = __fadd_rn(bf2f(mod[b * 6 * channels + k * channels + c]),
+                                  bf2f(tables[l][k * channels + c]));
+        out[i] = f2bf(v);
+    }
+}
+
+__device__ __forceinline__ float gelu_tanh(float x) {
+    const float c = 0.7978845608028654f;
+    const float x3 = __fmul_rn(__fmul_rn(x, x), x);
+    const float inner = __fmul_rn(c, __fadd_rn(x, __fmul_rn(0.044715f, x3)));
+    return __fmul_rn(__fmul_rn(0.5f, x), __fadd_rn(1.0f, tanhf(inner)));
+}
+__device__ __forceinline__ float silu(float x) { return __fdiv_rn(x, __fadd_rn(1.0f, expf(-x))); }
+
+template <typename T>
+__global__ void __launch_bounds__(256) k_activation(const T* __restrict__ x, T* __restrict__ out,
+                                                    int64_t n, int kind,
+                                                    const T* __restrict__ gate) {
+    for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < n;
+         i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+        const float v = Io<T>::ld(x, i);
+        float r = (kind == 2) ? silu(v) : (kind == 0 ? v : gelu_tanh(v));
+        if (kind == 3) r = __fmul_rn(r, Io<T>::ld(gate, i));
+        Io<T>::st(out, i, r);
+    }
+}
+
+// ---- patchify / unpatchify ------------------------------------------------------------------
+
+// One thread per token element. Forward: token layout (c, ky, kx); inverse: (ky, kx, c).
+template <typename T>
+__global__ void __launch_bounds__(256) k_patch(const T* __restrict__ in, T* __restrict__ out,
+                                               int64_t batch, int64_t C, int64_t G, int64_t P,
+                                               bool inverse) {
+    const int64_t per_token = C * P * P;
+    const int64_t n = batch * G * G * per_token;
+    const int64_t H = G * P;
+    for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < n;
+         i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+        const int64_t e = i % per_token;
+        const int64_t tok = (i / per_token) % (G * G);
+        const int64_t b = i / (per_token * G * G);
+        int64_t c, ky, kx;
+        if (inverse) {
+            c = e % C;
+            kx = (e / C) % P;
+            ky = e / (C * P);
+        } else {
+            kx = e % P;
+            ky = (e / P) % P;
+            c = e / (P * P);
+        }
+        const int64_t ty = tok / G, tx = tok % G;
+        const int64_t img = ((b * C + c) * H + ty * P + ky) * H + tx * P + kx;
+        if (inverse) out[img] = in[i];
+        else out[i] = in[img];
+    }
+}
+
+// ---- timestep embedding ---------------------------------------------------------------------
+
+__global__ void k_timestep_embedding(double t, int dim, int64_t batch, bf16_t* out) {
+    const int half = dim / 2;
+    for (int i = threadIdx.x; i < half; i += blockDim.x) {
+        const double freq = exp(-log(10000.0) * static_cast<double>(i) / half);
+        const double a = t * freq;
+        const bf16_t c = f2bf(static_cast<float>(cos(a)));
+        const bf16_t s = f2bf(static_cast<float>(sin(a)));
+        for (int64_t b = 0; b < batch; ++b) {
+            out[b * dim + i] = c;
+            out[b * dim + half + i] = s;
+        }
+    }
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+int grid_for(int64_t n, int block = 256) {
+    const int64_t g = (n + block - 1) / block;
+    return static_cast<int>(g < 1 ? 1 : (g > 65535 * 8 ? 65535 * 8 : g));
+}
+
+}  // namespace
+
+void launch_norm(const void* x, const void* weight, const void* bias, void* out, int64_t rows,
+                 int64_t cols, float eps, bool rms, bool f32, hipStream_t s) {
+    if (rows == 0) return;
+    const int grid = static_cast<int>((rows + 3) / 4);
+    if (f32) {
+        k_norm<float><<<grid, 256, 0, s>>>(static_cast<const float*>(x),
+                                           static_cast<const float*>(weight),
+                                           static_cast<const float*>(bias),
+                                           static_cast<float*>(out), rows, cols, eps, rms);
+    } else {
+        k_norm<bf16_t><<<grid, 256, 0, s>>>(static_cast<const bf16_t*>(x),
+                                            static_cast<const bf16_t*>(weight),
+                                            static_cast<const bf16_t*>(bias),
+                                            static_cast<bf16_t*>(out), rows, cols, eps, rms);
+    }
+    launch_check("norm");
+}
+
+namespace {
+template <bool PRE>
+void dispatch_norm_modulate(const bf16_t* x, const bf16_t* mod, int64_t mod_stride,
+                            const bf16_t* shift_src, const bf16_t* scale_src,
+                            const bf16_t* shift_tab, const bf16_t* scale_tab, bf16_t* out,
+                            int64_t rows, int64_t tokens, int64_t cols, float eps, hipStream_t s) {
+    require(cols % 8 == 0 && cols <= 8 * kWave * 8,
+            "norm_modulate: channels must be a multiple of 8 and at most 4096");
+    require(aligned16(x) && aligned16(out) && aligned16(mod) && aligned16(shift_src) &&
+                aligned16(scale_src) && aligned16(shift_tab) && aligned16(scale_tab),
+            "norm_modulate: every operand must be 16-byte aligned");
+    const int nv = static_cast<int>((cols / 8 + kWave - 1) / kWave);
+    const int grid = static_cast<int>((rows + 3) / 4);
+#define BH_NM(NV)                                                                             \
+    k_norm_modulate<NV, PRE><<<grid, 256, 0, s>>>(x, mod, mod_stride, shift_src, scale_src,   \
+                                                  shift_tab, scale_tab, out, rows, tokens,    \
+                                                  cols, eps)
+    switch (nv) {
+        case 1: BH_NM(1); break;
+        case 2: BH_NM(2); break;
+        case 3: BH_NM(3); break;
+        case 4: BH_NM(4); break;
+        case 5: BH_NM(5); break;
+        case 6: BH_NM(6); break;
+        case 7: BH_NM(7); break;
+        default: BH_NM(8); break;
+    }
+#undef BH_NM
+    launch_check("norm_modulate");
+}
+}  // namespace
+
+void launch_norm_modulate(const bf16_t* x, const bf16_t* mod, int64_t mod_chunks,
+                          int64_t shift_chunk, int64_t scale_chunk, const bf16_t* table,
+                          int64_t shift_row, int64_t scale_row, bf16_t* out, int64_t batch,
+                          int64_t tokens, int64_t channels, float eps, hipStream_t s) {
+    if (batch * tokens == 0) return;
+    dispatch_norm_modulate<false>(x, mod, mod_chunks * channels, mod + shift_chunk * channels,
+                                  mod + scale_chunk * channels, table + shift_row * channels,
+                                  table + scale_row * channels, out, batch * tokens, tokens,
+                                  channels, eps, s);
+}
+
+void launch_norm_modulate_pre(const bf16_t* x, const bf16_t* shift, const bf16_t* scale,
+                              bf16_t* out, int64_t batch, int64_t tokens, int64_t channels,
+                              float eps, hipStream_t s) {
+    if (batch * tokens == 0) return;
+    dispatch_norm_modulate<true>(x, nullptr, 0, shift, scale, nullptr, nullptr, out,
+                                 batch * tokens, tokens, channels, eps, s);
+}
+
+void launch_modulate(const void* x, const void* scale, const void* shift, void* out,
+                     int64_t batch, int64_t tokens, int64_t channels, const void* residual,
+                     const void* gate, bool f32, hipStream_t s) {
+    const int64_t n = batch * tokens * channels;
+    if (n == 0) return;
+    if (f32) {
+        k_modulate<float><<<grid_for(n), 256, 0, s>>>(
+            static_cast<const float*>(x), static_cast<const float*>(scale),
+            static_cast<const float*>(shift), static_cast<float*>(out), n, tokens, channels,
+            static_cast<const float*>(residual), static_cast<const float*>(gate));
+    } else if (channels % 8 == 0 && aligned16(x) && aligned16(scale) && aligned16(shift) &&
+               aligned16(out) && aligned16(residual) && aligned16(gate)) {
+        k_modulate_v8<<<grid_for(n / 8), 256, 0, s>>>(
+            static_cast<const bf16_t*>(x), static_cast<const bf16_t*>(scale),
+            static_cast<const bf16_t*>(shift), static_cast<bf16_t*>(out), n / 8, tokens, channels,
+            static_cast<const bf16_t*>(residual), static_cast<const bf16_t*>(gate));
+    } else {
+        k_modulate<bf16_t><<<grid_for(n), 256, 0, s>>>(
+            static_cast<const bf16_t*>(x), static_cast<const bf16_t*>(scale),
+            static_cast<const bf16_t*>(shift), static_cast<bf16_t*>(out), n, tokens, channels,
+            static_cast<const bf16_t*>(residual), static_cast<const bf16_t*>(gate));
+    }
+    launch_check("modulate");
+}
+
+void launch_activation(const void* x, void* out, int64_t numel, int kind, const void* gate,
+                       bool f32, hipStream_t s) {
+    if (numel == 0) return;
+    if (f32) {
+        k_activation<float><<<grid_for(numel), 256, 0, s>>>(
+            static_cast<const float*>(x), static_cast<float*>(out), numel, kind,
+            static_cast<const float*>(gate));
+    } else {
+        k_activation<bf16_t><<<grid_for(numel), 256, 0, s>>>(
+            static_cast<const bf16_t*>(x), static_cast<bf16_t*>(out), numel, kind,
+            static_cast<const bf16_t*>(gate));
+    }
+    launch_check("activation");
+}
+
+void launch_add(const void* a, const void* b, void* out, int64_t outer, int64_t inner,
+                float scale, bool broadcast_b, bool f32, hipStream_t s) {
+    const int64_t n = outer * inner;
+    if (n == 0) return;
+    if (f32) {
+        k_add<float><<<grid_for(n), 256, 0, s>>>(static_cast<const float*>(a),
+                                                 static_cast<const float*>(b),
+                                                 static_cast<float*>(out), n, inner, scale,
+                                                 broadcast_b);
+    } else {
+        k_add<bf16_t><<<grid_for(n), 256, 0, s>>>(static_cast<const bf16_t*>(a),
+                                                  static_cast<const bf16_t*>(b),
+                                                  static_cast<bf16_t*>(out), n, inner, scale,
+                                                  broadcast_b);
+    }
+    launch_check("add");
+}
+
+void launch_chunk(const void* mod, const void* table, void* out, int64_t batch, int64_t channels,
+                  int64_t chunks, int64_t chunk, int64_t table_chunk, bool f32, hipStream_t s) {
+    const int64_t n = batch * channels;
+    if (n == 0) return;
+    const int64_t trow = table_chunk >= 0 ? table_chunk : chunk;
+    if (f32) {
+        k_chunk<float><<<grid_for(n), 256, 0, s>>>(static_cast<const float*>(mod),
+                                                   static_cast<const float*>(table),
+                                                   static_cast<float*>(out), batch, channels,
+                                                   chunks, chunk, trow);
+    } else {
+        k_chunk<bf16_t><<<grid_for(n), 256, 0, s>>>(static_cast<const bf16_t*>(mod),
+                                                    static_cast<const bf16_t*>(table),
+                                                    static_cast<bf16_t*>(out), batch, channels,
+                                                    chunks, chunk, trow);
+    }
+    launch_check("chunk");
+}
+
+void launch_chunk_all(const bf16_t* mod, const bf16_t* const* tables_dev, bf16_t* out,
+                      int64_t layers, int64_t batch, int64_t channels, hipStream_t s) {
+    const int64_t n = layers * 6 * batch * channels;
+    if (n == 0) return;
+    k_chunk_all<<<grid_for(n), 256, 0, s>>>(mod, tables_dev, out, layers, batch, channels);
+    launch_check("chunk_all");
+}
+
+void launch_patch(const void* in, void* out, int64_t batch, int64_t channels, int64_t grid,
+                  int64_t patch, bool inverse, bool f32, hipStream_t s) {
+    const int64_t n = batch * grid * grid * channels * patch * patch;
+    if (n == 0) return;
+    if (f32) {
+        k_patch<float><<<grid_for(n), 256, 0, s>>>(static_cast<const float*>(in),
+                                                   static_cast<float*>(out), batch, channels,
+                                                   grid, patch, inverse);
+    } else {
+        k_patch<bf16_t><<<grid_for(n), 256, 0, s>>>(static_cast<const bf16_t*>(in),
+                                                    static_cast<bf16_t*>(out), batch, channels,
+                                                    grid, patch, inverse);
+    }
+    launch_check("patch");
+}
+
+void launch_timestep_embedding(double t, int dim, int64_t batch, bf16_t* out, hipStream_t s) {
+    k_timestep_embedding<<<1, 128, 0, s>>>(t, dim, batch, out);
+    launch_check("timestep_embedding");
+}
+
+}  // namespace bh

@@ -1,0 +1,254 @@
+/*
+ * burnisher_hip.h -- the C ABI of libburnisher_hip.so, the MI355X (gfx950) implementation of
+ * Burnisher's `dit-step` hot path.
+ *
+ * Every entry point takes plain device pointers, element counts and a HIP stream (`void*`,
+ * NULL = the default stream) and returns 0 on success or a nonzero status with a message
+ * readable through bh_last_error(). Nothing here allocates on the hot path except where a
+ * function says so. All launches are asynchronous on the given stream; nothing synchronises
+ * the host except bh_synchronize().
+ *
+ * Storage conventions follow the reference runtime:
+ *   - element types are `bh_dtype` (storage-only bf16 with round-to-nearest-even, or fp32);
+ *     every op reads its inputs as float, computes in fp32 and rounds ONCE per stored element;
+ *   - matrices are row-major, weights are the checkpoint's [out_features, in_features];
+ *   - attention tensors are HEAD-LAST, [batch, seq, heads, head_dim].
+ *
+ * The per-op entry points below are one-to-one with the reference's op surface
+ * (/root/reference/include/burnisher/ops.h) so a reference `register_impl<Args>` lambda can
+ * forward an Args struct field by field; INTEGRATION.md shows that adapter.
+ */
+#ifndef BURNISHER_HIP_H
+#define BURNISHER_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define BH_ABI_VERSION 1
+
+typedef enum bh_dtype { BH_F32 = 0, BH_BF16 = 1 } bh_dtype;
+
+/* Mirrors burnisher::Epilogue (ops.h:17-22). GeluGated is T5-only and is rejected. */
+typedef enum bh_epilogue { BH_EPI_NONE = 0, BH_EPI_GELU = 1, BH_EPI_SILU = 2, BH_EPI_GELU_GATED = 3 }
+    bh_epilogue;
+
+/* ---- library ------------------------------------------------------------------------------ */
+
+/* ABI version this library was built with (BH_ABI_VERSION). */
+int bh_abi_version(void);
+/* "gfx950 ..." build string. */
+const char* bh_build_info(void);
+/* Message of the last failing call on this host thread ("" if none). */
+const char* bh_last_error(void);
+/* Binds the calling thread to `device` and checks that it is a gfx950 part. Safe to repeat. */
+int bh_init(int device);
+/* hipStreamSynchronize(stream) with error reporting. */
+int bh_synchronize(void* stream);
+
+/* ---- per-op entry points (the registry boundary) ------------------------------------------ */
+
+/* GemmArgs (ops.h:29-44): out[M,N] = a[M,K] @ B (+bias[N]) then `epilogue`.
+ * B is [N,K] when b_transposed (every DiT call), else [K,N]. One rounding at the store.
+ * Replaces the reference `gemm_cuda` (src/cuda/ops_cuda.cu:476-513). */
+int bh_gemm(const void* a, const void* b, const void* bias, void* out, int64_t m, int64_t n,
+            int64_t k, int b_transposed, int epilogue, int dtype, void* stream);
+
+/* The fused epilogue the dit-step engine uses, exposed so it can be tested on its own.
+ * With v = epilogue(acc + bias):
+ *   if round_mid, v is rounded to the storage type first (exactly what a separate GEMM stores);
+ *   if row_add:  v = v + row_add[(row % row_add_period), n]           (AddArgs broadcast_b)
+ *   if residual: v = residual[row, n] + gate[row / gate_rows, n] * v    (ModulateArgs gated
+ *                residual with zero scale/shift; gate NULL means 1)
+ * `ld_out` is the row stride of out and residual (>= n). b is always [N,K] (b_transposed).
+ * bf16 only. out may alias residual. */
+typedef struct bh_gemm_fused {
+    int epilogue;
+    int round_mid;
+    const void* row_add;
+    int64_t row_add_period;
+    const void* residual;
+    const void* gate;
+    int64_t gate_rows;
+    int64_t ld_out;
+} bh_gemm_fused;
+int bh_gemm_fused_run(const void* a, const void* b, const void* bias, void* out, int64_t m,
+                      int64_t n, int64_t k, const bh_gemm_fused* f, void* stream);
+
+/* AttentionArgs (ops.h:62-77): softmax(scale * q k^T (+bias) , key_mask) v, head-last.
+ * scale <= 0 means 1/sqrt(head_dim). key_mask is [batch, kv_len] (1 keeps, 0 masks -> score
+ * -1e9, so an all-masked row is uniform over v), in `mask_dtype`; bias is [heads,q_len,kv_len].
+ * Replaces `attention_cuda` (src/cuda/ops_cuda.cu:883-886). */
+int bh_attention(const void* q, const void* k, const void* v, void* out, int64_t batch,
+                 int64_t heads, int64_t q_len, int64_t kv_len, int64_t head_dim, float scale,
+                 const void* bias, const void* key_mask, int mask_dtype, int dtype, void* stream);
+
+/* The same op over row-strided operands: element (b,s,h,d) of q lives at
+ * q[(b*q_len + s)*ld_q + h*head_dim + d], likewise k/v with ld_kv and out with ld_out.
+ * Lets attention read Q,K,V straight out of one fused [M, 3*d] projection. No bias. */
+int bh_attention_strided(const void* q, int64_t ld_q, const void* k, const void* v, int64_t ld_kv,
+                         void* out, int64_t ld_out, int64_t batch, int64_t heads, int64_t q_len,
+                         int64_t kv_len, int64_t head_dim, float scale, const void* key_mask,
+                         int mask_dtype, int dtype, void* stream);
+
+/* NormArgs (ops.h:81-94): LayerNorm (rms=0) or RMSNorm (rms=1) over the last dimension with
+ * optional weight/bias; fp64 statistics like the reference oracle. GroupNorm (groups>0) is a
+ * VAE op and is rejected. Replaces `k_layernorm` (src/cuda/ops_cuda.cu:227-272). */
+int bh_norm(const void* x, const void* weight, const void* bias, void* out, int64_t rows,
+            int64_t cols, float eps, int rms, int64_t groups, int64_t channels, int dtype,
+            void* stream);
+
+/* ModulateArgs (ops.h:101-109): out = x*(1+scale[b,c]) + shift[b,c], then *gate[b,c] and
+ * +residual when given. out may alias residual. Replaces `k_modulate` (ops_cuda.cu:194-221). */
+int bh_modulate(const void* x, const void* scale, const void* shift, void* out, int64_t batch,
+                int64_t tokens, int64_t channels, const void* residual, const void* gate,
+                int dtype, void* stream);
+
+/* ActivationArgs (ops.h:111-117): SiLU / GELU-tanh elementwise (GeluGated: * gate). */
+int bh_activation(const void* x, void* out, int64_t numel, int kind, const void* gate, int dtype,
+                  void* stream);
+
+/* AddArgs (ops.h:135-143): out[r,i] = a[r,i] + scale*b[(broadcast ? 0 : r), i]. out may alias a. */
+int bh_add(const void* a, const void* b, void* out, int64_t outer, int64_t inner, float scale,
+           int broadcast_b, int dtype, void* stream);
+
+/* ChunkArgs (ops.h:150-159): out[b,c] = modulation[b, chunk*channels + c] + table[trow, c],
+ * trow = table_chunk >= 0 ? table_chunk : chunk. */
+int bh_chunk(const void* modulation, const void* table, void* out, int64_t batch,
+             int64_t channels, int64_t chunks, int64_t chunk, int64_t table_chunk, int dtype,
+             void* stream);
+
+/* PatchArgs (ops.h:161-173): forward [B,C,G*P,G*P] -> [B,G*G,C*P*P] in (c,ky,kx) order; inverse
+ * [B,G*G,P*P*C] in (ky,kx,c) order -> [B,C,G*P,G*P]. */
+int bh_patch(const void* in, void* out, int64_t batch, int64_t channels, int64_t grid,
+             int64_t patch, int inverse, int dtype, void* stream);
+
+/* ---- fused ops (no single reference op; each equals a fixed reference op sequence) -------- */
+
+/* norm -> chunk(shift) -> chunk(scale) -> modulate, as the reference DiT block runs them
+ * (pixart_dit.cpp:226-231): with every intermediate rounded where the reference stores it,
+ *   shift[b,c] = mod[b, shift_chunk*C + c] + table[shift_row, c]
+ *   scale[b,c] = mod[b, scale_chunk*C + c] + table[scale_row, c]
+ *   out = LN(x)*(1+scale) + shift.
+ * mod is [batch, mod_chunks*C], table is [*, C], x/out are [batch*tokens, C]. bf16 only. */
+int bh_norm_modulate(const void* x, const void* mod, int64_t mod_chunks, int64_t shift_chunk,
+                     int64_t scale_chunk, const void* table, int64_t shift_row, int64_t scale_row,
+                     void* out, int64_t batch, int64_t tokens, int64_t channels, float eps,
+                     void* stream);
+
+/* ---- the dit-step engine ------------------------------------------------------------------ */
+
+/* DiTConfig (models.h:105-118). */
+typedef struct bh_dit_config {
+    int num_layers;       /* 28 */
+    int num_heads;        /* 16 */
+    int head_dim;         /* 72 */
+    int patch_size;       /* 2 */
+    int in_channels;      /* 4 */
+    int out_channels;     /* 8 */
+    int caption_channels; /* 4096 */
+    int sample_size;      /* 128: base grid = sample_size / patch_size */
+    double mlp_ratio;     /* 4.0 */
+    double eps;           /* 1e-6 */
+} bh_dit_config;
+
+/* One transformer block's weights, device pointers in bf16, named as in the checkpoint
+ * (`transformer_blocks.<i>.<name>`, weights.cpp:267-282). */
+typedef struct bh_dit_block_weights {
+    const void* scale_shift_table; /* [6, d] */
+    const void* attn1_q_w; const void* attn1_q_b;
+    const void* attn1_k_w; const void* attn1_k_b;
+    const void* attn1_v_w; const void* attn1_v_b;
+    const void* attn1_o_w; const void* attn1_o_b; /* to_out.0 */
+    const void* attn2_q_w; const void* attn2_q_b;
+    const void* attn2_k_w; const void* attn2_k_b;
+    const void* attn2_v_w; const void* attn2_v_b;
+    const void* attn2_o_w; const void* attn2_o_b;
+    const void* ff0_w; const void* ff0_b; /* ff.net.0.proj: [d_ff, d] */
+    const void* ff2_w; const void* ff2_b; /* ff.net.2:      [d, d_ff] */
+} bh_dit_block_weights;
+
+/* The model's weights (weights.cpp:252-266), device pointers in bf16. */
+typedef struct bh_dit_weights {
+    const void* pos_embed_w;  /* pos_embed.proj.weight [d, C, p, p] */
+    const void* pos_embed_b;
+    const void* t_emb1_w;     /* adaln_single.emb.timestep_embedder.linear_1 [d, 256] */
+    const void* t_emb1_b;
+    const void* t_emb2_w;     /* ...linear_2 [d, d] */
+    const void* t_emb2_b;
+    const void* adaln_w;      /* adaln_single.linear [6d, d] */
+    const void* adaln_b;
+    const void* cap1_w;       /* caption_projection.linear_1 [d, caption_channels] */
+    const void* cap1_b;
+    const void* cap2_w;       /* caption_projection.linear_2 [d, d] */
+    const void* cap2_b;
+    const void* out_table;    /* scale_shift_table [2, d] */
+    const void* proj_out_w;   /* proj_out [p*p*out_channels, d] */
+    const void* proj_out_b;
+    const bh_dit_block_weights* blocks; /* num_layers entries */
+} bh_dit_weights;
+
+/* How bh_dit_forward evaluates the graph. */
+typedef enum bh_dit_mode {
+    /* The MI355X plan: QKV fused into one GEMM, every layer's caption K/V in one GEMM, LN and
+     * modulation fused, gated residuals in GEMM epilogues. */
+    BH_DIT_FUSED = 0,
+    /* The reference graph (pixart_dit.cpp:112-304) op by op through the per-op entry points:
+     * the drop-in path a reference registry would run. */
+    BH_DIT_OPWISE = 1
+} bh_dit_mode;
+
+typedef struct bh_dit bh_dit;
+
+/* Prepares a forward for a fixed geometry: batch, latent side (H = W) and caption length.
+ * Allocates every intermediate once (zero-filled) and any repacked weights; the weight
+ * pointers must stay valid for the engine's lifetime. This call allocates; forward does not. */
+int bh_dit_create(const bh_dit_config* cfg, const bh_dit_weights* w, int64_t batch,
+                  int64_t latent_hw, int64_t caption_len, int mode, bh_dit** out);
+/* PixArtDiT::forward (pixart_dit.cpp:112-304): latent [B, in_ch, H, W], caption
+ * [B, caption_len, caption_channels], caption_mask [B, caption_len] in mask_dtype, output
+ * [B, out_ch, H, W]; all bf16 device pointers except the mask. No host synchronisation. */
+int bh_dit_forward(bh_dit* e, const void* latent, double timestep, const void* caption,
+                   const void* caption_mask, int mask_dtype, void* out, void* stream);
+/* Device bytes the engine holds (intermediates plus repacked weights). */
+int64_t bh_dit_workspace_bytes(const bh_dit* e);
+void bh_dit_destroy(bh_dit* e);
+
+/* ---- measurement and inputs --------------------------------------------------------------- */
+
+/* Kernel classes timed by the launch profiler. */
+typedef enum bh_kernel_class {
+    BH_K_GEMM = 0,        /* the MFMA GEMM, every shape */
+    BH_K_GEMV = 1,        /* small-M GEMMs (timestep / adaLN projections) */
+    BH_K_ATTN_SELF = 2,   /* flash attention, kv_len == q_len */
+    BH_K_ATTN_CROSS = 3,  /* flash attention, kv_len != q_len */
+    BH_K_NORM = 4,        /* LayerNorm and LayerNorm+modulate */
+    BH_K_ELEMENTWISE = 5, /* modulate, add, chunk, activation, patch, embeddings */
+    BH_K_GEMM_FF0 = 6,    /* engine: the [M,4608,1152] GELU projection (also counted as GEMM) */
+    BH_K_GEMM_FF2 = 7,    /* engine: the [M,1152,4608] projection (also counted as GEMM) */
+    BH_K_GEMM_QKV = 8,    /* engine: the fused [M,3456,1152] projection (also counted as GEMM) */
+    BH_K_COUNT = 9
+} bh_kernel_class;
+
+/* When enabled, every launch is bracketed by HIP events on its own stream and the elapsed
+ * time is accumulated per class. Enabling resets the counters. Costs a little per launch;
+ * off by default. */
+int bh_profile_enable(int class_mask);
+/* Sums since enable, synchronising on the recorded events: total ms, launches and algorithmic
+ * FLOP (or bytes, for the bandwidth classes) per class. */
+int bh_profile_read(int kernel_class, double* total_ms, int64_t* launches, double* work);
+
+/* Fills host memory with N(0, std^2) draws, rounded to bf16: Box-Muller over a splitmix64
+ * stream seeded from `seed` and the FNV-1a hash of `name` (the reference's per-name keying,
+ * weights.cpp:87-88, and noise recipe, pipeline.cpp:41-58). Element i uses stream draws
+ * 2*(i/2) and 2*(i/2)+1, so the result does not depend on how the work is split. Host only. */
+int bh_fill_normal_bf16(uint16_t* dst, int64_t n, uint64_t seed, const char* name, float std_dev);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* BURNISHER_HIP_H */

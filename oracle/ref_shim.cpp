@@ -1,0 +1,255 @@
+// oracle/ref_shim.cpp -- TEST INFRASTRUCTURE ONLY. A C entry layer over the REFERENCE runtime's
+// own `stock` implementation, compiled together with the reference sources where they lie
+// (/root/reference/src/...; see the `ref` target of oracle/Makefile) into
+// oracle/_ref/libref_stock.so. It lets the tests pin the restatement in stock.cpp against the
+// real reference at small shapes. Nothing here reimplements an op: every call goes through the
+// reference's registry (`OpRegistry<Args>::instance().get("stock")`) or its model code.
+#include <cstdint>
+#include <cstring>
+#include <map>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "burnisher/models.h"
+#include "burnisher/ops.h"
+
+#include "../include/burnisher_hip.h"
+
+using namespace burnisher;
+
+namespace {
+
+thread_local std::string g_err;
+
+DType dt_of(int dtype) { return dtype == BH_F32 ? DType::F32 : DType::BF16; }
+
+Tensor view(const void* p, std::vector<int64_t> shape, int dtype) {
+    return Tensor::view(const_cast<void*>(p), std::move(shape), dt_of(dtype));
+}
+
+template <typename Fn>
+int guard(Fn fn) {
+    try {
+        static bool registered = false;
+        if (!registered) {
+            register_all_ops();
+            registered = true;
+        }
+        fn();
+        return 0;
+    } catch (const std::exception& e) {
+        g_err = e.what();
+        return 1;
+    }
+}
+
+Epilogue epi_of(int e) {
+    switch (e) {
+        case BH_EPI_GELU: return Epilogue::Gelu;
+        case BH_EPI_SILU: return Epilogue::Silu;
+        case BH_EPI_GELU_GATED: return Epilogue::GeluGated;
+        default: return Epilogue::None;
+    }
+}
+
+// Serves the weight table the tests hand over, by checkpoint name, as bf16 views.
+class TableWeights : public WeightSource {
+  public:
+    TableWeights(const bh_dit_config& c, const bh_dit_weights& w) {
+        const int64_t d = static_cast<int64_t>(c.num_heads) * c.head_dim;
+        const int64_t dff = static_cast<int64_t>(static_cast<double>(d) * c.mlp_ratio);
+        const int64_t p = c.patch_size, p2 = p * p;
+        put("pos_embed.proj.weight", w.pos_embed_w, {d, c.in_channels, p, p});
+        put("pos_embed.proj.bias", w.pos_embed_b, {d});
+        put("adaln_single.emb.timestep_embedder.linear_1.weight", w.t_emb1_w, {d, 256});
+        put("adaln_single.emb.timestep_embedder.linear_1.bias", w.t_emb1_b, {d});
+        put("adaln_single.emb.timestep_embedder.linear_2.weight", w.t_emb2_w, {d, d});
+        put("adaln_single.emb.timestep_embedder.linear_2.bias", w.t_emb2_b, {d});
+        put("adaln_single.linear.weight", w.adaln_w, {6 * d, d});
+        put("adaln_single.linear.bias", w.adaln_b, {6 * d});
+        put("caption_projection.linear_1.weight", w.cap1_w, {d, c.caption_channels});
+        put("caption_projection.linear_1.bias", w.cap1_b, {d});
+        put("caption_projection.linear_2.weight", w.cap2_w, {d, d});
+        put("caption_projection.linear_2.bias", w.cap2_b, {d});
+        put("scale_shift_table", w.out_table, {2, d});
+        put("proj_out.weight", w.proj_out_w, {p2 * c.out_channels, d});
+        put("proj_out.bias", w.proj_out_b, {p2 * c.out_channels});
+        for (int i = 0; i < c.num_layers; ++i) {
+            const bh_dit_block_weights& b = w.blocks[i];
+            const std::string n = "transformer_blocks." + std::to_string(i) + ".";
+            put(n + "scale_shift_table", b.scale_shift_table, {6, d});
+            const void* ws[2][4][2] = {
+                {{b.attn1_q_w, b.attn1_q_b}, {b.attn1_k_w, b.attn1_k_b},
+                 {b.attn1_v_w, b.attn1_v_b}, {b.attn1_o_w, b.attn1_o_b}},
+                {{b.attn2_q_w, b.attn2_q_b}, {b.attn2_k_w, b.attn2_k_b},
+                 {b.attn2_v_w, b.attn2_v_b}, {b.attn2_o_w, b.attn2_o_b}}};
+            const char* an[2] = {"attn1", "attn2"};
+            const char* pn[4] = {"to_q", "to_k", "to_v", "to_out.0"};
+            for (int a = 0; a < 2; ++a)
+                for (int j = 0; j < 4; ++j) {
+                    put(n + an[a] + "." + pn[j] + ".weight", ws[a][j][0], {d, d});
+                    put(n + an[a] + "." + pn[j] + ".bias", ws[a][j][1], {d});
+                }
+            put(n + "ff.net.0.proj.weight", b.ff0_w, {dff, d});
+            put(n + "ff.net.0.proj.bias", b.ff0_b, {dff});
+            put(n + "ff.net.2.weight", b.ff2_w, {d, dff});
+            put(n + "ff.net.2.bias", b.ff2_b, {d});
+        }
+    }
+    bool has(const std::string& name) const override { return m_.count(name) != 0; }
+    Tensor get(const std::string& name) const override { return m_.at(name); }
+
+  private:
+    void put(const std::string& name, const void* p, std::vector<int64_t> shape) {
+        m_.emplace(name, view(p, std::move(shape), BH_BF16));
+    }
+    std::map<std::string, Tensor> m_;
+};
+
+}  // namespace
+
+extern "C" {
+
+const char* ref_last_error(void) { return g_err.c_str(); }
+
+int ref_gemm(const void* a, const void* b, const void* bias, void* out, int64_t m, int64_t n,
+             int64_t k, int b_transposed, int epilogue, int dtype) {
+    return guard([&] {
+        Tensor ta = view(a, {m, k}, dtype);
+        Tensor tb = view(b, b_transposed ? std::vector<int64_t>{n, k} : std::vector<int64_t>{k, n}, dtype);
+        Tensor tbias = bias ? view(bias, {n}, dtype) : Tensor();
+        Tensor to = view(out, {m, n}, dtype);
+        GemmArgs g{&ta, &tb, bias ? &tbias : nullptr, &to, m, n, k, b_transposed != 0,
+                   epi_of(epilogue)};
+        GemmRegistry::instance().get("stock")(g);
+    });
+}
+
+int ref_attention(const void* q, const void* k, const void* v, void* out, int64_t batch,
+                  int64_t heads, int64_t q_len, int64_t kv_len, int64_t head_dim, float scale,
+                  const void* bias, const void* key_mask, int mask_dtype, int dtype,
+                  int materialized) {
+    return guard([&] {
+        Tensor tq = view(q, {batch, q_len, heads, head_dim}, dtype);
+        Tensor tk = view(k, {batch, kv_len, heads, head_dim}, dtype);
+        Tensor tv = view(v, {batch, kv_len, heads, head_dim}, dtype);
+        Tensor to = view(out, {batch, q_len, heads, head_dim}, dtype);
+        Tensor tb = bias ? view(bias, {heads, q_len, kv_len}, dtype) : Tensor();
+        Tensor tm = key_mask ? view(key_mask, {batch, kv_len}, mask_dtype) : Tensor();
+        AttentionArgs args{&tq, &tk, &tv, &to, batch, heads, q_len, kv_len, head_dim, scale,
+                           bias ? &tb : nullptr, key_mask ? &tm : nullptr};
+        AttentionRegistry::instance().get(materialized ? "materialized" : "stock")(args);
+    });
+}
+
+int ref_norm(const void* x, const void* weight, const void* bias, void* out, int64_t rows,
+             int64_t cols, float eps, int rms, int dtype) {
+    return guard([&] {
+        Tensor tx = view(x, {rows, cols}, dtype), to = view(out, {rows, cols}, dtype);
+        Tensor tw = weight ? view(weight, {cols}, dtype) : Tensor();
+        Tensor tb = bias ? view(bias, {cols}, dtype) : Tensor();
+        NormArgs a{&tx, weight ? &tw : nullptr, bias ? &tb : nullptr, &to, rows, cols, eps,
+                   rms != 0, 0, 0};
+        NormRegistry::instance().get("stock")(a);
+    });
+}
+
+int ref_modulate(const void* x, const void* scale, const void* shift, void* out, int64_t batch,
+                 int64_t tokens, int64_t channels, const void* residual, const void* gate,
+                 int dtype) {
+    return guard([&] {
+        Tensor tx = view(x, {batch, tokens, channels}, dtype);
+        Tensor to = view(out, {batch, tokens, channels}, dtype);
+        Tensor ts = view(scale, {batch, channels}, dtype), th = view(shift, {batch, channels}, dtype);
+        Tensor tr = residual ? view(residual, {batch, tokens, channels}, dtype) : Tensor();
+        Tensor tg = gate ? view(gate, {batch, channels}, dtype) : Tensor();
+        ModulateArgs a{&tx, &ts, &th, &to, batch, tokens, channels, residual ? &tr : nullptr,
+                       gate ? &tg : nullptr};
+        ModulateRegistry::instance().get("stock")(a);
+    });
+}
+
+int ref_activation(const void* x, void* out, int64_t n, int kind, const void* gate, int dtype) {
+    return guard([&] {
+        Tensor tx = view(x, {n}, dtype), to = view(out, {n}, dtype);
+        Tensor tg = gate ? view(gate, {n}, dtype) : Tensor();
+        ActivationArgs a{&tx, &to, n, epi_of(kind), gate ? &tg : nullptr};
+        ActivationRegistry::instance().get("stock")(a);
+    });
+}
+
+int ref_add(const void* a, const void* b, void* out, int64_t outer, int64_t inner, float scale,
+            int broadcast_b, int dtype) {
+    return guard([&] {
+        Tensor ta = view(a, {outer, inner}, dtype), to = view(out, {outer, inner}, dtype);
+        Tensor tb = view(b, broadcast_b ? std::vector<int64_t>{inner} : std::vector<int64_t>{outer, inner}, dtype);
+        AddArgs args{&ta, &tb, &to, outer, inner, scale, broadcast_b != 0};
+        AddRegistry::instance().get("stock")(args);
+    });
+}
+
+int ref_chunk(const void* mod, const void* table, void* out, int64_t batch, int64_t channels,
+              int64_t chunks, int64_t chunk, int64_t table_chunk, int table_rows, int dtype) {
+    return guard([&] {
+        Tensor tm = view(mod, {batch, chunks * channels}, dtype);
+        Tensor tt = view(table, {table_rows, channels}, dtype);
+        Tensor to = view(out, {batch, channels}, dtype);
+        ChunkArgs a{&tm, &tt, &to, batch, channels, chunks, chunk, table_chunk};
+        ChunkRegistry::instance().get("stock")(a);
+    });
+}
+
+int ref_patch(const void* in, void* out, int64_t batch, int64_t channels, int64_t grid,
+              int64_t patch, int inverse, int dtype) {
+    return guard([&] {
+        const int64_t H = grid * patch, tok = grid * grid, per = channels * patch * patch;
+        Tensor img = view(inverse ? out : in, {batch, channels, H, H}, dtype);
+        Tensor tks = view(inverse ? in : out, {batch, tok, per}, dtype);
+        PatchArgs a{inverse ? &tks : &img, inverse ? &img : &tks, batch, channels, grid, patch,
+                    inverse != 0};
+        PatchRegistry::instance().get("stock")(a);
+    });
+}
+
+int ref_position_embedding(double* out, int dim, int grid, int base, double interp) {
+    return guard([&] {
+        const std::vector<double> pe = dit_position_embedding(dim, grid, base, interp);
+        std::memcpy(out, pe.data(), pe.size() * sizeof(double));
+    });
+}
+
+int ref_timestep_embedding(double t, int dim, float* out) {
+    return guard([&] {
+        Tensor e = sinusoidal_timestep_embedding(t, dim, DType::F32);
+        std::memcpy(out, e.data(), sizeof(float) * dim);
+    });
+}
+
+int ref_dit_forward(const bh_dit_config* cfg, const bh_dit_weights* w, int64_t batch,
+                    int64_t latent_hw, int64_t caption_len, const uint16_t* latent,
+                    double timestep, const uint16_t* caption, const void* mask, int mask_dtype,
+                    uint16_t* image, int layers) {
+    return guard([&] {
+        DiTConfig dc;
+        dc.num_layers = layers >= 0 ? std::min(layers, cfg->num_layers) : cfg->num_layers;
+        dc.num_heads = cfg->num_heads;
+        dc.head_dim = cfg->head_dim;
+        dc.patch_size = cfg->patch_size;
+        dc.in_channels = cfg->in_channels;
+        dc.out_channels = cfg->out_channels;
+        dc.caption_channels = cfg->caption_channels;
+        dc.mlp_ratio = cfg->mlp_ratio;
+        dc.eps = cfg->eps;
+        dc.sample_size = cfg->sample_size;
+        TableWeights weights(*cfg, *w);
+        PixArtDiT model(dc, weights, DType::BF16);
+        Tensor z = view(latent, {batch, cfg->in_channels, latent_hw, latent_hw}, BH_BF16);
+        Tensor cap = view(caption, {batch, caption_len, cfg->caption_channels}, BH_BF16);
+        Tensor m = view(mask, {batch, caption_len}, mask_dtype);
+        Tensor out = model.forward(z, timestep, cap, m, ImplSelection::from_request("stock"));
+        std::memcpy(image, out.data(), out.nbytes());
+    });
+}
+
+}  // extern "C"

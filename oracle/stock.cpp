@@ -1,0 +1,604 @@
+// oracle/stock.cpp -- TEST INFRASTRUCTURE ONLY. A CPU restatement of the reference runtime's
+// `stock` implementation of the dit-step ops and graph, used as the parity checker for the HIP
+// path and as the CPU baseline that bench.py times. Only tests/, __graft_entry__.smoke() and
+// bench.py's cpu_baseline leg may load it; the product (burnisher_amd/) never does.
+//
+// It follows, function by function (cited at each function):
+//   /root/reference/src/cpu/ops_cpu.cpp        the op kernels
+//   /root/reference/src/models/pixart_dit.cpp  the graph and the position table
+//   /root/reference/src/models/weights.cpp     the timestep embedding
+//   /root/reference/include/burnisher/dtype.h  bf16 round-to-nearest-even
+//
+// The numerics contract is the reference's, restated exactly:
+//   * every op reads its inputs as float, computes in fp32 and rounds ONCE per stored element
+//     to the storage dtype (tensor.cpp:85-96);
+//   * every reduction runs in the reference's fixed sequential order with an fp32 accumulator
+//     (GEMM over k, attention over d and over keys), LayerNorm statistics in fp64;
+//   * no fused multiply-add: this file is compiled with -ffp-contract=off, as the reference's
+//     x86-64 build has no FMA to contract into.
+// What differs from the reference is only speed: operands are widened to float once per call,
+// loops are blocked and vectorised ACROSS independent outputs (never across a reduction), and
+// the work is split over threads by output rows. Every output is therefore computed by the same
+// sequence of fp32 operations as in the reference, whatever the thread count.
+#include <algorithm>
+#include <atomic>
+#include <cmath>
+#include <cstdint>
+#include <cstring>
+#include <stdexcept>
+#include <string>
+#include <thread>
+#include <vector>
+
+#include "../include/burnisher_hip.h"
+
+namespace {
+
+// ---- dtype (dtype.h:50-72) ------------------------------------------------------------------
+
+inline float bf16_to_f32(uint16_t v) {
+    uint32_t u = static_cast<uint32_t>(v) << 16;
+    float f;
+    std::memcpy(&f, &u, 4);
+    return f;
+}
+inline uint16_t f32_to_bf16(float f) {
+    uint32_t u;
+    std::memcpy(&u, &f, 4);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x0040u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return static_cast<uint16_t>(u >> 16);
+}
+
+// A typed buffer: what Tensor::get/set do for one dtype.
+struct View {
+    const void* p;
+    int dt;  // BH_F32 or BH_BF16
+    float get(int64_t i) const {
+        return dt == BH_F32 ? static_cast<const float*>(p)[i]
+                            : bf16_to_f32(static_cast<const uint16_t*>(p)[i]);
+    }
+};
+struct Out {
+    void* p;
+    int dt;
+    void set(int64_t i, float v) const {
+        if (dt == BH_F32) static_cast<float*>(p)[i] = v;
+        else static_cast<uint16_t*>(p)[i] = f32_to_bf16(v);
+    }
+};
+// What storing through the dtype does to a value.
+inline float stored(float v, int dt) { return dt == BH_F32 ? v : bf16_to_f32(f32_to_bf16(v)); }
+
+std::vector<float> widen(const void* p, int dt, int64_t n) {
+    std::vector<float> out(static_cast<size_t>(n));
+    View v{p, dt};
+    for (int64_t i = 0; i < n; ++i) out[i] = v.get(i);
+    return out;
+}
+
+// ---- threads --------------------------------------------------------------------------------
+
+int resolve_threads(int t) {
+    if (t > 0) return t;
+    const unsigned hc = std::thread::hardware_concurrency();
+    return hc ? static_cast<int>(hc) : 1;
+}
+
+// Calls fn(i) for i in [0, n), items handed out dynamically. Each item writes only its own
+// outputs, so the result does not depend on the schedule.
+template <typename Fn>
+void parallel_for(int64_t n, int threads, Fn fn) {
+    threads = std::max(1, std::min<int>(threads, static_cast<int>(std::min<int64_t>(n, 1 << 20))));
+    if (threads <= 1) {
+        for (int64_t i = 0; i < n; ++i) fn(i);
+        return;
+    }
+    std::atomic<int64_t> next{0};
+    std::vector<std::thread> pool;
+    for (int t = 0; t < threads; ++t) {
+        pool.emplace_back([&] {
+            for (int64_t i = next++; i < n; i = next++) fn(i);
+        });
+    }
+    for (auto& th : pool) th.join();
+}
+
+// ---- activations (ops_cpu.cpp:27-46) --------------------------------------------------------
+
+inline float gelu_tanh(float x) {
+    const float c = 0.7978845608028654f;
+    float x3 = x * x * x;
+    return 0.5f * x * (1.0f + std::tanh(c * (x + 0.044715f * x3)));
+}
+inline float silu(float x) { return x / (1.0f + std::exp(-x)); }
+inline float apply_epilogue(int e, float v) {
+    switch (e) {
+        case BH_EPI_GELU: return gelu_tanh(v);
+        case BH_EPI_SILU: return silu(v);
+        case BH_EPI_GELU_GATED: return gelu_tanh(v);
+        default: return v;
+    }
+}
+
+// ---- gemm (ops_cpu.cpp:48-79) ---------------------------------------------------------------
+
+// out[i,j] = epilogue(sum_p a[i,p]*b(p,j) + bias[j]), p sequential from 0, fp32 accumulator.
+// Vectorised across j: bt is B widened and laid out [K][N] so that one k step updates a run of
+// independent column accumulators.
+void gemm_impl(const void* a, const void* b, const void* bias, void* out, int64_t M, int64_t N,
+               int64_t K, bool b_transposed, int epilogue, int dt, int threads) {
+    std::vector<float> af = widen(a, dt, M * K);
+    std::vector<float> bt(static_cast<size_t>(K * N));
+    {
+        View bv{b, dt};
+        for (int64_t p = 0; p < K; ++p)
+            for (int64_t j = 0; j < N; ++j)
+                bt[p * N + j] = bv.get(b_transposed ? (j * K + p) : (p * N + j));
+    }
+    std::vector<float> biasf = bias ? widen(bias, dt, N) : std::vector<float>();
+    const Out o{out, dt};
+    constexpr int64_t RB = 4, CB = 256;
+    const int64_t row_blocks = (M + RB - 1) / RB;
+    parallel_for(row_blocks, threads, [&](int64_t rb) {
+        const int64_t i0 = rb * RB, i1 = std::min(M, i0 + RB);
+        float acc[RB][CB];
+        for (int64_t j0 = 0; j0 < N; j0 += CB) {
+            const int64_t jn = std::min(CB, N - j0);
+            for (int64_t r = 0; r < RB; ++r)
+                for (int64_t jj = 0; jj < CB; ++jj) acc[r][jj] = 0.0f;
+            for (int64_t p = 0; p < K; ++p) {
+                const float* brow = &bt[p * N + j0];
+                for (int64_t i = i0; i < i1; ++i) {
+                    const float av = af[i * K + p];
+                    float* ac = acc[i - i0];
+                    for (int64_t jj = 0; jj < jn; ++jj) ac[jj] += av * brow[jj];
+                }
+            }
+            for (int64_t i = i0; i < i1; ++i) {
+                for (int64_t jj = 0; jj < jn; ++jj) {
+                    float v = acc[i - i0][jj];
+                    if (bias) v += biasf[j0 + jj];
+                    o.set(i * N + j0 + jj, apply_epilogue(epilogue, v));
+                }
+            }
+        }
+    });
+}
+
+// ---- attention (ops_cpu.cpp:84-184) ---------------------------------------------------------
+
+struct AttnGeom {
+    int64_t B, H, Sq, Skv, D;
+    int64_t ld_q, ld_kv, ld_o;
+};
+
+// Streaming attention (ops_cpu.cpp:84-131), one query row at a time: scores over d sequential,
+// times scale, + bias, masked keys set to -1e9; row max; exp(s - max) and the denominator summed
+// over keys in order; the value accumulator over keys in order; divide at the end.
+void attention_impl(const void* q, const void* k, const void* v, void* out, const AttnGeom& g,
+                    float scale, const void* bias, const void* mask, int mask_dt, int dt,
+                    int threads, bool materialized) {
+    const float sc = scale > 0.0f ? scale : 1.0f / std::sqrt(static_cast<float>(g.D));
+    const View qv{q, dt}, kv{k, dt}, vv{v, dt}, bv{bias, dt}, mv{mask, mask_dt};
+    const Out o{out, dt};
+    // per (b, h): K transposed to [D][Skv] and V as [Skv][D], widened once
+    const int64_t BH = g.B * g.H;
+    constexpr int64_t QB = 16;
+    const int64_t qblocks = (g.Sq + QB - 1) / QB;
+    std::vector<std::vector<float>> kt(BH), vf(BH);
+    parallel_for(BH, threads, [&](int64_t bh) {
+        const int64_t b = bh / g.H, h = bh % g.H;
+        kt[bh].resize(static_cast<size_t>(g.D * g.Skv));
+        vf[bh].resize(static_cast<size_t>(g.Skv * g.D));
+        for (int64_t j = 0; j < g.Skv; ++j) {
+            const int64_t base = (b * g.Skv + j) * g.ld_kv + h * g.D;
+            for (int64_t d = 0; d < g.D; ++d) {
+                kt[bh][d * g.Skv + j] = kv.get(base + d);
+                vf[bh][j * g.D + d] = vv.get(base + d);
+            }
+        }
+    });
+    std::vector<float> keep(static_cast<size_t>(mask ? g.B * g.Skv : 0));
+    for (size_t i = 0; i < keep.size(); ++i) keep[i] = mv.get(static_cast<int64_t>(i));
+    parallel_for(BH * qblocks, threads, [&](int64_t item) {
+        const int64_t bh = item / qblocks, qb = item % qblocks;
+        const int64_t b = bh / g.H, h = bh % g.H;
+        std::vector<float> s(static_cast<size_t>(g.Skv)), acc(static_cast<size_t>(g.D)),
+            qrow(static_cast<size_t>(g.D));
+        const float* K = kt[bh].data();
+        const float* V = vf[bh].data();
+        for (int64_t i = qb * QB; i < std::min(g.Sq, (qb + 1) * QB); ++i) {
+            const int64_t qbase = (b * g.Sq + i) * g.ld_q + h * g.D;
+            for (int64_t d = 0; d < g.D; ++d) qrow[d] = qv.get(qbase + d);
+            std::fill(s.begin(), s.end(), 0.0f);
+            for (int64_t d = 0; d < g.D; ++d) {
+                const float qd = qrow[d];
+                const float* krow = K + d * g.Skv;
+                for (int64_t j = 0; j < g.Skv; ++j) s[j] += qd * krow[j];
+            }
+            float row_max = -INFINITY;
+            for (int64_t j = 0; j < g.Skv; ++j) {
+                float x = s[j] * sc;
+                if (bias) x += bv.get((h * g.Sq + i) * g.Skv + j);
+                if (mask && keep[b * g.Skv + j] == 0.0f) x = -1e9f;
+                s[j] = x;
+                row_max = std::max(row_max, x);
+            }
+            float denom = 0.0f;
+            for (int64_t j = 0; j < g.Skv; ++j) {
+                s[j] = std::exp(s[j] - row_max);
+                denom += s[j];
+            }
+            if (materialized) {
+                // ops_cpu.cpp:163-181: weights normalised first, then one accumulation per d.
+                for (int64_t j = 0; j < g.Skv; ++j) s[j] /= denom;
+                std::fill(acc.begin(), acc.end(), 0.0f);
+                for (int64_t j = 0; j < g.Skv; ++j) {
+                    const float w = s[j];
+                    const float* vrow = V + j * g.D;
+                    for (int64_t d = 0; d < g.D; ++d) acc[d] += w * vrow[d];
+                }
+                const int64_t obase = (b * g.Sq + i) * g.ld_o + h * g.D;
+                for (int64_t d = 0; d < g.D; ++d) o.set(obase + d, acc[d]);
+            } else {
+                std::fill(acc.begin(), acc.end(), 0.0f);
+                for (int64_t j = 0; j < g.Skv; ++j) {
+                    const float w = s[j];
+                    const float* vrow = V + j * g.D;
+                    for (int64_t d = 0; d < g.D; ++d) acc[d] += w * vrow[d];
+                }
+                const int64_t obase = (b * g.Sq + i) * g.ld_o + h * g.D;
+                for (int64_t d = 0; d < g.D; ++d) o.set(obase + d, acc[d] / denom);
+            }
+        }
+    });
+}
+
+// ---- norm (ops_cpu.cpp:226-246) -------------------------------------------------------------
+
+void norm_impl(const void* x, const void* w, const void* bias, void* out, int64_t rows,
+               int64_t cols, float eps, bool rms, int dt, int threads) {
+    const View xv{x, dt}, wv{w, dt}, bv{bias, dt};
+    const Out o{out, dt};
+    parallel_for(rows, threads, [&](int64_t r) {
+        const int64_t base = r * cols;
+        double mean = 0.0;
+        if (!rms) {
+            for (int64_t i = 0; i < cols; ++i) mean += xv.get(base + i);
+            mean /= cols;
+        }
+        double var = 0.0;
+        for (int64_t i = 0; i < cols; ++i) {
+            double d = xv.get(base + i) - mean;
+            var += d * d;
+        }
+        var /= cols;
+        const float inv = 1.0f / std::sqrt(static_cast<float>(var) + eps);
+        for (int64_t i = 0; i < cols; ++i) {
+            float v = (xv.get(base + i) - static_cast<float>(mean)) * inv;
+            if (w) v *= wv.get(i);
+            if (bias) v += bv.get(i);
+            o.set(base + i, v);
+        }
+    });
+}
+
+// ---- modulate, activation, add, chunk, patch (ops_cpu.cpp:249-349) --------------------------
+
+void modulate_impl(const void* x, const void* scale, const void* shift, void* out, int64_t B,
+                   int64_t T, int64_t C, const void* residual, const void* gate, int dt) {
+    const View xv{x, dt}, sc{scale, dt}, sh{shift, dt}, rv{residual, dt}, gv{gate, dt};
+    const Out o{out, dt};
+    for (int64_t b = 0; b < B; ++b)
+        for (int64_t t = 0; t < T; ++t) {
+            const int64_t base = (b * T + t) * C;
+            for (int64_t c = 0; c < C; ++c) {
+                float v = xv.get(base + c);
+                v = v * (1.0f + sc.get(b * C + c)) + sh.get(b * C + c);
+                if (gate) v *= gv.get(b * C + c);
+                if (residual) v += rv.get(base + c);
+                o.set(base + c, v);
+            }
+        }
+}
+
+void activation_impl(const void* x, void* out, int64_t n, int kind, const void* gate, int dt) {
+    const View xv{x, dt}, gv{gate, dt};
+    const Out o{out, dt};
+    for (int64_t i = 0; i < n; ++i) {
+        float v = apply_epilogue(kind, xv.get(i));
+        if (kind == BH_EPI_GELU_GATED) v *= gv.get(i);
+        o.set(i, v);
+    }
+}
+
+void add_impl(const void* a, const void* b, void* out, int64_t outer, int64_t inner, float scale,
+              bool broadcast, int dt) {
+    const View av{a, dt}, bv{b, dt};
+    const Out o{out, dt};
+    for (int64_t r = 0; r < outer; ++r)
+        for (int64_t i = 0; i < inner; ++i) {
+            const int64_t at = r * inner + i;
+            o.set(at, av.get(at) + scale * bv.get(broadcast ? i : at));
+        }
+}
+
+void chunk_impl(const void* mod, const void* table, void* out, int64_t B, int64_t C,
+                int64_t chunks, int64_t chunk, int64_t table_chunk, int dt) {
+    const View mv{mod, dt}, tv{table, dt};
+    const Out o{out, dt};
+    const int64_t trow = table_chunk >= 0 ? table_chunk : chunk;
+    for (int64_t b = 0; b < B; ++b)
+        for (int64_t c = 0; c < C; ++c)
+            o.set(b * C + c, mv.get(b * chunks * C + chunk * C + c) + tv.get(trow * C + c));
+}
+
+void patch_impl(const void* in, void* out, int64_t B, int64_t C, int64_t G, int64_t P,
+                bool inverse, int dt) {
+    const View iv{in, dt};
+    const Out o{out, dt};
+    const int64_t H = G * P, per_token = C * P * P;
+    for (int64_t b = 0; b < B; ++b)
+        for (int64_t ty = 0; ty < G; ++ty)
+            for (int64_t tx = 0; tx < G; ++tx)
+                for (int64_t c = 0; c < C; ++c)
+                    for (int64_t ky = 0; ky < P; ++ky)
+                        for (int64_t kx = 0; kx < P; ++kx) {
+                            const int64_t img = ((b * C + c) * H + ty * P + ky) * H + tx * P + kx;
+                            const int64_t tok = (b * G * G + ty * G + tx) * per_token +
+                                                (inverse ? ((ky * P + kx) * C + c)
+                                                         : ((c * P + ky) * P + kx));
+                            if (inverse) o.set(img, iv.get(tok));
+                            else o.set(tok, iv.get(img));
+                        }
+}
+
+// ---- embeddings (pixart_dit.cpp:32-77, weights.cpp:107-121) ---------------------------------
+
+void sincos_1d(int dim, const std::vector<double>& pos, std::vector<double>* out) {
+    const int half = dim / 2;
+    out->assign(pos.size() * dim, 0.0);
+    std::vector<double> omega(half);
+    for (int i = 0; i < half; ++i) omega[i] = 1.0 / std::pow(10000.0, static_cast<double>(i) / half);
+    for (size_t m = 0; m < pos.size(); ++m)
+        for (int i = 0; i < half; ++i) {
+            const double a = pos[m] * omega[i];
+            (*out)[m * dim + i] = std::sin(a);
+            (*out)[m * dim + half + i] = std::cos(a);
+        }
+}
+
+std::vector<double> position_embedding(int dim, int grid, int base, double interp) {
+    std::vector<double> axis(grid);
+    for (int i = 0; i < grid; ++i)
+        axis[i] = static_cast<double>(i) / (static_cast<double>(grid) / base) / interp;
+    std::vector<double> first(static_cast<size_t>(grid) * grid), second(first.size());
+    for (int r = 0; r < grid; ++r)
+        for (int c = 0; c < grid; ++c) {
+            first[r * grid + c] = axis[c];
+            second[r * grid + c] = axis[r];
+        }
+    std::vector<double> a, b;
+    sincos_1d(dim / 2, first, &a);
+    sincos_1d(dim / 2, second, &b);
+    std::vector<double> out(static_cast<size_t>(grid) * grid * dim);
+    const int half = dim / 2;
+    for (int m = 0; m < grid * grid; ++m) {
+        for (int i = 0; i < half; ++i) out[m * dim + i] = a[m * half + i];
+        for (int i = 0; i < half; ++i) out[m * dim + half + i] = b[m * half + i];
+    }
+    return out;
+}
+
+void timestep_embedding(double t, int dim, float* out) {
+    const int half = dim / 2;
+    for (int i = 0; i < half; ++i) {
+        const double freq = std::exp(-std::log(10000.0) * static_cast<double>(i) / half);
+        const double a = t * freq;
+        out[i] = static_cast<float>(std::cos(a));
+        out[half + i] = static_cast<float>(std::sin(a));
+    }
+}
+
+// ---- the DiT graph (pixart_dit.cpp:112-304) -------------------------------------------------
+
+struct Buf {
+    std::vector<uint16_t> v;
+    explicit Buf(int64_t n = 0) : v(static_cast<size_t>(n), 0) {}
+    void* p() { return v.data(); }
+};
+
+void dit_forward(const bh_dit_config& c, const bh_dit_weights& w, int64_t B, int64_t Hl,
+                 int64_t cap_len, const uint16_t* latent, double t, const uint16_t* caption,
+                 const void* mask, int mask_dt, uint16_t* image, int threads, int layers) {
+    const int BF = BH_BF16;
+    const int64_t P = c.patch_size, grid = Hl / P, N = grid * grid, M = B * N;
+    const int64_t d = static_cast<int64_t>(c.num_heads) * c.head_dim;
+    const int64_t dff = static_cast<int64_t>(static_cast<double>(d) * c.mlp_ratio);
+    const int64_t Mcap = B * cap_len, pin = c.in_channels * P * P, pout = c.out_channels * P * P;
+    const float eps = static_cast<float>(c.eps);
+    auto gemm = [&](const void* a, const void* wt, const void* bias, void* out, int64_t m,
+                    int64_t n, int64_t k, int epi) {
+        gemm_impl(a, wt, bias, out, m, n, k, true, epi, BF, threads);
+    };
+
+    Buf patches(M * pin), x(M * d);
+    patch_impl(latent, patches.p(), B, c.in_channels, grid, P, false, BF);
+    gemm(patches.p(), w.pos_embed_w, w.pos_embed_b, x.p(), M, d, pin, BH_EPI_NONE);
+    {
+        const std::vector<double> pe =
+            position_embedding(static_cast<int>(d), static_cast<int>(grid), c.sample_size / c.patch_size, 2.0);
+        Buf pos(N * d);
+        for (int64_t i = 0; i < N * d; ++i) pos.v[i] = f32_to_bf16(static_cast<float>(pe[i]));
+        add_impl(x.p(), pos.p(), x.p(), B, N * d, 1.0f, true, BF);
+    }
+
+    Buf emb_t(B * d), modulation(B * 6 * d);
+    {
+        float proj[256];
+        timestep_embedding(t, 256, proj);
+        Buf broad(B * 256), h(B * d), s(B * d);
+        for (int64_t b = 0; b < B; ++b)
+            for (int i = 0; i < 256; ++i) broad.v[b * 256 + i] = f32_to_bf16(proj[i]);
+        gemm(broad.p(), w.t_emb1_w, w.t_emb1_b, h.p(), B, d, 256, BH_EPI_SILU);
+        gemm(h.p(), w.t_emb2_w, w.t_emb2_b, emb_t.p(), B, d, d, BH_EPI_NONE);
+        activation_impl(emb_t.p(), s.p(), B * d, BH_EPI_SILU, nullptr, BF);
+        gemm(s.p(), w.adaln_w, w.adaln_b, modulation.p(), B, 6 * d, d, BH_EPI_NONE);
+    }
+    Buf cap(Mcap * d);
+    {
+        Buf h(Mcap * d);
+        gemm(caption, w.cap1_w, w.cap1_b, h.p(), Mcap, d, c.caption_channels, BH_EPI_GELU);
+        gemm(h.p(), w.cap2_w, w.cap2_b, cap.p(), Mcap, d, d, BH_EPI_NONE);
+    }
+
+    Buf normed(M * d), modded(M * d), q(M * d), k(M * d), v(M * d), kc(Mcap * d), vc(Mcap * d),
+        ctx(M * d), proj(M * d), ff0(M * dff), shift(B * d), scale(B * d), gate(B * d), zero(B * d);
+    const AttnGeom self{B, c.num_heads, N, N, c.head_dim, d, d, d};
+    const AttnGeom cross{B, c.num_heads, N, cap_len, c.head_dim, d, d, d};
+    const int nl = layers >= 0 ? std::min(layers, c.num_layers) : c.num_layers;
+    for (int l = 0; l < nl; ++l) {
+        const bh_dit_block_weights& bw = w.blocks[l];
+        const void* table = bw.scale_shift_table;
+        norm_impl(x.p(), nullptr, nullptr, normed.p(), M, d, eps, false, BF, threads);
+        chunk_impl(modulation.p(), table, shift.p(), B, d, 6, 0, 0, BF);
+        chunk_impl(modulation.p(), table, scale.p(), B, d, 6, 1, 1, BF);
+        chunk_impl(modulation.p(), table, gate.p(), B, d, 6, 2, 2, BF);
+        modulate_impl(normed.p(), scale.p(), shift.p(), modded.p(), B, N, d, nullptr, nullptr, BF);
+        gemm(modded.p(), bw.attn1_q_w, bw.attn1_q_b, q.p(), M, d, d, BH_EPI_NONE);
+        gemm(modded.p(), bw.attn1_k_w, bw.attn1_k_b, k.p(), M, d, d, BH_EPI_NONE);
+        gemm(modded.p(), bw.attn1_v_w, bw.attn1_v_b, v.p(), M, d, d, BH_EPI_NONE);
+        attention_impl(q.p(), k.p(), v.p(), ctx.p(), self, 0.0f, nullptr, nullptr, BF, BF, threads,
+                       false);
+        gemm(ctx.p(), bw.attn1_o_w, bw.attn1_o_b, proj.p(), M, d, d, BH_EPI_NONE);
+        modulate_impl(proj.p(), zero.p(), zero.p(), x.p(), B, N, d, x.p(), gate.p(), BF);
+
+        gemm(x.p(), bw.attn2_q_w, bw.attn2_q_b, q.p(), M, d, d, BH_EPI_NONE);
+        gemm(cap.p(), bw.attn2_k_w, bw.attn2_k_b, kc.p(), Mcap, d, d, BH_EPI_NONE);
+        gemm(cap.p(), bw.attn2_v_w, bw.attn2_v_b, vc.p(), Mcap, d, d, BH_EPI_NONE);
+        attention_impl(q.p(), kc.p(), vc.p(), ctx.p(), cross, 0.0f, nullptr, mask, mask_dt, BF,
+                       threads, false);
+        gemm(ctx.p(), bw.attn2_o_w, bw.attn2_o_b, proj.p(), M, d, d, BH_EPI_NONE);
+        add_impl(x.p(), proj.p(), x.p(), M, d, 1.0f, false, BF);
+
+        norm_impl(x.p(), nullptr, nullptr, normed.p(), M, d, eps, false, BF, threads);
+        chunk_impl(modulation.p(), table, shift.p(), B, d, 6, 3, 3, BF);
+        chunk_impl(modulation.p(), table, scale.p(), B, d, 6, 4, 4, BF);
+        chunk_impl(modulation.p(), table, gate.p(), B, d, 6, 5, 5, BF);
+        modulate_impl(normed.p(), scale.p(), shift.p(), modded.p(), B, N, d, nullptr, nullptr, BF);
+        gemm(modded.p(), bw.ff0_w, bw.ff0_b, ff0.p(), M, dff, d, BH_EPI_GELU);
+        gemm(ff0.p(), bw.ff2_w, bw.ff2_b, proj.p(), M, d, dff, BH_EPI_NONE);
+        modulate_impl(proj.p(), zero.p(), zero.p(), x.p(), B, N, d, x.p(), gate.p(), BF);
+    }
+
+    chunk_impl(emb_t.p(), w.out_table, shift.p(), B, d, 1, 0, 0, BF);
+    chunk_impl(emb_t.p(), w.out_table, scale.p(), B, d, 1, 0, 1, BF);
+    norm_impl(x.p(), nullptr, nullptr, normed.p(), M, d, eps, false, BF, threads);
+    modulate_impl(normed.p(), scale.p(), shift.p(), modded.p(), B, N, d, nullptr, nullptr, BF);
+    Buf tokens(M * pout);
+    gemm(modded.p(), w.proj_out_w, w.proj_out_b, tokens.p(), M, pout, d, BH_EPI_NONE);
+    patch_impl(tokens.p(), image, B, c.out_channels, grid, P, true, BF);
+}
+
+thread_local std::string g_err;
+
+template <typename Fn>
+int guard(Fn fn) {
+    try {
+        fn();
+        return 0;
+    } catch (const std::exception& e) {
+        g_err = e.what();
+        return 1;
+    }
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* stock_last_error(void) { return g_err.c_str(); }
+
+int stock_gemm(const void* a, const void* b, const void* bias, void* out, int64_t m, int64_t n,
+               int64_t k, int b_transposed, int epilogue, int dtype, int threads) {
+    return guard([&] {
+        gemm_impl(a, b, bias, out, m, n, k, b_transposed != 0, epilogue, dtype,
+                  resolve_threads(threads));
+    });
+}
+
+int stock_attention(const void* q, const void* k, const void* v, void* out, int64_t batch,
+                    int64_t heads, int64_t q_len, int64_t kv_len, int64_t head_dim, float scale,
+                    const void* bias, const void* key_mask, int mask_dtype, int dtype,
+                    int materialized, int threads) {
+    return guard([&] {
+        const int64_t ld = heads * head_dim;
+        attention_impl(q, k, v, out, AttnGeom{batch, heads, q_len, kv_len, head_dim, ld, ld, ld},
+                       scale, bias, key_mask, mask_dtype, dtype, resolve_threads(threads),
+                       materialized != 0);
+    });
+}
+
+int stock_norm(const void* x, const void* weight, const void* bias, void* out, int64_t rows,
+               int64_t cols, float eps, int rms, int dtype, int threads) {
+    return guard([&] {
+        norm_impl(x, weight, bias, out, rows, cols, eps, rms != 0, dtype, resolve_threads(threads));
+    });
+}
+
+int stock_modulate(const void* x, const void* scale, const void* shift, void* out, int64_t batch,
+                   int64_t tokens, int64_t channels, const void* residual, const void* gate,
+                   int dtype) {
+    return guard([&] {
+        modulate_impl(x, scale, shift, out, batch, tokens, channels, residual, gate, dtype);
+    });
+}
+
+int stock_activation(const void* x, void* out, int64_t n, int kind, const void* gate, int dtype) {
+    return guard([&] { activation_impl(x, out, n, kind, gate, dtype); });
+}
+
+int stock_add(const void* a, const void* b, void* out, int64_t outer, int64_t inner, float scale,
+              int broadcast_b, int dtype) {
+    return guard([&] { add_impl(a, b, out, outer, inner, scale, broadcast_b != 0, dtype); });
+}
+
+int stock_chunk(const void* mod, const void* table, void* out, int64_t batch, int64_t channels,
+                int64_t chunks, int64_t chunk, int64_t table_chunk, int dtype) {
+    return guard([&] { chunk_impl(mod, table, out, batch, channels, chunks, chunk, table_chunk, dtype); });
+}
+
+int stock_patch(const void* in, void* out, int64_t batch, int64_t channels, int64_t grid,
+                int64_t patch, int inverse, int dtype) {
+    return guard([&] { patch_impl(in, out, batch, channels, grid, patch, inverse != 0, dtype); });
+}
+
+int stock_position_embedding(double* out, int dim, int grid, int base, double interp) {
+    return guard([&] {
+        const std::vector<double> pe = position_embedding(dim, grid, base, interp);
+        std::copy(pe.begin(), pe.end(), out);
+    });
+}
+
+int stock_timestep_embedding(double t, int dim, float* out) {
+    return guard([&] {
+        if (dim % 2) throw std::runtime_error("timestep embedding needs an even dimension");
+        timestep_embedding(t, dim, out);
+    });
+}
+
+// `layers` < 0 runs every block; otherwise the first `layers` blocks (the reference's
+// `dit-step --layers`, burnisher_main.cpp:704-707).
+int stock_dit_forward(const bh_dit_config* cfg, const bh_dit_weights* w, int64_t batch,
+                      int64_t latent_hw, int64_t caption_len, const uint16_t* latent,
+                      double timestep, const uint16_t* caption, const void* mask, int mask_dtype,
+                      uint16_t* image, int threads, int layers) {
+    return guard([&] {
+        if (!cfg || !w) throw std::runtime_error("stock_dit_forward: null argument");
+        dit_forward(*cfg, *w, batch, latent_hw, caption_len, latent, timestep, caption, mask,
+                    mask_dtype, image, resolve_threads(threads), layers);
+    });
+}
+
+}  // extern "C"

@@ -1,0 +1,155 @@
+"""The dit-step engine (bh_dit_create / bh_dit_forward) against the stock oracle's dit-step on
+the same seeded weights and inputs, and the reference's graph invariants on the device
+(/root/reference/tests/test_models.cpp:274-348)."""
+import ctypes
+
+import numpy as np
+import pytest
+
+import oracle
+from burnisher_amd.workload import PIXART_SIGMA, config_struct, make_workload
+from helpers import F32, TOLERANCE, addr, from_bf16, stats
+
+pytestmark = pytest.mark.gpu
+
+SMALL = dict(num_layers=2, num_heads=4, head_dim=8, patch_size=2, in_channels=4, out_channels=8,
+             caption_channels=32, sample_size=8, mlp_ratio=4.0, eps=1e-6)
+
+
+class Engine:
+    """A device copy of a workload plus one engine over it."""
+
+    def __init__(self, wl, mode):
+        import torch
+        import burnisher_amd as bh
+        self.wl = wl
+        self.top, self.blocks, self.latent, self.caption, self.mask = wl.to_device()
+        self.cfg = config_struct(wl.cfg)
+        self.w, self._keep = wl.weight_struct(self.top, self.blocks)
+        self.handle = ctypes.c_void_p()
+        bh.call("bh_dit_create", ctypes.byref(self.cfg), ctypes.byref(self.w), wl.batch, wl.latent_hw,
+                wl.caption_len, mode, ctypes.byref(self.handle))
+        self.out = torch.zeros((wl.batch, wl.cfg["out_channels"], wl.latent_hw, wl.latent_hw),
+                               dtype=torch.bfloat16, device="cuda")
+
+    def forward(self, timestep=None, caption=None, mask=None):
+        import torch
+        import burnisher_amd as bh
+        cap = self.caption if caption is None else caption
+        m = self.mask if mask is None else mask
+        t = self.wl.timestep if timestep is None else timestep
+        bh.call("bh_dit_forward", self.handle, self.latent.data_ptr(), t, cap.data_ptr(), m.data_ptr(),
+                F32, self.out.data_ptr(), None)
+        torch.cuda.synchronize()
+        return self.out.cpu().view(torch.int16).numpy().view(np.uint16).copy()
+
+    def close(self):
+        import burnisher_amd as bh
+        if self.handle:
+            bh.lib().bh_dit_destroy(self.handle)
+            self.handle = ctypes.c_void_p()
+
+
+def oracle_forward(wl, layers=-1):
+    cfg = config_struct(wl.cfg)
+    w, keep = wl.weight_struct(wl.top, wl.blocks)
+    out = np.zeros((wl.batch, wl.cfg["out_channels"], wl.latent_hw, wl.latent_hw), np.uint16)
+    oracle.call(oracle.stock(), "stock_dit_forward", ctypes.byref(cfg), ctypes.byref(w), wl.batch,
+                wl.latent_hw, wl.caption_len, addr(wl.latent), wl.timestep, addr(wl.caption),
+                addr(wl.mask), F32, addr(out), 0, layers)
+    return out
+
+
+def check_step(got, want, where):
+    tol = TOLERANCE["dit_step"]
+    s = stats(from_bf16(got), from_bf16(want))
+    print(f"dit-step parity {where}: {s}")
+    assert np.all(np.isfinite(from_bf16(got))), where
+    assert s["max_abs"] <= tol["max_abs"] and s["rel_l2"] <= tol["rel_l2"] and \
+        s["cosine"] >= tol["cosine"], f"{where}: {s} vs {tol}"
+    return s
+
+
+@pytest.mark.parametrize("mode", [0, 1], ids=["fused", "opwise"])
+def test_small_config_matches_oracle(hip, mode):
+    wl = make_workload(SMALL, batch=2, latent_hw=8, caption_len=5)
+    e = Engine(wl, mode)
+    try:
+        got = e.forward()
+        check_step(got, oracle_forward(wl), f"small mode={mode}")
+        assert np.array_equal(got, e.forward()), "not byte-identical across two forwards"
+    finally:
+        e.close()
+
+
+def test_fused_plan_equals_opwise_plan(hip):
+    # Fusion moves no rounding point, so the two plans agree bit for bit.
+    wl = make_workload(PIXART_SIGMA, batch=2, latent_hw=64, caption_len=300, layers=2)
+    a, b = Engine(wl, 0), Engine(wl, 1)
+    try:
+        assert np.array_equal(a.forward(), b.forward())
+    finally:
+        a.close()
+        b.close()
+
+
+def test_two_blocks_512px_matches_oracle(hip):
+    wl = make_workload(PIXART_SIGMA, batch=2, latent_hw=64, caption_len=300, layers=2)
+    e = Engine(wl, 0)
+    try:
+        check_step(e.forward(), oracle_forward(wl), "512px, 2 blocks")
+    finally:
+        e.close()
+
+
+def test_one_block_1024px_matches_oracle(hip):
+    wl = make_workload(PIXART_SIGMA, batch=2, latent_hw=128, caption_len=300, layers=1)
+    e = Engine(wl, 0)
+    try:
+        check_step(e.forward(), oracle_forward(wl), "1024px, 1 block")
+    finally:
+        e.close()
+
+
+def test_full_depth_512px_matches_oracle(hip):
+    wl = make_workload(PIXART_SIGMA, batch=2, latent_hw=64, caption_len=300)
+    e = Engine(wl, 0)
+    try:
+        check_step(e.forward(), oracle_forward(wl), "512px, 28 blocks")
+    finally:
+        e.close()
+
+
+def test_full_depth_1024px_invariants(hip):
+    wl = make_workload(PIXART_SIGMA, batch=2, latent_hw=128, caption_len=300)
+    e = Engine(wl, 0)
+    try:
+        a = e.forward()
+        fa = from_bf16(a)
+        assert np.all(np.isfinite(fa)) and fa.std() > 1e-3
+        assert np.array_equal(a, e.forward())
+        assert np.max(np.abs(fa - from_bf16(e.forward(timestep=100.0)))) > 1e-3
+        # masked caption positions do not reach the output
+        import torch
+        cap = e.caption.clone()
+        for b in range(wl.batch):
+            keep = int(wl.mask[b].sum())
+            cap[b, keep:, :] = 99.0
+        assert np.array_equal(a, e.forward(caption=cap))
+        assert np.max(np.abs(fa - from_bf16(e.forward(mask=torch.ones_like(e.mask))))) > 1e-3
+    finally:
+        e.close()
+
+
+def test_engine_rejects_bad_geometry(hip):
+    import burnisher_amd as bh
+    wl = make_workload(SMALL, batch=2, latent_hw=8, caption_len=5)
+    top, blocks, *_ = wl.to_device()
+    cfg = config_struct(wl.cfg)
+    w, keep = wl.weight_struct(top, blocks)
+    h = ctypes.c_void_p()
+    with pytest.raises(bh.BurnisherError, match="divisible"):
+        bh.call("bh_dit_create", ctypes.byref(cfg), ctypes.byref(w), 2, 9, 5, 0, ctypes.byref(h))
+    w.t_emb1_w = None
+    with pytest.raises(bh.BurnisherError, match="null"):
+        bh.call("bh_dit_create", ctypes.byref(cfg), ctypes.byref(w), 2, 8, 5, 0, ctypes.byref(h))

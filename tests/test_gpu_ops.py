@@ -1,0 +1,340 @@
+"""Each hip-gfx950 op against the stock oracle on identical seeded inputs, through the C ABI.
+
+Modelled on the reference's device-vs-oracle tests (/root/reference/tests/test_cuda_ops.cpp):
+odd small shapes that catch stride and layout slips, the DiT's own shapes, masks that keep
+different key counts per batch row (one keeps a single key), and a byte-identical second call.
+Tolerances are configs/tolerance.json's per-op bf16 gates.
+"""
+import numpy as np
+import pytest
+
+import oracle
+from helpers import (BF16, F32, addr, assert_within, from_bf16, ramp, randn_bf16, stats, to_bf16)
+
+pytestmark = pytest.mark.gpu
+
+RNG = np.random.default_rng(20260911)
+
+
+def dev(a):
+    import torch
+    if a is None:
+        return None
+    if a.dtype == np.uint16:
+        return torch.from_numpy(a.view(np.int16)).view(torch.bfloat16).cuda()
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def host(t, like):
+    import torch
+    torch.cuda.synchronize()
+    if t.dtype == torch.bfloat16:
+        return t.cpu().view(torch.int16).numpy().view(np.uint16).reshape(like.shape)
+    return t.cpu().numpy().reshape(like.shape)
+
+
+def empty(shape, bf16=True):
+    import torch
+    return torch.zeros(shape, dtype=torch.bfloat16 if bf16 else torch.float32, device="cuda")
+
+
+def P(t):
+    return None if t is None else t.data_ptr()
+
+
+def call(name, *args):
+    import burnisher_amd as bh
+    bh.call(name, *args)
+
+
+def st(name, *args):
+    oracle.call(oracle.stock(), name, *args)
+
+
+# ---- gemm ---------------------------------------------------------------------------------
+
+GEMM_SHAPES = [(13, 11, 40), (37, 150, 64), (2, 6912, 1152), (5, 1152, 256), (600, 1152, 4096),
+               (1024, 1152, 1152), (512, 3456, 1152), (512, 4608, 1152), (256, 1152, 4608),
+               (1024, 32, 1152), (2048, 1152, 16), (300, 200, 72)]
+
+
+@pytest.mark.parametrize("shape", GEMM_SHAPES, ids=lambda s: "x".join(map(str, s)))
+@pytest.mark.parametrize("epi", [0, 1, 2])
+def test_gemm_matches_oracle(hip, shape, epi):
+    M, N, K = shape
+    a, b, bias = randn_bf16(RNG, (M, K)), randn_bf16(RNG, (N, K), 0.02), randn_bf16(RNG, (N,), 0.02)
+    want = np.zeros((M, N), np.uint16)
+    st("stock_gemm", addr(a), addr(b), addr(bias), addr(want), M, N, K, 1, epi, BF16, 0)
+    da, db, dbias = dev(a), dev(b), dev(bias)
+    got, again = empty((M, N)), empty((M, N))
+    call("bh_gemm", P(da), P(db), P(dbias), P(got), M, N, K, 1, epi, BF16, None)
+    call("bh_gemm", P(da), P(db), P(dbias), P(again), M, N, K, 1, epi, BF16, None)
+    g = host(got, want)
+    assert_within(from_bf16(g), from_bf16(want), "gemm", f"{shape} epi={epi}")
+    assert np.array_equal(g, host(again, want)), "not byte-identical across two calls"
+
+
+def test_gemm_unaligned_k_and_plain_layouts(hip):
+    # K % 8 != 0, B as [K, N], and fp32: the reference-order kernel, bit-exact with the oracle
+    M, N, K = 9, 7, 13
+    a, b, bias = randn_bf16(RNG, (M, K)), randn_bf16(RNG, (N, K), 0.3), randn_bf16(RNG, (N,), 0.1)
+    for bt in (1, 0):
+        want = np.zeros((M, N), np.uint16)
+        st("stock_gemm", addr(a), addr(b), addr(bias), addr(want), M, N, K, bt, 1, BF16, 1)
+        got = empty((M, N))
+        call("bh_gemm", P(dev(a)), P(dev(b)), P(dev(bias)), P(got), M, N, K, bt, 1, BF16, None)
+        assert np.array_equal(host(got, want), want)
+    af, bf = from_bf16(a), from_bf16(b)
+    want = np.zeros((M, N), np.float32)
+    st("stock_gemm", addr(af), addr(bf), None, addr(want), M, N, K, 1, 0, F32, 1)
+    got = empty((M, N), bf16=False)
+    call("bh_gemm", P(dev(af)), P(dev(bf)), None, P(got), M, N, K, 1, 0, F32, None)
+    assert np.array_equal(host(got, want), want)
+
+
+def test_gemm_fused_epilogues(hip):
+    import burnisher_amd as bh
+    import ctypes
+    B, N_tok, d, K = 2, 300, 1152, 1152
+    M = B * N_tok
+    a, w, bias = randn_bf16(RNG, (M, K)), randn_bf16(RNG, (d, K), 0.02), randn_bf16(RNG, (d,), 0.02)
+    x, gate = randn_bf16(RNG, (M, d)), randn_bf16(RNG, (B, d), 0.5)
+    pos = randn_bf16(RNG, (N_tok, d))
+    zero = np.zeros((B, d), np.uint16)
+    proj = np.zeros((M, d), np.uint16)
+    st("stock_gemm", addr(a), addr(w), addr(bias), addr(proj), M, d, K, 1, 0, BF16, 0)
+    # gated residual: x + gate * proj, through modulate with zero scale/shift (pixart_dit.cpp:249)
+    want = x.copy()
+    st("stock_modulate", addr(proj), addr(zero), addr(zero), addr(want), B, N_tok, d, addr(want), addr(gate), BF16)
+    # residual add (pixart_dit.cpp:268) and broadcast position add (pixart_dit.cpp:149)
+    want_add = x.copy()
+    st("stock_add", addr(want_add), addr(proj), addr(want_add), M, d, 1.0, 0, BF16)
+    want_pos = np.zeros_like(proj)
+    st("stock_add", addr(proj), addr(pos), addr(want_pos), B, N_tok * d, 1.0, 1, BF16)
+
+    dx, dgate, dpos = dev(x), dev(gate), dev(pos)
+    da, dw, db = dev(a), dev(w), dev(bias)
+    f = bh.GemmFused(epilogue=0, round_mid=1, residual=P(dx), gate=P(dgate), gate_rows=N_tok, ld_out=d)
+    call("bh_gemm_fused_run", P(da), P(dw), P(db), P(dx), M, d, K, ctypes.byref(f), None)
+    s1 = assert_within(from_bf16(host(dx, want)), from_bf16(want), "gemm_fused", "gated residual")
+    dx2 = dev(x)
+    f = bh.GemmFused(epilogue=0, round_mid=1, residual=P(dx2), ld_out=d)
+    call("bh_gemm_fused_run", P(da), P(dw), P(db), P(dx2), M, d, K, ctypes.byref(f), None)
+    assert_within(from_bf16(host(dx2, want_add)), from_bf16(want_add), "gemm_fused", "residual add")
+    out = empty((M, d))
+    f = bh.GemmFused(epilogue=0, round_mid=1, row_add=P(dpos), row_add_period=N_tok, ld_out=d)
+    call("bh_gemm_fused_run", P(da), P(dw), P(db), P(out), M, d, K, ctypes.byref(f), None)
+    assert_within(from_bf16(host(out, want_pos)), from_bf16(want_pos), "gemm_fused", "row add")
+    assert s1["mismatch_frac"] < 0.01
+
+
+# ---- attention ----------------------------------------------------------------------------
+
+def attention_case(B, S, KV, H, D, mask=None, scale=0.0, strided=False, inputs=None):
+    if inputs is None:
+        q, k, v = (randn_bf16(RNG, s) for s in ((B, S, H, D), (B, KV, H, D), (B, KV, H, D)))
+    else:
+        q, k, v = inputs
+    want = np.zeros((B, S, H, D), np.uint16)
+    st("stock_attention", addr(q), addr(k), addr(v), addr(want), B, H, S, KV, D, scale, None,
+       addr(mask), F32, BF16, 0, 0)
+    dmask = dev(mask)
+    got, again = empty((B, S, H, D)), empty((B, S, H, D))
+    if strided:
+        import torch
+        d = H * D
+        # Q, K, V as column blocks of one [B*S, 3d] tensor (the fused QKV projection layout)
+        assert S == KV
+        fused = torch.cat([dev(q).reshape(B * S, d), dev(k).reshape(B * S, d), dev(v).reshape(B * S, d)], 1).contiguous()
+        for out in (got, again):
+            call("bh_attention_strided", fused.data_ptr(), 3 * d, fused.data_ptr() + 2 * d,
+                 fused.data_ptr() + 4 * d, 3 * d, P(out), d, B, H, S, KV, D, scale, P(dmask), F32, BF16, None)
+    else:
+        dq, dk, dv = dev(q), dev(k), dev(v)
+        for out in (got, again):
+            call("bh_attention", P(dq), P(dk), P(dv), P(out), B, H, S, KV, D, scale, None, P(dmask),
+                 F32, BF16, None)
+    g = host(got, want)
+    assert np.array_equal(g, host(again, want)), "attention is not byte-identical across two calls"
+    return g, want
+
+
+@pytest.mark.parametrize("case", [
+    (2, 7, 5, 3, 4), (2, 9, 9, 2, 6), (2, 64, 64, 2, 72), (2, 64, 20, 2, 72), (1, 300, 300, 2, 64),
+    (2, 257, 100, 3, 72), (2, 1024, 1024, 16, 72), (2, 1024, 300, 16, 72), (1, 130, 70, 1, 128),
+    (1, 40, 33, 2, 16)], ids=lambda c: "B{}S{}K{}H{}D{}".format(*c))
+def test_attention_matches_oracle(hip, case):
+    B, S, KV, H, D = case
+    mask = None
+    if KV != S:
+        mask = np.zeros((B, KV), np.float32)
+        mask[0, :max(1, KV // 4)] = 1.0
+        if B > 1:
+            mask[1, :1] = 1.0   # one row keeps a single key
+    g, want = attention_case(B, S, KV, H, D, mask=mask)
+    assert_within(from_bf16(g), from_bf16(want), "attention", str(case))
+
+
+def test_attention_masks(hip):
+    B, S, KV, H, D = 2, 128, 300, 4, 72
+    # non-prefix mask, a fully masked 64-key block in the middle, and an all-masked row
+    mask = np.ones((B, KV), np.float32)
+    mask[0, 64:128] = 0.0
+    mask[0, 200:260:3] = 0.0
+    mask[1, :] = 0.0
+    g, want = attention_case(B, S, KV, H, D, mask=mask)
+    assert_within(from_bf16(g), from_bf16(want), "attention", "masks")
+    # the all-masked row is the plain mean of V, not NaN
+    assert np.all(np.isfinite(from_bf16(g)))
+
+
+def test_attention_masked_values_do_not_leak(hip):
+    B, S, KV, H, D = 2, 64, 150, 2, 72
+    q, k, v = (randn_bf16(RNG, s) for s in ((B, S, H, D), (B, KV, H, D), (B, KV, H, D)))
+    mask = np.zeros((B, KV), np.float32)
+    mask[0, :37] = 1.0
+    mask[1, :75] = 1.0
+    g1, _ = attention_case(B, S, KV, H, D, mask=mask, inputs=(q, k, v))
+    v2 = v.copy()
+    v2[0, 37:] = to_bf16(np.float32(1234.0))
+    v2[1, 75:] = to_bf16(np.float32(-77.0))
+    g2, _ = attention_case(B, S, KV, H, D, mask=mask, inputs=(q, k, v2))
+    assert np.array_equal(g1, g2)
+
+
+def test_attention_strided_qkv(hip):
+    g, want = attention_case(2, 512, 512, 16, 72, strided=True)
+    assert_within(from_bf16(g), from_bf16(want), "attention", "strided")
+
+
+def test_attention_reference_order_path(hip):
+    # fp32, and an additive bias: the reference-order kernel
+    B, S, KV, H, D = 2, 7, 5, 3, 4
+    q, k, v = ramp((B, S, H, D), 0.31), ramp((B, KV, H, D), 0.17), ramp((B, KV, H, D), 0.53)
+    bias = ramp((H, S, KV), 0.07)
+    mask = np.array([[1, 1, 1, 0, 0], [1, 0, 0, 0, 0]], np.float32)
+    want = np.zeros((B, S, H, D), np.float32)
+    st("stock_attention", addr(q), addr(k), addr(v), addr(want), B, H, S, KV, D, 1.0, addr(bias),
+       addr(mask), F32, F32, 0, 1)
+    got = empty((B, S, H, D), bf16=False)
+    call("bh_attention", P(dev(q)), P(dev(k)), P(dev(v)), P(got), B, H, S, KV, D, 1.0, P(dev(bias)),
+         P(dev(mask)), F32, F32, None)
+    # reference tolerance for fp32 device kernels (test_cuda_ops.cpp:50)
+    assert np.max(np.abs(host(got, want) - want)) < 2e-5
+
+
+# ---- norm and the fused norm + modulate ---------------------------------------------------
+
+@pytest.mark.parametrize("rows,cols", [(37, 1152), (8, 100), (3, 4608), (1, 8)])
+def test_norm_matches_oracle(hip, rows, cols):
+    x = randn_bf16(RNG, (rows, cols), 2.0)
+    x[0, :] = to_bf16(np.float32(3.0) + ramp((cols,), 0.01))  # a nearly constant row
+    for rms in (0, 1):
+        want = np.zeros_like(x)
+        st("stock_norm", addr(x), None, None, addr(want), rows, cols, 1e-6, rms, BF16, 1)
+        got = empty((rows, cols))
+        call("bh_norm", P(dev(x)), None, None, P(got), rows, cols, 1e-6, rms, 0, 0, BF16, None)
+        s = assert_within(from_bf16(host(got, want)), from_bf16(want), "norm", f"{rows}x{cols} rms={rms}")
+        assert s["mismatch_frac"] <= 1e-4, s
+
+
+def test_norm_affine_and_groupnorm_refused(hip):
+    import burnisher_amd as bh
+    rows, cols = 5, 64
+    x, w, b = randn_bf16(RNG, (rows, cols)), randn_bf16(RNG, (cols,)), randn_bf16(RNG, (cols,))
+    want = np.zeros_like(x)
+    st("stock_norm", addr(x), addr(w), addr(b), addr(want), rows, cols, 1e-6, 0, BF16, 1)
+    got = empty((rows, cols))
+    call("bh_norm", P(dev(x)), P(dev(w)), P(dev(b)), P(got), rows, cols, 1e-6, 0, 0, 0, BF16, None)
+    assert np.array_equal(host(got, want), want)
+    with pytest.raises(bh.BurnisherError, match="GroupNorm"):
+        call("bh_norm", P(dev(x)), None, None, P(got), 1, rows * cols, 1e-6, 0, 4, 4, BF16, None)
+
+
+@pytest.mark.parametrize("tokens", [1024, 77])
+def test_norm_modulate_matches_oracle_sequence(hip, tokens):
+    B, C = 2, 1152
+    x = randn_bf16(RNG, (B * tokens, C), 1.5)
+    mod, table = randn_bf16(RNG, (B, 6 * C), 0.5), randn_bf16(RNG, (6, C), 0.5)
+    normed, shift, scale, want = (np.zeros(s, np.uint16) for s in ((B * tokens, C), (B, C), (B, C), (B * tokens, C)))
+    # the reference block's op sequence, pixart_dit.cpp:226-231 (chunks 3/4: the MLP half)
+    st("stock_norm", addr(x), None, None, addr(normed), B * tokens, C, 1e-6, 0, BF16, 0)
+    st("stock_chunk", addr(mod), addr(table), addr(shift), B, C, 6, 3, 3, BF16)
+    st("stock_chunk", addr(mod), addr(table), addr(scale), B, C, 6, 4, 4, BF16)
+    st("stock_modulate", addr(normed), addr(scale), addr(shift), addr(want), B, tokens, C, None, None, BF16)
+    got = empty((B * tokens, C))
+    call("bh_norm_modulate", P(dev(x)), P(dev(mod)), 6, 3, 4, P(dev(table)), 3, 4, P(got), B, tokens, C,
+         1e-6, None)
+    s = assert_within(from_bf16(host(got, want)), from_bf16(want), "norm_modulate", str(tokens))
+    assert s["mismatch_frac"] <= 1e-4, s
+
+
+# ---- elementwise --------------------------------------------------------------------------
+
+@pytest.mark.parametrize("C", [1152, 12])
+def test_modulate_matches_oracle(hip, C):
+    B, T = 2, 33
+    x, res = randn_bf16(RNG, (B, T, C)), randn_bf16(RNG, (B, T, C))
+    sc, sh, gt = (randn_bf16(RNG, (B, C), 0.3) for _ in range(3))
+    for r, g in ((None, None), (res, gt)):
+        want = np.zeros_like(x)
+        st("stock_modulate", addr(x), addr(sc), addr(sh), addr(want), B, T, C, addr(r), addr(g), BF16)
+        got = empty((B, T, C))
+        call("bh_modulate", P(dev(x)), P(dev(sc)), P(dev(sh)), P(got), B, T, C, P(dev(r)), P(dev(g)), BF16, None)
+        assert np.array_equal(host(got, want), want)
+    # in place on the residual, as the graph calls it (pixart_dit.cpp:249)
+    zero = np.zeros((B, C), np.uint16)
+    want = res.copy()
+    st("stock_modulate", addr(x), addr(zero), addr(zero), addr(want), B, T, C, addr(want), addr(gt), BF16)
+    dres = dev(res)
+    call("bh_modulate", P(dev(x)), P(dev(zero)), P(dev(zero)), P(dres), B, T, C, P(dres), P(dev(gt)), BF16, None)
+    assert np.array_equal(host(dres, want), want)
+
+
+def test_add_chunk_activation_patch(hip):
+    B, T, C = 2, 40, 1152
+    a, b, row = randn_bf16(RNG, (B, T * C)), randn_bf16(RNG, (B, T * C)), randn_bf16(RNG, (T * C,))
+    for bb, bc in ((b, 0), (row, 1)):
+        want = np.zeros_like(a)
+        st("stock_add", addr(a), addr(bb), addr(want), B, T * C, 1.0, bc, BF16)
+        got = empty((B, T * C))
+        call("bh_add", P(dev(a)), P(dev(bb)), P(got), B, T * C, 1.0, bc, BF16, None)
+        assert np.array_equal(host(got, want), want)
+    mod, table, emb, out_table = (randn_bf16(RNG, s) for s in ((B, 6 * C), (6, C), (B, C), (2, C)))
+    for m, t, chunks, chunk, trow in ((mod, table, 6, 2, 2), (mod, table, 6, 5, -1), (emb, out_table, 1, 0, 1)):
+        want = np.zeros((B, C), np.uint16)
+        st("stock_chunk", addr(m), addr(t), addr(want), B, C, chunks, chunk, trow, BF16)
+        got = empty((B, C))
+        call("bh_chunk", P(dev(m)), P(dev(t)), P(got), B, C, chunks, chunk, trow, BF16, None)
+        assert np.array_equal(host(got, want), want)
+    x = randn_bf16(RNG, (B, C), 3.0)
+    for kind in (1, 2):
+        want = np.zeros_like(x)
+        st("stock_activation", addr(x), addr(want), x.size, kind, None, BF16)
+        got = empty((B, C))
+        call("bh_activation", P(dev(x)), P(got), x.size, kind, None, BF16, None)
+        assert_within(from_bf16(host(got, want)), from_bf16(want), "activation", f"kind={kind}")
+    img = randn_bf16(RNG, (2, 4, 32, 32))
+    want = np.zeros((2, 256, 16), np.uint16)
+    st("stock_patch", addr(img), addr(want), 2, 4, 16, 2, 0, BF16)
+    got = empty((2, 256, 16))
+    call("bh_patch", P(dev(img)), P(got), 2, 4, 16, 2, 0, BF16, None)
+    assert np.array_equal(host(got, want), want)
+    tok = randn_bf16(RNG, (2, 256, 32))
+    want = np.zeros((2, 8, 32, 32), np.uint16)
+    st("stock_patch", addr(tok), addr(want), 2, 8, 16, 2, 1, BF16)
+    got = empty((2, 8, 32, 32))
+    call("bh_patch", P(dev(tok)), P(got), 2, 8, 16, 2, 1, BF16, None)
+    assert np.array_equal(host(got, want), want)
+
+
+def test_contract_errors(hip):
+    import burnisher_amd as bh
+    host_a = np.zeros((4, 8), np.uint16)
+    d = empty((4, 8))
+    with pytest.raises(bh.BurnisherError, match="HOST pointer|not memory"):
+        call("bh_gemm", host_a.ctypes.data, P(d), None, P(d), 4, 4, 8, 1, 0, BF16, None)
+    with pytest.raises(bh.BurnisherError, match="GeluGated"):
+        call("bh_gemm", P(d), P(d), None, P(d), 4, 4, 8, 1, 3, BF16, None)
+    with pytest.raises(bh.BurnisherError, match="dtype"):
+        call("bh_add", P(d), P(d), P(d), 4, 8, 1.0, 0, 7, None)
