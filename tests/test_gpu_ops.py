@@ -16,18 +16,28 @@ pytestmark = pytest.mark.gpu
 RNG = np.random.default_rng(20260911)
 
 
+# Device copies made inline as call arguments (`P(dev(x))`) would be freed -- and their memory
+# handed to the next copy by the caching allocator -- before the asynchronous kernel reads them.
+# They are kept here until the next synchronising read-back.
+_LIVE = []
+
+
 def dev(a):
     import torch
     if a is None:
         return None
     if a.dtype == np.uint16:
-        return torch.from_numpy(a.view(np.int16)).view(torch.bfloat16).cuda()
-    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+        t = torch.from_numpy(a.view(np.int16)).view(torch.bfloat16).cuda()
+    else:
+        t = torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    _LIVE.append(t)
+    return t
 
 
 def host(t, like):
     import torch
     torch.cuda.synchronize()
+    _LIVE.clear()
     if t.dtype == torch.bfloat16:
         return t.cpu().view(torch.int16).numpy().view(np.uint16).reshape(like.shape)
     return t.cpu().numpy().reshape(like.shape)
