@@ -1,23 +1,29 @@
 // bf16 GEMM for the dit-step on gfx950: out[M,N] = A[M,K] . B[N,K]^T (+bias, activation,
 // fused residual), fp32 accumulation on the MFMA cores.
 //
-// Tile: 256 (M) x 144 (N) x 64 (K) per 256-thread workgroup; wave w owns rows [64w, 64w+64)
-// and all 144 columns as a 4 x 9 grid of 16x16 accumulators (v_mfma_f32_16x16x32_bf16).
-// 144 divides every DiT output width (1152, 3456, 4608) and 256 divides M = 2*4096, so the
-// 8192-row GEMMs launch exactly 256, 768 and 1024 tiles: whole waves on 256 CUs, where the
-// usual 256x128 tile would leave the last wave of N=1152 one-eighth full.
+// Tile: 256 (M) x 144 (N) x 64 (K) per 256-thread workgroup; wave w owns rows [64w, 64w+64) and
+// all 144 columns as a 4 x 9 grid of 16x16 accumulators (v_mfma_f32_16x16x32_bf16). 144 divides
+// every DiT output width (1152, 3456, 4608, 28*2304) and 256 divides M = 2*4096, so the
+// 8192-row GEMMs launch exactly 256, 768 and 1024 tiles: whole waves on 256 CUs, where the usual
+// 256x128 tile would leave the last wave of N=1152 one-eighth full.
 //
-// The MFMA is issued with the weight tile as its first operand, so the accumulator layout puts
-// four consecutive OUTPUT COLUMNS of one row in each lane: the epilogue reads bias, residual and
-// gate and writes the result with 8-byte accesses.
+// Operand staging: direct global->LDS loads (global_load_lds_dwordx4: each wave instruction
+// writes 1 KiB = eight 128-byte LDS rows without passing through VGPRs) into THREE LDS stages of
+// 50 KiB, so k-tiles are fetched up to three ahead of the one being multiplied (see k_gemm_tn).
 //
-// Operands are staged through LDS, double-buffered: while the waves multiply tile k out of one
-// buffer, the next tile's global loads are in flight in registers and land in the other buffer
-// after the multiply. Each LDS row is padded from 128 to 144 bytes so the 16-byte fragment reads
-// of 8 consecutive rows hit disjoint banks.
+// LDS rows are 128 bytes (64 bf16 of K) with the 16-byte chunk c of row r stored at slot
+// c ^ ((r >> 1) & 7): the 16 rows one ds_read_b128 fragment touches then cover all 64 banks
+// exactly once, with no padding (padding would break the 1 KiB contiguity of a DMA write).
 //
-// Tile order is XCD-aware: workgroup i runs on XCD i%8, so tiles are renumbered so that each
-// XCD gets a contiguous band of 4 M-tiles x all N-tiles, whose A and B panels fit its 4 MB L2.
+// The MFMA is issued with the weight fragment as its first operand, so the accumulator layout
+// puts four consecutive OUTPUT COLUMNS of one row in each lane: the epilogue reads bias,
+// residual and gate and writes the result with 8-byte accesses. Epilogues are template
+// specialisations, so each instantiation is straight-line code and the accumulators stay in
+// registers.
+//
+// Tile order is XCD-aware: workgroup i runs on XCD i%8, so tiles are renumbered so that each XCD
+// gets a contiguous band of M-tiles x N-tiles, walked 4 M-tiles at a time, whose A and B panels
+// share that XCD's L2.
 //
 // Summation order inside an MFMA differs from the reference oracle's sequential loop
 // (ops_cpu.cpp:60-66); products of bf16 are exact in fp32, so results differ only by fp32
@@ -28,14 +34,22 @@ namespace bh {
 namespace {
 
 constexpr int BM = 256, BN = 144, BK = 64;
-constexpr int kThreads = 256;
-constexpr int kLdsRow = BK + 8;                      // bf16 per LDS row: 144 bytes
-constexpr int kAElems = BM * kLdsRow;
-constexpr int kBElems = BN * kLdsRow;
-constexpr int kStage = kAElems + kBElems;            // 57,600 bytes per stage
-constexpr int kAChunks = BM * (BK / 8) / kThreads;   // 8 16-byte chunks per thread
-constexpr int kBChunks = (BN * (BK / 8) + kThreads - 1) / kThreads;  // 5 (last partial)
-constexpr int kMT = 4, kNT = 9;                      // 16x16 tiles per wave
+constexpr int kRowBytes = BK * 2;                 // 128
+constexpr int kABytes = BM * kRowBytes;           // 32 KiB
+constexpr int kBBytes = BN * kRowBytes;           // 18 KiB
+// Each stage also has one spare 1 KiB row block: waves 2-3 have one B row block fewer than waves
+// 0-1 and load a duplicate into it, so every wave issues the same 13 DMA instructions per k-tile
+// and the loop body has no per-wave branch.
+constexpr int kStageBytes = kABytes + kBBytes + 1024;   // 51 KiB
+constexpr int kMT = 4, kNT = 9;                   // 16x16 tiles per wave
+
+// Epilogue modes. v = act(acc + bias), then:
+enum EpiMode {
+    EPI_STORE = 0,     // out = v
+    EPI_ROW_ADD = 1,   // out = v' + row_add[row % period, n]
+    EPI_RESIDUAL = 2,  // out = residual[row, n] + v'
+    EPI_GATED = 3,     // out = residual[row, n] + gate[row / gate_rows, n] * v'
+};                     // v' = round_mid ? bf16(v) : v
 
 struct Epi {
     const bf16_t* bias;
@@ -49,6 +63,9 @@ struct Epi {
     int64_t ld_out;
 };
 
+// ---- activations ------------------------------------------------------------------------------
+
+// Exact forms, the oracle's expressions operation for operation (ops_cpu.cpp:27-36).
 __device__ __forceinline__ float gelu_tanh(float x) {
     const float c = 0.7978845608028654f;
     const float x3 = __fmul_rn(__fmul_rn(x, x), x);
@@ -57,11 +74,28 @@ __device__ __forceinline__ float gelu_tanh(float x) {
 }
 __device__ __forceinline__ float silu(float x) { return __fdiv_rn(x, __fadd_rn(1.0f, expf(-x))); }
 
-// acc (+ bias already added) -> activation -> optional mid rounding -> row add -> residual.
-__device__ __forceinline__ float epi_value(float v, int act, bool round_mid) {
-    if (act == 1) v = gelu_tanh(v);
-    else if (act == 2) v = silu(v);
-    if (round_mid) v = round_bf16(v);
+// The MFMA epilogue's GELU: 0.5 x (1 + tanh u) = x / (1 + exp(-2u)), with the hardware exp2 and
+// reciprocal. Its fp32 error (a few ulp) is far below the bf16 ulp it is rounded to, so it moves a
+// stored value by at most one bf16 ulp, the same bound the summation order already takes.
+__device__ __forceinline__ float gelu_tanh_fast(float x) {
+    const float u = 0.7978845608028654f * (x + 0.044715f * x * x * x);
+    const float e = __builtin_amdgcn_exp2f(-2.8853900817779268f * u);   // exp(-2u)
+    return x * __builtin_amdgcn_rcpf(1.0f + e);
+}
+__device__ __forceinline__ float silu_fast(float x) {
+    const float e = __builtin_amdgcn_exp2f(-1.4426950408889634f * x);   // exp(-x)
+    return x * __builtin_amdgcn_rcpf(1.0f + e);
+}
+
+template <int ACT>
+__device__ __forceinline__ float act_fast(float v) {
+    if (ACT == 1) return gelu_tanh_fast(v);
+    if (ACT == 2) return silu_fast(v);
+    return v;
+}
+__device__ __forceinline__ float act_exact(int act, float v) {
+    if (act == 1) return gelu_tanh(v);
+    if (act == 2) return silu(v);
     return v;
 }
 
@@ -78,63 +112,201 @@ __device__ __forceinline__ uint2 pack4(const float (&f)[4]) {
     return r;
 }
 
-// Four consecutive columns [n, n+4) of row m. `vec` means all four are in range and every
-// operand is 8-byte aligned there.
-__device__ __forceinline__ void store_quad(const Epi& e, bf16_t* out, int64_t m, int64_t n,
-                                           int64_t N, const float (&acc)[4], bool vec) {
-    if (vec) {
-        float v[4], t[4];
-        if (e.bias) {
-            unpack4(*reinterpret_cast<const uint2*>(e.bias + n), t);
-#pragma unroll
-            for (int r = 0; r < 4; ++r) v[r] = __fadd_rn(acc[r], t[r]);
-        } else {
-#pragma unroll
-            for (int r = 0; r < 4; ++r) v[r] = acc[r];
-        }
-#pragma unroll
-        for (int r = 0; r < 4; ++r) v[r] = epi_value(v[r], e.act, e.round_mid);
-        if (e.row_add) {
-            unpack4(*reinterpret_cast<const uint2*>(e.row_add + (m % e.row_add_period) * N + n), t);
-#pragma unroll
-            for (int r = 0; r < 4; ++r) v[r] = __fadd_rn(v[r], t[r]);
-        }
-        if (e.residual) {
-            float res[4];
-            unpack4(*reinterpret_cast<const uint2*>(e.residual + m * e.ld_out + n), res);
-            if (e.gate) {
-                unpack4(*reinterpret_cast<const uint2*>(e.gate + (m / e.gate_rows) * N + n), t);
-#pragma unroll
-                for (int r = 0; r < 4; ++r) v[r] = __fadd_rn(__fmul_rn(v[r], t[r]), res[r]);
-            } else {
-#pragma unroll
-                for (int r = 0; r < 4; ++r) v[r] = __fadd_rn(res[r], v[r]);
-            }
-        }
-        *reinterpret_cast<uint2*>(out + m * e.ld_out + n) = pack4(v);
-        return;
+// One output element after the activation, any mode (the scalar tail and the small kernels).
+__device__ __forceinline__ float finish(const Epi& e, int mode, float v, int64_t m, int64_t c,
+                                        int64_t N) {
+    if (mode != EPI_STORE && e.round_mid) v = round_bf16(v);
+    if (mode == EPI_ROW_ADD) v = __fadd_rn(v, bf2f(e.row_add[(m % e.row_add_period) * N + c]));
+    if (mode == EPI_RESIDUAL) v = __fadd_rn(bf2f(e.residual[m * e.ld_out + c]), v);
+    if (mode == EPI_GATED) {
+        v = __fadd_rn(__fmul_rn(v, bf2f(e.gate[(m / e.gate_rows) * N + c])),
+                      bf2f(e.residual[m * e.ld_out + c]));
     }
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        const int64_t c = n + r;
-        if (c >= N) break;
-        float v = acc[r];
-        if (e.bias) v = __fadd_rn(v, bf2f(e.bias[c]));
-        v = epi_value(v, e.act, e.round_mid);
-        if (e.row_add) v = __fadd_rn(v, bf2f(e.row_add[(m % e.row_add_period) * N + c]));
-        if (e.residual) {
-            const float res = bf2f(e.residual[m * e.ld_out + c]);
-            if (e.gate) v = __fadd_rn(__fmul_rn(v, bf2f(e.gate[(m / e.gate_rows) * N + c])), res);
-            else v = __fadd_rn(res, v);
-        }
-        out[m * e.ld_out + c] = f2bf(v);
-    }
+    return v;
 }
 
-__global__ void __launch_bounds__(kThreads, 1)
-k_gemm_mfma(const bf16_t* __restrict__ A, const bf16_t* __restrict__ B, bf16_t* out, int64_t M,
-            int64_t N, int64_t K, Epi e, int tiles_m, int tiles_n, int group_m, bool vec_epi) {
-    __shared__ __attribute__((aligned(16))) bf16_t smem[2 * kStage];
+// Four consecutive columns, all in range and 8-byte aligned.
+template <int ACT, int MODE>
+__device__ __forceinline__ void store_quad(const Epi& e, bf16_t* out, int64_t m, int64_t n,
+                                           int64_t N, const f32x4_t& acc) {
+    float v[4], t[4];
+    if (e.bias) {
+        unpack4(*reinterpret_cast<const uint2*>(e.bias + n), t);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) v[r] = __fadd_rn(acc[r], t[r]);
+    } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) v[r] = acc[r];
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) v[r] = act_fast<ACT>(v[r]);
+    if (MODE != EPI_STORE && e.round_mid) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) v[r] = round_bf16(v[r]);
+    }
+    if (MODE == EPI_ROW_ADD) {
+        unpack4(*reinterpret_cast<const uint2*>(e.row_add + (m % e.row_add_period) * N + n), t);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) v[r] = __fadd_rn(v[r], t[r]);
+    }
+    if (MODE == EPI_RESIDUAL || MODE == EPI_GATED) {
+        float res[4];
+        unpack4(*reinterpret_cast<const uint2*>(e.residual + m * e.ld_out + n), res);
+        if (MODE == EPI_GATED) {
+            unpack4(*reinterpret_cast<const uint2*>(e.gate + (m / e.gate_rows) * N + n), t);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) v[r] = __fadd_rn(__fmul_rn(v[r], t[r]), res[r]);
+        } else {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) v[r] = __fadd_rn(res[r], v[r]);
+        }
+    }
+    *reinterpret_cast<uint2*>(out + m * e.ld_out + n) = pack4(v);
+}
+
+// ---- the MFMA tile kernel ----------------------------------------------------------------------
+
+// Wait until at most N vector-memory operations of this wave are outstanding and every LDS
+// operation has completed.
+template <int N>
+__device__ __forceinline__ void wait_vm_lgkm0() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" : : "n"(N) : "memory");
+}
+
+// One global_load_lds_dwordx4: lane L's 16 bytes at `src` land at LDS address lds + 16 L, where
+// `lds` is wave-uniform. Issued as inline assembly so that the compiler does not track these LDS
+// writes: its own tracking of them is conservative at the loop header (it waits for every
+// outstanding load before the first LDS read), which would drain the pipeline each round. The
+// explicit waits in wait_and_join() cover them instead. M0 carries the LDS address; nothing else in
+// these kernels uses M0.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma16(const void* src, const char* lds) {
+    const uint32_t l = static_cast<uint32_t>(
+        reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const char*)(lds)));
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
+                 :
+                 : "s"(l), "v"(src)
+                 : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+struct TileArgs {
+    const bf16_t* A;
+    const bf16_t* B;
+    int64_t M, N, K;
+    int64_t m0, n0;
+    int wave, lane;
+};
+
+// DMA item r (0..12) of dma_tile(): r < 8 is A row block 4r + wave, r >= 8 is B row block
+// 4(r-8) + wave, or for the one that does not exist (waves 2-3, r = 12) a duplicate of the last B
+// row block into the stage's spare block.
+__device__ __forceinline__ void dma_item(char* stage, const TileArgs& t, int64_t k0, int r) {
+    const int sub = t.lane >> 3, slot = t.lane & 7;
+    if (r < BM / 32) {
+        const int rb = r * 4 + t.wave;
+        const int row_in = rb * 8 + sub;
+        const int c = slot ^ ((row_in >> 1) & 7);
+        const int64_t row = min(t.m0 + row_in, t.M - 1);
+        dma16(t.A + row * t.K + k0 + c * 8, stage + rb * 1024);
+    } else {
+        const int rb = (r - BM / 32) * 4 + t.wave;
+        const int row_in = min(rb, BN / 8 - 1) * 8 + sub;
+        const int c = slot ^ ((row_in >> 1) & 7);
+        const int64_t row = min(t.n0 + row_in, t.N - 1);
+        // rb == 18 (waves 2-3, last item) lands in the spare block
+        dma16(t.B + row * t.K + k0 + c * 8, stage + kABytes + min(rb, BN / 8) * 1024);
+    }
+}
+constexpr int kDmaItems = BM / 32 + (BN / 8 + 3) / 4;   // 13
+
+// The whole k-tile `k0` into one stage: 13 DMA instructions per wave. Rows past M or N re-read
+// the last valid row; their results are never stored.
+__device__ __forceinline__ void dma_tile(char* stage, const TileArgs& t, int64_t k0) {
+#pragma unroll
+    for (int r = 0; r < kDmaItems; ++r) dma_item(stage, t, k0, r);
+}
+
+// One k-tile of MFMAs for a consumer wave out of `cur`: 4 activation fragments per K=32 half
+// (rows 64w + 16i + lane%16) and 9 weight fragments (rows 16j + lane%16), 72 MFMAs. The second
+// half's weight fragment j is read into the registers of the first half's, right after the four
+// MFMAs that consume it, so only 17 fragments (68 VGPRs) are live: two waves per SIMD fit in the
+// register file with the 144 accumulators. `off0`/`off1` are this lane's byte offsets of its
+// chunk within a 16-row block for the two halves (row lane%16, chunk 4*half + lane/16, swizzled).
+__device__ __forceinline__ bf16x8_t frag(const char* p) { return *reinterpret_cast<const bf16x8_t*>(p); }
+
+__device__ __forceinline__ void consume_tile(f32x4_t (&acc)[kMT][kNT], const char* cur, int wave,
+                                             int off0, int off1) {
+    const char* a_rows = cur + wave * 64 * kRowBytes;
+    const char* b_rows = cur + kABytes;
+    bf16x8_t a0[kMT], a1[kMT], b[kNT];
+#pragma unroll
+    for (int i = 0; i < kMT; ++i) a0[i] = frag(a_rows + i * 16 * kRowBytes + off0);
+#pragma unroll
+    for (int j = 0; j < kNT; ++j) b[j] = frag(b_rows + j * 16 * kRowBytes + off0);
+#pragma unroll
+    for (int i = 0; i < kMT; ++i) a1[i] = frag(a_rows + i * 16 * kRowBytes + off1);
+#pragma unroll
+    for (int j = 0; j < kNT; ++j) {
+#pragma unroll
+        for (int i = 0; i < kMT; ++i)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(b[j], a0[i], acc[i][j], 0, 0, 0);
+        b[j] = frag(b_rows + j * 16 * kRowBytes + off1);
+    }
+#pragma unroll
+    for (int j = 0; j < kNT; ++j)
+#pragma unroll
+        for (int i = 0; i < kMT; ++i)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(b[j], a1[i], acc[i][j], 0, 0, 0);
+    // Keep that order: all 17 first reads up front, each second-half weight read right after its
+    // register's last use, then the second half. Left alone, the scheduler sinks every read next
+    // to its first use and exposes the LDS latency before each group of four MFMAs.
+    __builtin_amdgcn_sched_group_barrier(0x100, 2 * kMT + kNT, 0);
+#pragma unroll
+    for (int j = 0; j < kNT; ++j) {
+        __builtin_amdgcn_sched_group_barrier(0x008, kMT, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, kMT * kNT, 0);
+}
+
+// Waits until this wave has at most N DMA operations outstanding and none of its LDS reads, then
+// joins the workgroup. The empty asm statements are compiler-level memory barriers: no LDS read
+// or DMA may be moved across the wait and the hardware barrier.
+template <int N>
+__device__ __forceinline__ void wait_and_join() {
+    asm volatile("" ::: "memory");
+    wait_vm_lgkm0<N>();
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+// The kernel is warp-specialised: waves 0-3 are consumers (LDS fragment reads and MFMAs, one
+// per SIMD), waves 4-7 producers (the DMA). A wave issues in order and a DMA instruction holds
+// its wave until the address unit accepts it; in a single-role wave that stall delays the
+// wave's MFMAs, here it only delays the producer, and the consumer on the same SIMD keeps the
+// matrix core busy.
+//
+// Per k-tile kt (stage kt % 3), every wave:
+//   producers: wait until tile kt has landed (tile kt+1 may still be in flight)
+//   consumers: wait until their LDS reads of the previous stage are done
+//   barrier
+//   producers: DMA tile kt+2 -> stage (kt+2) % 3 (it held tile kt-1, which every consumer
+//              finished reading before the barrier)
+//   consumers: multiply stage kt % 3
+// so two k-tiles are in flight behind the one being multiplied. The last two steps load a copy
+// of the last k-tile into the stage nobody will read again, which keeps every step's wait count
+// identical.
+constexpr int kConsumers = 4;
+constexpr int kWgThreads = 2 * kConsumers * 64;   // 512
+
+template <int ACT, int MODE>
+__global__ void __launch_bounds__(kWgThreads, 1)
+k_gemm_tn(const bf16_t* __restrict__ A, const bf16_t* __restrict__ B, bf16_t* out, int64_t M,
+          int64_t N, int64_t K, Epi e, int tiles_m, int tiles_n, int group_m) {
+    __shared__ __attribute__((aligned(1024))) char smem[3 * kStageBytes];
 
     // ---- tile selection: XCD-contiguous bands, grouped by `group_m` M-tiles ----
     const int T = tiles_m * tiles_n;
@@ -147,48 +319,42 @@ k_gemm_mfma(const bf16_t* __restrict__ A, const bf16_t* __restrict__ B, bf16_t* 
     const int in_group = bid - g * group_size;
     const int tm = first_m + in_group % gm;
     const int tn = in_group / gm;
-    const int64_t m0 = static_cast<int64_t>(tm) * BM;
-    const int64_t n0 = static_cast<int64_t>(tn) * BN;
 
-    const int tid = threadIdx.x;
-    const int wave = tid >> 6;
-    const int lane = tid & 63;
-    const int kc = tid & 7;          // 16-byte chunk within a 64-wide K slab
-    const int r0 = tid >> 3;         // first row this thread stages
+    // The wave index through readfirstlane: the compiler then knows it is uniform, so the role
+    // branch and the DMA's LDS address are scalar.
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int KT = static_cast<int>(K / BK);
 
-    uint4 ra[kAChunks], rb[kBChunks];
-    const int KT = static_cast<int>((K + BK - 1) / BK);
+    if (wave >= kConsumers) {
+        // ---- producer ----
+        TileArgs t;
+        t.A = A;
+        t.B = B;
+        t.M = M;
+        t.N = N;
+        t.K = K;
+        t.m0 = static_cast<int64_t>(tm) * BM;
+        t.n0 = static_cast<int64_t>(tn) * BN;
+        t.wave = wave - kConsumers;
+        t.lane = lane;
+        dma_tile(smem, t, 0);
+        dma_tile(smem + kStageBytes, t, static_cast<int64_t>(min(1, KT - 1)) * BK);
+        int stage = 0;
+        for (int kt = 0; kt < KT; ++kt) {
+            wait_and_join<kDmaItems>();
+            const int s2 = stage == 0 ? 2 : stage - 1;   // (kt + 2) % 3
+            dma_tile(smem + s2 * kStageBytes, t, static_cast<int64_t>(min(kt + 2, KT - 1)) * BK);
+            stage = stage == 2 ? 0 : stage + 1;
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // the two trailing copies
+        return;
+    }
 
-    auto load_tile = [&](int kt) {
-        const int64_t k = static_cast<int64_t>(kt) * BK + kc * 8;
-        const bool kin = k < K;
-#pragma unroll
-        for (int i = 0; i < kAChunks; ++i) {
-            const int64_t row = m0 + r0 + 32 * i;
-            ra[i] = (kin && row < M) ? *reinterpret_cast<const uint4*>(A + row * K + k)
-                                     : make_uint4(0, 0, 0, 0);
-        }
-#pragma unroll
-        for (int i = 0; i < kBChunks; ++i) {
-            const int lr = r0 + 32 * i;
-            const int64_t row = n0 + lr;
-            rb[i] = (lr < BN && kin && row < N) ? *reinterpret_cast<const uint4*>(B + row * K + k)
-                                                 : make_uint4(0, 0, 0, 0);
-        }
-    };
-    auto store_tile = [&](int stage) {
-        bf16_t* As = smem + stage * kStage;
-        bf16_t* Bs = As + kAElems;
-#pragma unroll
-        for (int i = 0; i < kAChunks; ++i) {
-            *reinterpret_cast<uint4*>(As + (r0 + 32 * i) * kLdsRow + kc * 8) = ra[i];
-        }
-#pragma unroll
-        for (int i = 0; i < kBChunks; ++i) {
-            const int lr = r0 + 32 * i;
-            if (lr < BN) *reinterpret_cast<uint4*>(Bs + lr * kLdsRow + kc * 8) = rb[i];
-        }
-    };
+    // ---- consumer ----
+    const int lr = lane & 15, sw = (lane >> 1) & 7, hi = lane >> 4;
+    const int off0 = lr * kRowBytes + ((hi ^ sw) * 16);
+    const int off1 = lr * kRowBytes + (((4 + hi) ^ sw) * 16);
 
     f32x4_t acc[kMT][kNT];
 #pragma unroll
@@ -196,51 +362,24 @@ k_gemm_mfma(const bf16_t* __restrict__ A, const bf16_t* __restrict__ B, bf16_t* 
 #pragma unroll
         for (int j = 0; j < kNT; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-    load_tile(0);
-    store_tile(0);
-    __syncthreads();
-
-    const int frag_row = lane & 15;
-    const int frag_k = (lane >> 4) * 8;
+    int stage = 0;
     for (int kt = 0; kt < KT; ++kt) {
-        const int cur = kt & 1;
-        if (kt + 1 < KT) load_tile(kt + 1);
-        const bf16_t* As = smem + cur * kStage;
-        const bf16_t* Bs = As + kAElems;
-#pragma unroll
-        for (int kk = 0; kk < BK; kk += 32) {
-            bf16x8_t af[kMT];
-#pragma unroll
-            for (int i = 0; i < kMT; ++i) {
-                af[i] = *reinterpret_cast<const bf16x8_t*>(
-                    As + (wave * 64 + i * 16 + frag_row) * kLdsRow + kk + frag_k);
-            }
-#pragma unroll
-            for (int j = 0; j < kNT; ++j) {
-                const bf16x8_t bw = *reinterpret_cast<const bf16x8_t*>(
-                    Bs + (j * 16 + frag_row) * kLdsRow + kk + frag_k);
-#pragma unroll
-                for (int i = 0; i < kMT; ++i) {
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bw, af[i], acc[i][j], 0, 0, 0);
-                }
-            }
-        }
-        if (kt + 1 < KT) store_tile(cur ^ 1);
-        __syncthreads();
+        wait_and_join<63>();   // only this wave's LDS reads (it issues no DMA)
+        consume_tile(acc, smem + stage * kStageBytes, wave, off0, off1);
+        stage = stage == 2 ? 0 : stage + 1;
     }
 
-    // ---- epilogue: lane holds C[m][n..n+3] for each (i, j) ----
-    const int quad = (lane >> 4) * 4;
+    // ---- epilogue: lane holds C[m][n..n+3] for each (i, j); N % 4 == 0, so a quad is either
+    // wholly in range or wholly out ----
+    const int64_t m0 = static_cast<int64_t>(tm) * BM, n0 = static_cast<int64_t>(tn) * BN;
+    const int quad = hi * 4;
 #pragma unroll
     for (int i = 0; i < kMT; ++i) {
-        const int64_t m = m0 + wave * 64 + i * 16 + frag_row;
-        if (m >= M) continue;
+        const int64_t m = m0 + wave * 64 + i * 16 + lr;
 #pragma unroll
         for (int j = 0; j < kNT; ++j) {
             const int64_t n = n0 + j * 16 + quad;
-            if (n >= N) continue;
-            const float a4[4] = {acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]};
-            store_quad(e, out, m, n, N, a4, vec_epi && n + 4 <= N);
+            if (m < M && n < N) store_quad<ACT, MODE>(e, out, m, n, N, acc[i][j]);
         }
     }
 }
@@ -250,7 +389,7 @@ constexpr int kGemvMaxM = 8;
 
 __global__ void __launch_bounds__(256) k_gemv(const bf16_t* __restrict__ A,
                                               const bf16_t* __restrict__ B, bf16_t* out,
-                                              int64_t M, int64_t N, int64_t K, Epi e) {
+                                              int64_t M, int64_t N, int64_t K, Epi e, int mode) {
     const int lane = threadIdx.x & 63;
     const int64_t n = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
     if (n >= N) return;
@@ -294,13 +433,7 @@ __global__ void __launch_bounds__(256) k_gemv(const bf16_t* __restrict__ A,
             if (m == lane) a = part[m];
         const int64_t m = lane;
         float v = e.bias ? __fadd_rn(a, bf2f(e.bias[n])) : a;
-        v = epi_value(v, e.act, e.round_mid);
-        if (e.row_add) v = __fadd_rn(v, bf2f(e.row_add[(m % e.row_add_period) * N + n]));
-        if (e.residual) {
-            const float res = bf2f(e.residual[m * e.ld_out + n]);
-            if (e.gate) v = __fadd_rn(__fmul_rn(v, bf2f(e.gate[(m / e.gate_rows) * N + n])), res);
-            else v = __fadd_rn(res, v);
-        }
+        v = finish(e, mode, act_exact(e.act, v), m, n, N);
         out[m * e.ld_out + n] = f2bf(v);
     }
 }
@@ -331,11 +464,47 @@ __global__ void __launch_bounds__(256) k_gemm_generic(const T* __restrict__ A, c
         acc = __fadd_rn(acc, __fmul_rn(ldv(A, i * K + p), bv));
     }
     if (bias) acc = __fadd_rn(acc, ldv(bias, j));
-    stv(out, idx, epi_value(acc, act, false));
+    stv(out, idx, act_exact(act, acc));
+}
+
+// Reference order with the fused epilogue (bf16, B as [N,K]): shapes whose K is not a multiple
+// of the MFMA kernel's 64, e.g. the patch embedding's K = in_channels * patch^2 = 16.
+__global__ void __launch_bounds__(256) k_gemm_fused_small(const bf16_t* __restrict__ A,
+                                                          const bf16_t* __restrict__ B,
+                                                          bf16_t* out, int64_t M, int64_t N,
+                                                          int64_t K, Epi e, int mode) {
+    const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (idx >= M * N) return;
+    const int64_t m = idx / N, n = idx % N;
+    float acc = 0.f;
+    for (int64_t p = 0; p < K; ++p)
+        acc = __fadd_rn(acc, __fmul_rn(bf2f(A[m * K + p]), bf2f(B[n * K + p])));
+    if (e.bias) acc = __fadd_rn(acc, bf2f(e.bias[n]));
+    out[m * e.ld_out + n] = f2bf(finish(e, mode, act_exact(e.act, acc), m, n, N));
 }
 
 bool aligned(const void* p, int bytes) {
     return (reinterpret_cast<uintptr_t>(p) % bytes) == 0;
+}
+
+template <int ACT, int MODE>
+void launch_tn(const bf16_t* a, const bf16_t* b, bf16_t* out, int64_t m, int64_t n, int64_t k,
+               const Epi& e, hipStream_t s) {
+    const int tiles_m = static_cast<int>((m + BM - 1) / BM);
+    const int tiles_n = static_cast<int>((n + BN - 1) / BN);
+    k_gemm_tn<ACT, MODE><<<tiles_m * tiles_n, kWgThreads, 0, s>>>(a, b, out, m, n, k, e, tiles_m,
+                                                                 tiles_n, 4);
+}
+
+template <int ACT>
+void launch_tn_mode(int mode, const bf16_t* a, const bf16_t* b, bf16_t* out, int64_t m, int64_t n,
+                    int64_t k, const Epi& e, hipStream_t s) {
+    switch (mode) {
+        case EPI_STORE: launch_tn<ACT, EPI_STORE>(a, b, out, m, n, k, e, s); break;
+        case EPI_ROW_ADD: launch_tn<ACT, EPI_ROW_ADD>(a, b, out, m, n, k, e, s); break;
+        case EPI_RESIDUAL: launch_tn<ACT, EPI_RESIDUAL>(a, b, out, m, n, k, e, s); break;
+        default: launch_tn<ACT, EPI_GATED>(a, b, out, m, n, k, e, s); break;
+    }
 }
 
 }  // namespace
@@ -362,32 +531,38 @@ void launch_gemm_generic(const void* a, const void* b, const void* bias, void* o
 void launch_gemm_bf16(const bf16_t* a, const bf16_t* b, const bf16_t* bias, bf16_t* out,
                       int64_t m, int64_t n, int64_t k, const GemmEpilogue& ep, hipStream_t s) {
     if (m == 0 || n == 0) return;
+    require(!ep.gate || ep.residual, "gemm: a gate needs a residual");
     Epi e{bias, ep.act, ep.round_mid, ep.row_add, ep.row_add_period > 0 ? ep.row_add_period : 1,
           ep.residual, ep.gate, ep.gate_rows > 0 ? ep.gate_rows : 1, ep.ld_out > 0 ? ep.ld_out : n};
-    const bool fast_k = (k % 8 == 0) && aligned(a, 16) && aligned(b, 16);
+    const int mode = ep.residual ? (ep.gate ? EPI_GATED : EPI_RESIDUAL)
+                                 : (ep.row_add ? EPI_ROW_ADD : EPI_STORE);
     const double flops = 2.0 * static_cast<double>(m) * n * k;
-    if (!fast_k) {
-        require(!ep.row_add && !ep.residual && !ep.round_mid && e.ld_out == n,
-                "gemm: fused epilogues need K % 8 == 0 and 16-byte aligned operands");
-        ProfileScope ps(K_GEMM, s, flops);
-        launch_gemm_generic(a, b, bias, out, m, n, k, true, ep.act, false, s);
-        return;
-    }
-    if (m <= kGemvMaxM) {
+    const bool k8 = (k % 8 == 0) && aligned(a, 16) && aligned(b, 16);
+    if (k8 && m <= kGemvMaxM) {
         ProfileScope ps(K_GEMV, s, flops);
         const int grid = static_cast<int>((n + 3) / 4);
-        k_gemv<<<grid, 256, 0, s>>>(a, b, out, m, n, k, e);
+        k_gemv<<<grid, 256, 0, s>>>(a, b, out, m, n, k, e, mode);
         launch_check("gemm (small M)");
         return;
     }
-    const int tiles_m = static_cast<int>((m + BM - 1) / BM);
-    const int tiles_n = static_cast<int>((n + BN - 1) / BN);
-    const bool vec = (n % 4 == 0) && (e.ld_out % 4 == 0) && aligned(out, 8) &&
-                     (!bias || aligned(bias, 8)) && (!e.residual || aligned(e.residual, 8)) &&
-                     (!e.gate || aligned(e.gate, 8)) && (!e.row_add || aligned(e.row_add, 8));
+    // The MFMA kernel stores whole aligned quads of columns.
+    const bool vec = (e.ld_out % 4 == 0) && aligned(out, 8) && (!bias || aligned(bias, 8)) &&
+                     (!e.residual || aligned(e.residual, 8)) && (!e.gate || aligned(e.gate, 8)) &&
+                     (!e.row_add || aligned(e.row_add, 8)) && (n % 4 == 0);
+    if (!k8 || k % BK != 0 || !vec) {
+        ProfileScope ps(K_GEMM, s, flops);
+        const int64_t total = m * n;
+        k_gemm_fused_small<<<static_cast<int>((total + 255) / 256), 256, 0, s>>>(a, b, out, m, n,
+                                                                                k, e, mode);
+        launch_check("gemm (reference order, fused epilogue)");
+        return;
+    }
     ProfileScope ps(K_GEMM, s, flops, gemm_subclass());
-    k_gemm_mfma<<<tiles_m * tiles_n, kThreads, 0, s>>>(a, b, out, m, n, k, e, tiles_m, tiles_n,
-                                                       4, vec);
+    switch (ep.act) {
+        case 1: launch_tn_mode<1>(mode, a, b, out, m, n, k, e, s); break;
+        case 2: launch_tn_mode<2>(mode, a, b, out, m, n, k, e, s); break;
+        default: launch_tn_mode<0>(mode, a, b, out, m, n, k, e, s); break;
+    }
     launch_check("gemm (mfma)");
 }
 
