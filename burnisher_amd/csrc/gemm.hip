@@ -99,19 +99,6 @@ __device__ __forceinline__ float act_exact(int act, float v) {
     return v;
 }
 
-__device__ __forceinline__ void unpack4(uint2 raw, float (&f)[4]) {
-    f[0] = __uint_as_float(raw.x << 16);
-    f[1] = __uint_as_float(raw.x & 0xffff0000u);
-    f[2] = __uint_as_float(raw.y << 16);
-    f[3] = __uint_as_float(raw.y & 0xffff0000u);
-}
-__device__ __forceinline__ uint2 pack4(const float (&f)[4]) {
-    uint2 r;
-    r.x = static_cast<uint32_t>(f2bf(f[0])) | (static_cast<uint32_t>(f2bf(f[1])) << 16);
-    r.y = static_cast<uint32_t>(f2bf(f[2])) | (static_cast<uint32_t>(f2bf(f[3])) << 16);
-    return r;
-}
-
 // One output element after the activation, any mode (the scalar tail and the small kernels).
 __device__ __forceinline__ float finish(const Epi& e, int mode, float v, int64_t m, int64_t c,
                                         int64_t N) {
@@ -125,43 +112,60 @@ __device__ __forceinline__ float finish(const Epi& e, int mode, float v, int64_t
     return v;
 }
 
-// Four consecutive columns, all in range and 8-byte aligned.
-template <int ACT, int MODE>
-__device__ __forceinline__ void store_quad(const Epi& e, bf16_t* out, int64_t m, int64_t n,
-                                           int64_t N, const f32x4_t& acc) {
-    float v[4], t[4];
-    if (e.bias) {
-        unpack4(*reinterpret_cast<const uint2*>(e.bias + n), t);
+__device__ __forceinline__ void unpack8(uint4 raw, float (&f)[8]) {
+    const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
 #pragma unroll
-        for (int r = 0; r < 4; ++r) v[r] = __fadd_rn(acc[r], t[r]);
+    for (int i = 0; i < 4; ++i) {
+        f[2 * i] = __uint_as_float(w[i] << 16);
+        f[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+    }
+}
+__device__ __forceinline__ uint4 pack8(const float (&f)[8]) {
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        w[i] = static_cast<uint32_t>(f2bf(f[2 * i])) | (static_cast<uint32_t>(f2bf(f[2 * i + 1])) << 16);
+    return make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+// Eight consecutive columns [n, n+8) of row m, all in range and 16-byte aligned: the epilogue
+// for one 16-byte store.
+template <int ACT, int MODE>
+__device__ __forceinline__ void store_oct(const Epi& e, bf16_t* out, int64_t m, int64_t n,
+                                          int64_t N, const float (&acc)[8]) {
+    float v[8], t[8];
+    if (e.bias) {
+        unpack8(*reinterpret_cast<const uint4*>(e.bias + n), t);
+#pragma unroll
+        for (int r = 0; r < 8; ++r) v[r] = __fadd_rn(acc[r], t[r]);
     } else {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) v[r] = acc[r];
+        for (int r = 0; r < 8; ++r) v[r] = acc[r];
     }
 #pragma unroll
-    for (int r = 0; r < 4; ++r) v[r] = act_fast<ACT>(v[r]);
+    for (int r = 0; r < 8; ++r) v[r] = act_fast<ACT>(v[r]);
     if (MODE != EPI_STORE && e.round_mid) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) v[r] = round_bf16(v[r]);
+        for (int r = 0; r < 8; ++r) v[r] = round_bf16(v[r]);
     }
     if (MODE == EPI_ROW_ADD) {
-        unpack4(*reinterpret_cast<const uint2*>(e.row_add + (m % e.row_add_period) * N + n), t);
+        unpack8(*reinterpret_cast<const uint4*>(e.row_add + (m % e.row_add_period) * N + n), t);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) v[r] = __fadd_rn(v[r], t[r]);
+        for (int r = 0; r < 8; ++r) v[r] = __fadd_rn(v[r], t[r]);
     }
     if (MODE == EPI_RESIDUAL || MODE == EPI_GATED) {
-        float res[4];
-        unpack4(*reinterpret_cast<const uint2*>(e.residual + m * e.ld_out + n), res);
+        float res[8];
+        unpack8(*reinterpret_cast<const uint4*>(e.residual + m * e.ld_out + n), res);
         if (MODE == EPI_GATED) {
-            unpack4(*reinterpret_cast<const uint2*>(e.gate + (m / e.gate_rows) * N + n), t);
+            unpack8(*reinterpret_cast<const uint4*>(e.gate + (m / e.gate_rows) * N + n), t);
 #pragma unroll
-            for (int r = 0; r < 4; ++r) v[r] = __fadd_rn(__fmul_rn(v[r], t[r]), res[r]);
+            for (int r = 0; r < 8; ++r) v[r] = __fadd_rn(__fmul_rn(v[r], t[r]), res[r]);
         } else {
 #pragma unroll
-            for (int r = 0; r < 4; ++r) v[r] = __fadd_rn(res[r], v[r]);
+            for (int r = 0; r < 8; ++r) v[r] = __fadd_rn(res[r], v[r]);
         }
     }
-    *reinterpret_cast<uint2*>(out + m * e.ld_out + n) = pack4(v);
+    *reinterpret_cast<uint4*>(out + m * e.ld_out + n) = pack8(v);
 }
 
 // ---- the MFMA tile kernel ----------------------------------------------------------------------
@@ -302,6 +306,67 @@ __device__ __forceinline__ void wait_and_join() {
 constexpr int kConsumers = 4;
 constexpr int kWgThreads = 2 * kConsumers * 64;   // 512
 
+// The output tile is staged in LDS as fp32 before the epilogue: rows of 144 floats padded to
+// 148 (592 bytes), which makes the consumers' 16-byte writes of 16 rows land on disjoint banks.
+constexpr int kCRow = BN + 4;
+static_assert(BM * kCRow * 4 <= 3 * kStageBytes, "fp32 output tile must fit in the stages");
+
+// Consumer wave: the k-loop, then its 64 x 144 accumulators into the LDS output tile.
+__device__ __forceinline__ void consume(char* smem, int KT, int wave, int lane) {
+    const int lr = lane & 15, sw = (lane >> 1) & 7, hi = lane >> 4;
+    const int off0 = lr * kRowBytes + ((hi ^ sw) * 16);
+    const int off1 = lr * kRowBytes + (((4 + hi) ^ sw) * 16);
+
+    f32x4_t acc[kMT][kNT];
+#pragma unroll
+    for (int i = 0; i < kMT; ++i)
+#pragma unroll
+        for (int j = 0; j < kNT; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+    int stage = 0;
+    for (int kt = 0; kt < KT; ++kt) {
+        wait_and_join<63>();   // only this wave's LDS reads (it issues no DMA)
+        consume_tile(acc, smem + stage * kStageBytes, wave, off0, off1);
+        stage = stage == 2 ? 0 : stage + 1;
+    }
+    wait_and_join<63>();   // every wave is done with the stages (producers drained their DMA)
+
+    // lane holds C[row][col..col+3] for each (i, j)
+    float* ctile = reinterpret_cast<float*>(smem);
+#pragma unroll
+    for (int i = 0; i < kMT; ++i)
+#pragma unroll
+        for (int j = 0; j < kNT; ++j) {
+            const int row = wave * 64 + i * 16 + lr, col = j * 16 + hi * 4;
+            *reinterpret_cast<f32x4_t*>(ctile + row * kCRow + col) = acc[i][j];
+        }
+}
+
+// All 512 threads: the fp32 tile out of LDS, through the epilogue, to global memory in 16-byte
+// stores, 18 consecutive lanes per 288-byte output row (the MFMA layout itself would store
+// 8-byte pieces of 16 rows at a time, which runs at about half the write bandwidth).
+template <int ACT, int MODE>
+__device__ __forceinline__ void store_tile(const char* smem, const Epi& e, bf16_t* out, int64_t M,
+                                           int64_t N, int64_t m0, int64_t n0) {
+    const float* ctile = reinterpret_cast<const float*>(smem);
+    constexpr int kChunks = BN / 8;   // 18 per row
+    for (int c = threadIdx.x; c < BM * kChunks; c += kWgThreads) {
+        const int r = c / kChunks, ch = c - r * kChunks;
+        const int64_t m = m0 + r, n = n0 + ch * 8;
+        if (m < M && n < N) {
+            float v[8];
+            const f32x4_t lo = *reinterpret_cast<const f32x4_t*>(ctile + r * kCRow + ch * 8);
+            const f32x4_t hi = *reinterpret_cast<const f32x4_t*>(ctile + r * kCRow + ch * 8 + 4);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                v[q] = lo[q];
+                v[4 + q] = hi[q];
+            }
+            store_oct<ACT, MODE>(e, out, m, n, N, v);
+        }
+    }
+}
+
 template <int ACT, int MODE>
 __global__ void __launch_bounds__(kWgThreads, 1)
 k_gemm_tn(const bf16_t* __restrict__ A, const bf16_t* __restrict__ B, bf16_t* out, int64_t M,
@@ -347,42 +412,15 @@ k_gemm_tn(const bf16_t* __restrict__ A, const bf16_t* __restrict__ B, bf16_t* ou
             dma_tile(smem + s2 * kStageBytes, t, static_cast<int64_t>(min(kt + 2, KT - 1)) * BK);
             stage = stage == 2 ? 0 : stage + 1;
         }
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // the two trailing copies
-        return;
+        wait_and_join<0>();   // the two trailing copies have landed before LDS is reused below
+    } else {
+        consume(smem, KT, wave, lane);
     }
-
-    // ---- consumer ----
-    const int lr = lane & 15, sw = (lane >> 1) & 7, hi = lane >> 4;
-    const int off0 = lr * kRowBytes + ((hi ^ sw) * 16);
-    const int off1 = lr * kRowBytes + (((4 + hi) ^ sw) * 16);
-
-    f32x4_t acc[kMT][kNT];
-#pragma unroll
-    for (int i = 0; i < kMT; ++i)
-#pragma unroll
-        for (int j = 0; j < kNT; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-
-    int stage = 0;
-    for (int kt = 0; kt < KT; ++kt) {
-        wait_and_join<63>();   // only this wave's LDS reads (it issues no DMA)
-        consume_tile(acc, smem + stage * kStageBytes, wave, off0, off1);
-        stage = stage == 2 ? 0 : stage + 1;
-    }
-
-    // ---- epilogue: lane holds C[m][n..n+3] for each (i, j); N % 4 == 0, so a quad is either
-    // wholly in range or wholly out ----
-    const int64_t m0 = static_cast<int64_t>(tm) * BM, n0 = static_cast<int64_t>(tn) * BN;
-    const int quad = hi * 4;
-#pragma unroll
-    for (int i = 0; i < kMT; ++i) {
-        const int64_t m = m0 + wave * 64 + i * 16 + lr;
-#pragma unroll
-        for (int j = 0; j < kNT; ++j) {
-            const int64_t n = n0 + j * 16 + quad;
-            if (m < M && n < N) store_quad<ACT, MODE>(e, out, m, n, N, acc[i][j]);
-        }
-    }
+    wait_and_join<63>();   // the staged output tile is complete and visible
+    store_tile<ACT, MODE>(smem, e, out, M, N, static_cast<int64_t>(tm) * BM,
+                          static_cast<int64_t>(tn) * BN);
 }
+
 
 // ---- small M: one wave per output column, both operands read with 16-byte loads ----
 constexpr int kGemvMaxM = 8;
@@ -545,10 +583,10 @@ void launch_gemm_bf16(const bf16_t* a, const bf16_t* b, const bf16_t* bias, bf16
         launch_check("gemm (small M)");
         return;
     }
-    // The MFMA kernel stores whole aligned quads of columns.
-    const bool vec = (e.ld_out % 4 == 0) && aligned(out, 8) && (!bias || aligned(bias, 8)) &&
-                     (!e.residual || aligned(e.residual, 8)) && (!e.gate || aligned(e.gate, 8)) &&
-                     (!e.row_add || aligned(e.row_add, 8)) && (n % 4 == 0);
+    // The MFMA kernel's epilogue works on aligned runs of 8 columns.
+    const bool vec = (e.ld_out % 8 == 0) && aligned(out, 16) && (!bias || aligned(bias, 16)) &&
+                     (!e.residual || aligned(e.residual, 16)) && (!e.gate || aligned(e.gate, 16)) &&
+                     (!e.row_add || aligned(e.row_add, 16)) && (n % 8 == 0);
     if (!k8 || k % BK != 0 || !vec) {
         ProfileScope ps(K_GEMM, s, flops);
         const int64_t total = m * n;
