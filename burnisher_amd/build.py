@@ -46,9 +46,15 @@ def sources() -> list[Path]:
     return sorted(p for p in CSRC.iterdir() if p.suffix in (".hip", ".cpp"))
 
 
+# Per-file code-generation options. flash72.hip keeps its output accumulators in VGPRs: they are
+# rescaled by VALU multiplies, and in the default AGPR form every rescale and loop iteration
+# copies all 80 of them between the register files.
+EXTRA_FLAGS = {"flash72.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+
+
 def _compile(src: Path) -> Path:
     obj = OBJ / (src.name + ".o")
-    cmd = [hipcc(), *COMMON_FLAGS, "-c", str(src), "-o", str(obj)]
+    cmd = [hipcc(), *COMMON_FLAGS, *EXTRA_FLAGS.get(src.name, []), "-c", str(src), "-o", str(obj)]
     if src.suffix == ".cpp":
         cmd[1:1] = ["-x", "hip"]
     proc = subprocess.run(cmd, capture_output=True, text=True)

@@ -24,6 +24,7 @@
 #include "common.h"
 
 #include <cmath>
+#include <mutex>
 
 namespace bh {
 namespace {
@@ -395,14 +396,48 @@ __global__ void __launch_bounds__(128) k_attention_generic(const T* __restrict__
     for (int64_t d = 0; d < D; ++d) stv(orow, d, __fdiv_rn(acc[d], denom));
 }
 
+}  // namespace
+
+namespace {
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
+// V^T scratch for the head_dim-72 path of the op-level entry point: grown on demand, kept until
+// the process ends, one per device. Calls that overlap on one device share it.
+bf16_t* vt_workspace(size_t elems) {
+    static std::mutex mu;
+    static void* ptr[64] = {};
+    static size_t cap[64] = {};
+    int dev = 0;
+    hip_check(hipGetDevice(&dev), "hipGetDevice");
+    require(dev >= 0 && dev < 64, "attention: device index out of range");
+    std::lock_guard<std::mutex> lock(mu);
+    if (cap[dev] < elems) {
+        if (ptr[dev]) hip_check(hipFree(ptr[dev]), "hipFree");
+        ptr[dev] = nullptr;
+        cap[dev] = 0;
+        hip_check(hipMalloc(&ptr[dev], elems * sizeof(bf16_t)), "hipMalloc (V^T workspace)");
+        cap[dev] = elems;
+    }
+    return static_cast<bf16_t*>(ptr[dev]);
+}
 }  // namespace
 
 void launch_attention_bf16(const bf16_t* q, const bf16_t* k, const bf16_t* v, bf16_t* out,
                            const AttnShape& sh, const void* key_mask, bool mask_f32,
                            hipStream_t s) {
     if (sh.batch * sh.heads * sh.q_len == 0) return;
+    // head_dim 72 (the DiT): V transposed once, then the flash kernel built for that width.
+    const bool fast72 = sh.head_dim == 72 && sh.kv_len <= 16384 && sh.ld_q % 8 == 0 &&
+                        sh.ld_kv % 8 == 0 && sh.ld_o % 4 == 0 && aligned16(q) && aligned16(k) &&
+                        aligned16(v) && (reinterpret_cast<uintptr_t>(out) % 8 == 0);
+    if (fast72) {
+        const int64_t vt_ld = flash72_vt_ld(sh.kv_len);
+        bf16_t* vt = vt_workspace(static_cast<size_t>(sh.batch * sh.heads * 72 * vt_ld));
+        launch_transpose_v72(v, sh.ld_kv, sh.batch, sh.heads, sh.kv_len, vt, vt_ld, s);
+        launch_flash72(q, sh.ld_q, k, sh.ld_kv, vt, vt_ld, out, sh.ld_o, sh.batch, sh.heads,
+                       sh.q_len, sh.kv_len, sh.scale, key_mask, mask_f32, s);
+        return;
+    }
     require(sh.kv_len > 0, "attention: kv_len must be positive");
     require(sh.head_dim >= 1 && sh.head_dim <= 128,
             "attention (hip-gfx950): head_dim must be in [1, 128]");

@@ -153,6 +153,16 @@ struct AttnShape {
 void launch_attention_bf16(const bf16_t* q, const bf16_t* k, const bf16_t* v, bf16_t* out,
                            const AttnShape& sh, const void* key_mask, bool mask_f32,
                            hipStream_t s);
+// Flash attention at head_dim 72 with V supplied transposed (flash72.hip): vt holds, for each
+// (b, h, d), a row of vt_ld >= flash72_vt_ld(kv_len) keys, zero past kv_len.
+int64_t flash72_vt_ld(int64_t kv_len);
+void launch_flash72(const bf16_t* q, int64_t ld_q, const bf16_t* k, int64_t ld_k,
+                    const bf16_t* vt, int64_t vt_ld, bf16_t* out, int64_t ld_o, int64_t batch,
+                    int64_t heads, int64_t q_len, int64_t kv_len, float scale,
+                    const void* key_mask, bool mask_f32, hipStream_t s);
+// V [batch, kv_len, ld_v] (head-last, head_dim 72) -> the V^T rows launch_flash72 reads.
+void launch_transpose_v72(const bf16_t* v, int64_t ld_v, int64_t batch, int64_t heads,
+                          int64_t kv_len, bf16_t* vt, int64_t vt_ld, hipStream_t s);
 // Reference-order attention (one thread per query row), any dtype, additive bias supported.
 void launch_attention_generic(const void* q, const void* k, const void* v, void* out,
                               const AttnShape& sh, const void* bias, const void* key_mask,
