@@ -16,10 +16,8 @@ The JSON line also carries:
   step          the whole step's algorithmic FLOP (the reference's accounting,
                 eval/burnscore/geometry.py:275-367) over the measured step time, same peak;
   kernels       per-class time of one separately profiled step (not the timed region);
-  cpu_baseline  the stock oracle's dit-step on this host's cores, on a bounded sample: the
-                prologue plus one and two blocks at the same 1024px shape, extrapolated to 28
-                blocks by the per-block time (the graph is a fixed prologue, 28 identical blocks
-                and a head).
+  cpu_baseline  the stock oracle's whole dit-step on this host's cores (about 30 s on 16
+                threads at 1024px), same workload and seeds.
 """
 from __future__ import annotations
 
@@ -59,7 +57,7 @@ def parse() -> argparse.Namespace:
 
 
 def cpu_baseline(wl, threads: int) -> dict:
-    """The stock oracle on this host: prologue + 1 block and prologue + 2 blocks, timed."""
+    """The stock oracle's whole dit-step (all 28 blocks) on this host, timed once."""
     import numpy as np
     import oracle
     from burnisher_amd.workload import config_struct
@@ -67,22 +65,16 @@ def cpu_baseline(wl, threads: int) -> dict:
     cfg = config_struct(wl.cfg)
     w, keep = wl.weight_struct(wl.top, wl.blocks)
     out = np.zeros((wl.batch, wl.cfg["out_channels"], wl.latent_hw, wl.latent_hw), np.uint16)
-    times = {}
-    for layers in (1, 2):
-        t0 = time.perf_counter()
-        oracle.call(oracle.stock(), "stock_dit_forward", ctypes.byref(cfg), ctypes.byref(w),
-                    wl.batch, wl.latent_hw, wl.caption_len, wl.latent.ctypes.data, wl.timestep,
-                    wl.caption.ctypes.data, wl.mask.ctypes.data, 0, out.ctypes.data, threads,
-                    layers)
-        times[layers] = time.perf_counter() - t0
-        log(f"cpu baseline: prologue + {layers} block(s) in {times[layers]:.2f} s")
-    per_block = times[2] - times[1]
-    fixed = times[1] - per_block
-    step_s = fixed + wl.cfg["num_layers"] * per_block
+    t0 = time.perf_counter()
+    oracle.call(oracle.stock(), "stock_dit_forward", ctypes.byref(cfg), ctypes.byref(w),
+                wl.batch, wl.latent_hw, wl.caption_len, wl.latent.ctypes.data, wl.timestep,
+                wl.caption.ctypes.data, wl.mask.ctypes.data, 0, out.ctypes.data, threads, -1)
+    step_s = time.perf_counter() - t0
+    log(f"cpu baseline: one full dit-step in {step_s:.2f} s")
     return {"value": round(step_s * 1e3, 1), "unit": "ms", "cores": threads, "kind": "port",
-            "sample": (f"stock oracle (oracle/stock.cpp) dit-step at the same 1024px B=2 shape, "
-                       f"run with 1 and with 2 of the 28 blocks ({times[1]:.1f} s, "
-                       f"{times[2]:.1f} s); step = prologue/head + 28 x per-block time")}
+            "sample": (f"one whole dit-step of the stock oracle (oracle/stock.cpp, the reference's "
+                       f"stock numerics) at the same {wl.latent_hw * 8}px B=2 workload and seeds, "
+                       f"{threads} threads, not extrapolated")}
 
 
 def main() -> int:
