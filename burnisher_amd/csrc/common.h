@@ -134,6 +134,14 @@ struct GemmEpilogue {
     const bf16_t* gate = nullptr;
     int64_t gate_rows = 1;
     int64_t ld_out = 0;        // 0 means n
+    // Transposed store of the V columns of a fused projection, for the head_dim-72 attention:
+    // column n with w = n % vt_period >= vt_col0 is head h = (w - vt_col0) / vt_dim, dim
+    // dd = (w - vt_col0) % vt_dim of block n / vt_period, and row m is token m % vt_seq of batch
+    // m / vt_seq; it goes to vt[((blk * batches + b) * vt_heads + h) * vt_dim + dd][token] with
+    // rows of vt_ld tokens, and nowhere else. vt_col0 and vt_period must be multiples of 144.
+    bf16_t* vt = nullptr;
+    int64_t vt_period = 0, vt_col0 = 0, vt_seq = 0, vt_ld = 0;
+    int vt_heads = 0, vt_dim = 72;
 };
 
 // bf16 out[m, n] = A[m, k] . B[n, k]^T (+bias) with `ep`. Picks the MFMA tile kernel, the

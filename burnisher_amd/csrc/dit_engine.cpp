@@ -113,6 +113,9 @@ struct bh_dit {
     DevBuf temb, h_t, emb_t, silu_t, modulation, cap_h, cap, kv_all, chunks, tables_dev;
     DevBuf shift, scale, gate, zero, tokens;
     DevBuf w_qkv, b_qkv, w_kv, b_kv;   // repacked weights (fused plan)
+    DevBuf vt_self, vt_cross;         // V transposed for the attention kernel (fused plan)
+    int64_t vt_ld_self = 0, vt_ld_cross = 0;
+    bool vt72 = false;
     int64_t workspace = 0;
 
     DevBuf make(int64_t elems) {
@@ -277,7 +280,17 @@ void forward_fused(bh_dit& e, const void* latent, double t, const void* caption,
         gemm(static_cast<const bf16_t*>(caption), e.w.cap1_w, e.w.cap1_b, e.cap_h.bf(), e.Mcap, d,
              c.caption_channels, gelu, s);
         gemm(e.cap_h.bf(), e.w.cap2_w, e.w.cap2_b, e.cap.bf(), e.Mcap, d, d, plain, s);
-        gemm(e.cap.bf(), e.w_kv.p, e.b_kv.p, e.kv_all.bf(), e.Mcap, L * 2 * d, d, plain, s);
+        GemmEpilogue kv;   // every layer's K into kv_all; V into V^T at head_dim 72
+        if (e.vt72) {
+            kv.vt = e.vt_cross.bf();
+            kv.vt_period = 2 * d;
+            kv.vt_col0 = d;
+            kv.vt_seq = e.cap_len;
+            kv.vt_ld = e.vt_ld_cross;
+            kv.vt_heads = c.num_heads;
+            kv.vt_dim = c.head_dim;
+        }
+        gemm(e.cap.bf(), e.w_kv.p, e.b_kv.p, e.kv_all.bf(), e.Mcap, L * 2 * d, d, kv, s);
     }
     {
         ProfileScope ps(K_ELEMENTWISE, s, 2.0 * (B * 6 * d + L * 6 * d + L * 6 * B * d));
@@ -300,12 +313,29 @@ void forward_fused(bh_dit& e, const void* latent, double t, const void* caption,
             ProfileScope ps(K_NORM, s, 4.0 * M * d);
             launch_norm_modulate_pre(e.x.bf(), shift_msa, scale_msa, e.modded.bf(), B, N, d, eps, s);
         }
-        {
+        {   // Q and K into the [M, 3d] buffer; at head_dim 72, V straight into V^T for the
+            // attention kernel (other widths keep V in the buffer for the generic attention)
             SubclassScope sc(K_GEMM_QKV);
-            gemm(e.modded.bf(), wqkv, bqkv, e.qkv.bf(), M, 3 * d, d, plain, s);
+            GemmEpilogue ep;
+            if (e.vt72) {
+                ep.vt = e.vt_self.bf();
+                ep.vt_period = 3 * d;
+                ep.vt_col0 = 2 * d;
+                ep.vt_seq = N;
+                ep.vt_ld = e.vt_ld_self;
+                ep.vt_heads = static_cast<int>(H);
+                ep.vt_dim = static_cast<int>(Dh);
+            }
+            gemm(e.modded.bf(), wqkv, bqkv, e.qkv.bf(), M, 3 * d, d, ep, s);
         }
-        launch_attention_bf16(e.qkv.bf(), e.qkv.bf() + d, e.qkv.bf() + 2 * d, e.ctx.bf(),
-                              AttnShape{B, H, N, N, Dh, 3 * d, 3 * d, d, scale}, nullptr, false, s);
+        if (e.vt72) {
+            launch_flash72(e.qkv.bf(), 3 * d, e.qkv.bf() + d, 3 * d, e.vt_self.bf(), e.vt_ld_self,
+                           e.ctx.bf(), d, B, H, N, N, scale, nullptr, false, s);
+        } else {
+            launch_attention_bf16(e.qkv.bf(), e.qkv.bf() + d, e.qkv.bf() + 2 * d, e.ctx.bf(),
+                                  AttnShape{B, H, N, N, Dh, 3 * d, 3 * d, d, scale}, nullptr,
+                                  false, s);
+        }
         {
             GemmEpilogue ep;
             ep.round_mid = true;
@@ -316,9 +346,16 @@ void forward_fused(bh_dit& e, const void* latent, double t, const void* caption,
         }
         // 2. cross-attention (no norm before it: pixart_dit.cpp:251-253)
         gemm(e.x.bf(), bw.attn2_q_w, bw.attn2_q_b, e.q2.bf(), M, d, d, plain, s);
-        launch_attention_bf16(e.q2.bf(), e.kv_all.bf() + l * 2 * d, e.kv_all.bf() + l * 2 * d + d,
-                              e.ctx.bf(), AttnShape{B, H, N, e.cap_len, Dh, d, L * 2 * d, d, scale},
-                              mask, mask_f32, s);
+        if (e.vt72) {
+            launch_flash72(e.q2.bf(), d, e.kv_all.bf() + l * 2 * d, L * 2 * d,
+                           e.vt_cross.bf() + l * B * H * Dh * e.vt_ld_cross, e.vt_ld_cross,
+                           e.ctx.bf(), d, B, H, N, e.cap_len, scale, mask, mask_f32, s);
+        } else {
+            launch_attention_bf16(e.q2.bf(), e.kv_all.bf() + l * 2 * d,
+                                  e.kv_all.bf() + l * 2 * d + d, e.ctx.bf(),
+                                  AttnShape{B, H, N, e.cap_len, Dh, d, L * 2 * d, d, scale}, mask,
+                                  mask_f32, s);
+        }
         {
             GemmEpilogue ep;
             ep.round_mid = true;
@@ -445,6 +482,14 @@ int bh_dit_create(const bh_dit_config* cfg, const bh_dit_weights* w, int64_t bat
             e->q2 = e->make(M * d);
             e->kv_all = e->make(e->Mcap * L * 2 * d);
             e->chunks = e->make(L * 6 * B * d);
+            // the head_dim-72 attention reads V transposed, written by the projections' epilogue
+            e->vt72 = c.head_dim == 72 && e->N <= 16384 && caption_len <= 16384 && d % 144 == 0;
+            if (e->vt72) {
+                e->vt_ld_self = flash72_vt_ld(e->N);
+                e->vt_ld_cross = flash72_vt_ld(caption_len);
+                e->vt_self = e->make(B * c.num_heads * 72 * e->vt_ld_self);
+                e->vt_cross = e->make(L * B * c.num_heads * 72 * e->vt_ld_cross);
+            }
             e->w_qkv = e->make(L * 3 * d * d);
             e->b_qkv = e->make(L * 3 * d);
             e->w_kv = e->make(L * 2 * d * d);

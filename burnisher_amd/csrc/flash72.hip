@@ -91,32 +91,63 @@ __device__ __forceinline__ void wait_and_join() {
     asm volatile("" ::: "memory");
 }
 
-// The key block starting at kv0 into `stage`: K rows (144 bytes each, contiguous) as DMA blocks
-// 0..8 and V^T rows 0..71 (128 bytes = the block's 64 keys, 16-byte chunk c of row d stored at
-// slot c ^ ((d >> 1) & 7)) as blocks 9..17, spread over the waves; blocks 18-19 re-load block 0
-// into the spare area so every wave issues exactly kDmaPerWave instructions.
-__device__ __forceinline__ void dma_block(char* stage, const Flash72Args& a, int b, int h,
-                                          int kv0, int wave, int lane) {
-    // per-lane parts of the two kinds of item (K block ki: row lg/9, chunk lg%9 of lg = 64ki + L;
-    // V^T block vi: row 8vi + L/8, swizzled chunk)
-    const int vsub = lane >> 3, vslot = lane & 7;
-    const bf16_t* vt_bh = a.vt + (static_cast<int64_t>(b) * a.H + h) * D * a.vt_ld + kv0;
-    const bf16_t* k_b = a.k + static_cast<int64_t>(b) * a.Skv * a.ld_k + h * D;
+// The key blocks stream into `stage` as K rows (144 bytes each, contiguous) in DMA blocks 0..8
+// and V^T rows 0..71 (128 bytes = the block's 64 keys, 16-byte chunk c of row d stored at slot
+// c ^ ((d >> 1) & 7)) in blocks 9..17, spread over the waves; blocks 18-19 re-load block 0 into
+// the spare area so every wave issues exactly kDmaPerWave instructions. DmaPlan holds this
+// lane's part of each of its wave's instructions, so a block costs one add per instruction.
+struct DmaPlan {
+    int64_t off[kDmaPerWave];    // element offset from a.k (K items) or a.vt (V^T items), kv0 = 0
+    int krow[kDmaPerWave];       // K items: the row within the block (-1 for V^T items)
+    int dst[kDmaPerWave];        // byte offset within the stage
+};
+
+__device__ __forceinline__ DmaPlan dma_plan(const Flash72Args& a, int b, int h, int wave, int lane) {
+    DmaPlan p;
 #pragma unroll
     for (int i = 0; i < kDmaPerWave; ++i) {
         const int item = i * kWaves + wave;            // wave-uniform
         const bool is_v = item >= 9 && item < 18;
-        const int ki = item < 9 ? item : 0;             // spares (18, 19) re-load K block 0
-        const int lg = ki * 64 + lane;
-        const int row = lg / 9, ch = lg - row * 9;
-        const bf16_t* ksrc = k_b + static_cast<int64_t>(min(kv0 + row, a.Skv - 1)) * a.ld_k + ch * 8;
-        const int vi = is_v ? item - 9 : 0;
-        const int d = vi * 8 + vsub;
-        const bf16_t* vsrc = vt_bh + static_cast<int64_t>(d) * a.vt_ld + ((vslot ^ ((d >> 1) & 7)) * 8);
-        const int dst = item < 9 ? item * 1024
-                                 : (is_v ? kKBytes + vi * 1024 : kKBytes + kVBytes + (item - 18) * 1024);
-        dma16(is_v ? vsrc : ksrc, stage + dst);
+        if (is_v) {
+            const int vi = item - 9;
+            const int d = vi * 8 + (lane >> 3);
+            const int c = (lane & 7) ^ ((d >> 1) & 7);
+            p.off[i] = ((static_cast<int64_t>(b) * a.H + h) * D + d) * a.vt_ld + c * 8;
+            p.krow[i] = -1;
+            p.dst[i] = kKBytes + vi * 1024;
+        } else {
+            const int ki = item < 9 ? item : 0;        // spares (18, 19) re-load K block 0
+            const int lg = ki * 64 + lane;
+            const int row = lg / 9, ch = lg - row * 9;
+            p.off[i] = static_cast<int64_t>(b) * a.Skv * a.ld_k + h * D + ch * 8;
+            p.krow[i] = row;
+            p.dst[i] = item < 9 ? item * 1024 : kKBytes + kVBytes + (item - 18) * 1024;
+        }
     }
+    return p;
+}
+
+template <bool CLAMP>
+__device__ __forceinline__ void dma_block(char* stage, const Flash72Args& a, const DmaPlan& p,
+                                          int kv0) {
+#pragma unroll
+    for (int i = 0; i < kDmaPerWave; ++i) {
+        const bf16_t* src;
+        if (p.krow[i] < 0) {
+            src = a.vt + p.off[i] + kv0;
+        } else {
+            const int key = CLAMP ? min(kv0 + p.krow[i], a.Skv - 1) : kv0 + p.krow[i];
+            src = a.k + p.off[i] + static_cast<int64_t>(key) * a.ld_k;
+        }
+        dma16(src, stage + p.dst[i]);
+    }
+}
+
+// Three-input maximum (v_max3_f32). This file is compiled with -fno-honor-nans: with IEEE NaN
+// rules the compiler would first quiet every MFMA result with an extra v_max, doubling the cost
+// of the row maximum. Scores here are finite, or -inf for masked keys.
+__device__ __forceinline__ float max3(float a, float b, float c) {
+    return __builtin_fmaxf(a, __builtin_fmaxf(b, c));
 }
 
 __device__ __forceinline__ bf16x8_t ld_frag(const char* p) {
@@ -203,7 +234,9 @@ __global__ void __launch_bounds__(kThreads, 1) k_flash72(Flash72Args a) {
     int koff[3];
 #pragma unroll
     for (int ks = 0; ks < 3; ++ks) koff[ks] = lr * kKRow + (ks * 4 + g) * 16;
-    const bool kpad = g != 0;   // ks = 2 covers dims 64..95: only g = 0 (64..71) is real
+    // ks = 2 covers dims 64..95 and only g = 0 (dims 64..71) is real: Q is zero in the other
+    // lanes, and the K bytes read there are the next row's (or, past the last row, V^T's) finite
+    // values, so their products vanish without zeroing K.
     int voff[2][2];
 #pragma unroll
     for (int cc = 0; cc < 2; ++cc) {
@@ -222,14 +255,15 @@ __global__ void __launch_bounds__(kThreads, 1) k_flash72(Flash72Args a) {
     for (int u = 0; u < kQT; ++u) mc[u] = -INFINITY;
 
     // ---- the key-block pipeline ----
-    dma_block(smem, a, b, h, live[0] * kKV, wave, lane);
-    dma_block(smem + kStage, a, b, h, live[min(1, nlive - 1)] * kKV, wave, lane);
+    const DmaPlan plan = dma_plan(a, b, h, wave, lane);
+    dma_block<MASKED>(smem, a, plan, live[0] * kKV);
+    dma_block<MASKED>(smem + kStage, a, plan, live[min(1, nlive - 1)] * kKV);
     int stage = 0;
     for (int jj = 0; jj < nlive; ++jj) {
         wait_and_join<kDmaPerWave>();
         {
             const int s2 = stage == 0 ? 2 : stage - 1;
-            dma_block(smem + s2 * kStage, a, b, h, live[min(jj + 2, nlive - 1)] * kKV, wave, lane);
+            dma_block<MASKED>(smem + s2 * kStage, a, plan, live[min(jj + 2, nlive - 1)] * kKV);
         }
         const char* cur = smem + stage * kStage;
         const int blk = live[jj];
@@ -241,9 +275,6 @@ __global__ void __launch_bounds__(kThreads, 1) k_flash72(Flash72Args a) {
             bf16x8_t kf[3];
 #pragma unroll
             for (int ks = 0; ks < 3; ++ks) kf[ks] = ld_frag(cur + t * 16 * kKRow + koff[ks]);
-#pragma unroll
-            for (int e = 0; e < 8; ++e)
-                if (kpad) kf[2][e] = static_cast<__bf16>(0.0f);
 #pragma unroll
             for (int u = 0; u < kQT; ++u) {
                 f32x4_t acc = f32x4_t{0.f, 0.f, 0.f, 0.f};
@@ -278,12 +309,18 @@ __global__ void __launch_bounds__(kThreads, 1) k_flash72(Flash72Args a) {
         bool need = false;
 #pragma unroll
         for (int u = 0; u < kQT; ++u) {
-            float m = fmaxf(fmaxf(s[0][u][0], s[0][u][1]), fmaxf(s[0][u][2], s[0][u][3]));
-#pragma unroll
-            for (int t = 1; t < kKT; ++t)
-                m = fmaxf(m, fmaxf(fmaxf(s[t][u][0], s[t][u][1]), fmaxf(s[t][u][2], s[t][u][3])));
-            m = fmaxf(m, __shfl_xor(m, 16, 64));
-            m = fmaxf(m, __shfl_xor(m, 32, 64));
+            float m = max3(s[0][u][0], s[0][u][1], s[0][u][2]);
+            m = max3(m, s[0][u][3], s[1][u][0]);
+            m = max3(m, s[1][u][1], s[1][u][2]);
+            m = max3(m, s[1][u][3], s[2][u][0]);
+            m = max3(m, s[2][u][1], s[2][u][2]);
+            m = max3(m, s[2][u][3], s[3][u][0]);
+            m = max3(m, s[3][u][1], s[3][u][2]);
+            m = max3(m, s[3][u][3], s[3][u][3]);
+            const float m16 = __shfl_xor(m, 16, 64);
+            m = max3(m, m16, m16);
+            const float m32 = __shfl_xor(m, 32, 64);
+            m = max3(m, m32, m32);
             lmc[u] = m * a.c;
             need |= lmc[u] > mc[u] + kRescaleThreshold;
         }

@@ -61,6 +61,9 @@ struct Epi {
     const bf16_t* gate;
     int64_t gate_rows;
     int64_t ld_out;
+    bf16_t* vt;                 // transposed V columns (see GemmEpilogue)
+    int64_t vt_period, vt_col0, vt_seq, vt_ld;
+    int vt_heads, vt_dim;
 };
 
 // ---- activations ------------------------------------------------------------------------------
@@ -349,6 +352,43 @@ template <int ACT, int MODE>
 __device__ __forceinline__ void store_tile(const char* smem, const Epi& e, bf16_t* out, int64_t M,
                                            int64_t N, int64_t m0, int64_t n0) {
     const float* ctile = reinterpret_cast<const float*>(smem);
+    if (e.vt && n0 % e.vt_period >= e.vt_col0) {
+        // V columns: 8 consecutive tokens of one column per 16-byte store, consecutive threads
+        // along the token axis of one V^T row. A thread keeps its 8-row group (512 threads over
+        // 32 groups), so its batch and token are worked out once.
+        constexpr int kGroups = BM / 8;   // 32
+        const int rg = threadIdx.x % kGroups;
+        const int64_t m = m0 + rg * 8;
+        if (m >= M) return;
+        const int64_t batches = M / e.vt_seq;
+        const int64_t b = m / e.vt_seq, tok = m - b * e.vt_seq;
+        const bool whole = tok + 8 <= e.vt_seq && m + 8 <= M;
+        const int vbase = static_cast<int>(n0 % e.vt_period - e.vt_col0);
+        const int64_t blk = n0 / e.vt_period;
+        for (int col = threadIdx.x / kGroups; col < BN; col += kWgThreads / kGroups) {
+            if (n0 + col >= N) break;
+            const int vc = vbase + col;
+            const int h = vc / 72, dd = vc - h * 72;   // the vt store is built for head_dim 72
+            const float bias = e.bias ? bf2f(e.bias[n0 + col]) : 0.f;
+            float v[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                v[j] = ctile[(rg * 8 + j) * kCRow + col];
+                if (e.bias) v[j] = __fadd_rn(v[j], bias);
+            }
+            const int64_t hrow = ((blk * batches + b) * e.vt_heads + h) * 72 + dd;
+            if (whole) {
+                *reinterpret_cast<uint4*>(e.vt + hrow * e.vt_ld + tok) = pack8(v);
+            } else {
+                for (int j = 0; j < 8 && m + j < M; ++j) {
+                    const int64_t bj = (m + j) / e.vt_seq, tj = (m + j) - bj * e.vt_seq;
+                    e.vt[(((blk * batches + bj) * e.vt_heads + h) * 72 + dd) * e.vt_ld + tj] =
+                        f2bf(v[j]);
+                }
+            }
+        }
+        return;
+    }
     constexpr int kChunks = BN / 8;   // 18 per row
     for (int c = threadIdx.x; c < BM * kChunks; c += kWgThreads) {
         const int r = c / kChunks, ch = c - r * kChunks;
@@ -521,6 +561,66 @@ __global__ void __launch_bounds__(256) k_gemm_fused_small(const bf16_t* __restri
     out[m * e.ld_out + n] = f2bf(finish(e, mode, act_exact(e.act, acc), m, n, N));
 }
 
+// Small K (the patch embedding's K = in_channels * patch^2 = 16): one thread per 8 consecutive
+// output columns of one row, the reference's sequential k order, 16-byte loads and stores. Needs
+// K % 8 == 0, N % 8 == 0 and 16-byte aligned operands.
+__global__ void __launch_bounds__(256) k_gemm_smallk(const bf16_t* __restrict__ A,
+                                                     const bf16_t* __restrict__ B, bf16_t* out,
+                                                     int M, int N, int K, Epi e, int mode) {
+    const int groups = N >> 3;
+    const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= M * groups) return;
+    const int m = idx / groups, n0 = (idx - m * groups) * 8;
+    float acc[8];
+#pragma unroll
+    for (int r = 0; r < 8; ++r) acc[r] = 0.f;
+    for (int k0 = 0; k0 < K; k0 += 8) {
+        float a[8];
+        unpack8(*reinterpret_cast<const uint4*>(A + static_cast<int64_t>(m) * K + k0), a);
+#pragma unroll
+        for (int r = 0; r < 8; ++r) {
+            float w[8];
+            unpack8(*reinterpret_cast<const uint4*>(B + static_cast<int64_t>(n0 + r) * K + k0), w);
+#pragma unroll
+            for (int t = 0; t < 8; ++t) acc[r] = __fadd_rn(acc[r], __fmul_rn(a[t], w[t]));
+        }
+    }
+    float v[8], t[8];
+    if (e.bias) {
+        unpack8(*reinterpret_cast<const uint4*>(e.bias + n0), t);
+#pragma unroll
+        for (int r = 0; r < 8; ++r) v[r] = __fadd_rn(acc[r], t[r]);
+    } else {
+#pragma unroll
+        for (int r = 0; r < 8; ++r) v[r] = acc[r];
+    }
+#pragma unroll
+    for (int r = 0; r < 8; ++r) v[r] = act_exact(e.act, v[r]);
+    if (mode != EPI_STORE && e.round_mid) {
+#pragma unroll
+        for (int r = 0; r < 8; ++r) v[r] = round_bf16(v[r]);
+    }
+    if (mode == EPI_ROW_ADD) {
+        const int pr = static_cast<int>(m % static_cast<int>(e.row_add_period));
+        unpack8(*reinterpret_cast<const uint4*>(e.row_add + static_cast<int64_t>(pr) * N + n0), t);
+#pragma unroll
+        for (int r = 0; r < 8; ++r) v[r] = __fadd_rn(v[r], t[r]);
+    } else if (mode == EPI_RESIDUAL || mode == EPI_GATED) {
+        float res[8];
+        unpack8(*reinterpret_cast<const uint4*>(e.residual + static_cast<int64_t>(m) * e.ld_out + n0), res);
+        if (mode == EPI_GATED) {
+            const int gr = static_cast<int>(m / static_cast<int>(e.gate_rows));
+            unpack8(*reinterpret_cast<const uint4*>(e.gate + static_cast<int64_t>(gr) * N + n0), t);
+#pragma unroll
+            for (int r = 0; r < 8; ++r) v[r] = __fadd_rn(__fmul_rn(v[r], t[r]), res[r]);
+        } else {
+#pragma unroll
+            for (int r = 0; r < 8; ++r) v[r] = __fadd_rn(res[r], v[r]);
+        }
+    }
+    *reinterpret_cast<uint4*>(out + static_cast<int64_t>(m) * e.ld_out + n0) = pack8(v);
+}
+
 bool aligned(const void* p, int bytes) {
     return (reinterpret_cast<uintptr_t>(p) % bytes) == 0;
 }
@@ -571,11 +671,24 @@ void launch_gemm_bf16(const bf16_t* a, const bf16_t* b, const bf16_t* bias, bf16
     if (m == 0 || n == 0) return;
     require(!ep.gate || ep.residual, "gemm: a gate needs a residual");
     Epi e{bias, ep.act, ep.round_mid, ep.row_add, ep.row_add_period > 0 ? ep.row_add_period : 1,
-          ep.residual, ep.gate, ep.gate_rows > 0 ? ep.gate_rows : 1, ep.ld_out > 0 ? ep.ld_out : n};
+          ep.residual, ep.gate, ep.gate_rows > 0 ? ep.gate_rows : 1, ep.ld_out > 0 ? ep.ld_out : n,
+          ep.vt, ep.vt_period, ep.vt_col0, ep.vt_seq, ep.vt_ld, ep.vt_heads, ep.vt_dim};
+    if (ep.vt) {
+        require(!ep.residual && !ep.row_add && !ep.round_mid,
+                "gemm: the transposed V store has no residual or row-add epilogue");
+        require(ep.vt_period > 0 && ep.vt_period % BN == 0 && ep.vt_col0 % BN == 0 &&
+                    ep.vt_col0 < ep.vt_period && ep.vt_seq > 0 && m % ep.vt_seq == 0 &&
+                    ep.vt_ld >= ep.vt_seq && ep.vt_heads > 0 && ep.vt_dim > 0 &&
+                    ep.vt_dim == 72 && (ep.vt_period - ep.vt_col0) == int64_t{ep.vt_heads} * 72 &&
+                    ep.vt_ld % 8 == 0 && aligned(ep.vt, 16),
+                "gemm: transposed V store geometry");
+    }
     const int mode = ep.residual ? (ep.gate ? EPI_GATED : EPI_RESIDUAL)
                                  : (ep.row_add ? EPI_ROW_ADD : EPI_STORE);
     const double flops = 2.0 * static_cast<double>(m) * n * k;
     const bool k8 = (k % 8 == 0) && aligned(a, 16) && aligned(b, 16);
+    require(!ep.vt || (k8 && m > kGemvMaxM && k % BK == 0),
+            "gemm: the transposed V store needs the MFMA kernel (K % 64 == 0, M > 8)");
     if (k8 && m <= kGemvMaxM) {
         ProfileScope ps(K_GEMV, s, flops);
         const int grid = static_cast<int>((n + 3) / 4);
@@ -587,6 +700,15 @@ void launch_gemm_bf16(const bf16_t* a, const bf16_t* b, const bf16_t* bias, bf16
     const bool vec = (e.ld_out % 8 == 0) && aligned(out, 16) && (!bias || aligned(bias, 16)) &&
                      (!e.residual || aligned(e.residual, 16)) && (!e.gate || aligned(e.gate, 16)) &&
                      (!e.row_add || aligned(e.row_add, 16)) && (n % 8 == 0);
+    if (k8 && k % BK != 0 && vec && k <= 256 && m * (n / 8) < (int64_t{1} << 31) &&
+        e.row_add_period < (int64_t{1} << 31) && e.gate_rows < (int64_t{1} << 31)) {
+        ProfileScope ps(K_GEMM, s, flops);
+        const int64_t threads = m * (n / 8);
+        k_gemm_smallk<<<static_cast<int>((threads + 255) / 256), 256, 0, s>>>(
+            a, b, out, static_cast<int>(m), static_cast<int>(n), static_cast<int>(k), e, mode);
+        launch_check("gemm (small K)");
+        return;
+    }
     if (!k8 || k % BK != 0 || !vec) {
         ProfileScope ps(K_GEMM, s, flops);
         const int64_t total = m * n;
