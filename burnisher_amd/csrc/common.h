@@ -50,6 +50,17 @@ __host__ __device__ inline bf16_t f2bf(float f) {
 // What a store through the tensor dtype does to a float.
 __host__ __device__ inline float round_bf16(float f) { return bf2f(f2bf(f)); }
 
+// s_waitcnt through the builtin (gfx9 encoding: vmcnt in bits 3:0 and 15:14, expcnt 6:4, lgkmcnt
+// 11:8; expcnt is left unconstrained). Unlike inline assembly, the compiler's own wait insertion
+// sees this wait: after an opaque one it must assume that scalar loads issued before a loop may
+// still be outstanding, and then waits for lgkmcnt(0) before the first use of ANY LDS read in
+// the loop instead of only the reads that use needs.
+template <int VM, int LGKM>
+__device__ __forceinline__ void s_waitcnt() {
+    static_assert(VM >= 0 && VM < 64 && LGKM >= 0 && LGKM < 16, "waitcnt range");
+    __builtin_amdgcn_s_waitcnt((VM & 15) | (7 << 4) | (LGKM << 8) | ((VM >> 4) << 14));
+}
+
 // ---- errors ---------------------------------------------------------------------------------
 
 struct Error : std::runtime_error {

@@ -86,60 +86,73 @@ __device__ __forceinline__ void dma16(const void* src, const char* lds) {
 template <int N>
 __device__ __forceinline__ void wait_and_join() {
     asm volatile("" ::: "memory");
-    asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" : : "n"(N) : "memory");
+    s_waitcnt<N, 0>();
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
 }
 
 // The key blocks stream into `stage` as K rows (144 bytes each, contiguous) in DMA blocks 0..8
 // and V^T rows 0..71 (128 bytes = the block's 64 keys, 16-byte chunk c of row d stored at slot
-// c ^ ((d >> 1) & 7)) in blocks 9..17, spread over the waves; blocks 18-19 re-load block 0 into
-// the spare area so every wave issues exactly kDmaPerWave instructions. DmaPlan holds this
-// lane's part of each of its wave's instructions, so a block costs one add per instruction.
+// c ^ ((d >> 1) & 7)) in blocks 9..17, spread over the waves: instruction i of wave w carries
+// block 4i + w. Blocks 18-19 re-load block 0 into the spare area so every wave issues exactly
+// kDmaPerWave instructions. Which kind an instruction is depends only on (i, wave), so the
+// branch on it is scalar. DmaPlan holds this lane's element offset for each instruction at key
+// block 0 (for K items including its row's stride), so a block costs one 64-bit add per
+// instruction, plus a clamp of the row for the partial last block of a masked run.
 struct DmaPlan {
-    int64_t off[kDmaPerWave];    // element offset from a.k (K items) or a.vt (V^T items), kv0 = 0
-    int krow[kDmaPerWave];       // K items: the row within the block (-1 for V^T items)
-    int dst[kDmaPerWave];        // byte offset within the stage
+    int64_t off[kDmaPerWave];
+    int krow[kDmaPerWave];       // K items: the row within the block
 };
+
+__device__ __forceinline__ bool dma_is_v(int i, int wave) {
+    const int item = i * kWaves + wave;
+    return item >= 9 && item < 18;
+}
+__device__ __forceinline__ int dma_dst(int i, int wave) {
+    const int item = i * kWaves + wave;
+    return item < 9 ? item * 1024 : item < 18 ? kKBytes + (item - 9) * 1024
+                                              : kKBytes + kVBytes + (item - 18) * 1024;
+}
 
 __device__ __forceinline__ DmaPlan dma_plan(const Flash72Args& a, int b, int h, int wave, int lane) {
     DmaPlan p;
 #pragma unroll
     for (int i = 0; i < kDmaPerWave; ++i) {
         const int item = i * kWaves + wave;            // wave-uniform
-        const bool is_v = item >= 9 && item < 18;
-        if (is_v) {
+        if (dma_is_v(i, wave)) {
             const int vi = item - 9;
             const int d = vi * 8 + (lane >> 3);
             const int c = (lane & 7) ^ ((d >> 1) & 7);
             p.off[i] = ((static_cast<int64_t>(b) * a.H + h) * D + d) * a.vt_ld + c * 8;
-            p.krow[i] = -1;
-            p.dst[i] = kKBytes + vi * 1024;
+            p.krow[i] = 0;
         } else {
             const int ki = item < 9 ? item : 0;        // spares (18, 19) re-load K block 0
             const int lg = ki * 64 + lane;
             const int row = lg / 9, ch = lg - row * 9;
-            p.off[i] = static_cast<int64_t>(b) * a.Skv * a.ld_k + h * D + ch * 8;
+            p.off[i] = (static_cast<int64_t>(b) * a.Skv + row) * a.ld_k + h * D + ch * 8;
             p.krow[i] = row;
-            p.dst[i] = item < 9 ? item * 1024 : kKBytes + kVBytes + (item - 18) * 1024;
         }
     }
     return p;
 }
 
-template <bool CLAMP>
+// Key block starting at key kv0 into `stage`. `partial`: the block runs past the last key, whose
+// row then stands in for the missing ones (their scores are masked).
 __device__ __forceinline__ void dma_block(char* stage, const Flash72Args& a, const DmaPlan& p,
-                                          int kv0) {
+                                          int wave, int kv0, bool partial) {
+    const int64_t kstep = static_cast<int64_t>(kv0) * a.ld_k;
 #pragma unroll
     for (int i = 0; i < kDmaPerWave; ++i) {
         const bf16_t* src;
-        if (p.krow[i] < 0) {
+        if (dma_is_v(i, wave)) {
             src = a.vt + p.off[i] + kv0;
+        } else if (!partial) {
+            src = a.k + p.off[i] + kstep;
         } else {
-            const int key = CLAMP ? min(kv0 + p.krow[i], a.Skv - 1) : kv0 + p.krow[i];
-            src = a.k + p.off[i] + static_cast<int64_t>(key) * a.ld_k;
+            const int key = min(kv0 + p.krow[i], a.Skv - 1);
+            src = a.k + p.off[i] + (static_cast<int64_t>(key) - p.krow[i]) * a.ld_k;
         }
-        dma16(src, stage + p.dst[i]);
+        dma16(src, stage + dma_dst(i, wave));
     }
 }
 
@@ -173,6 +186,25 @@ __global__ void __launch_bounds__(kThreads, 1) k_flash72(Flash72Args a) {
     const int b = bh / a.H, h = bh - b * a.H;
     const int q_base = (bid - bh * a.qblocks) * kQPerWg + wave * kQPerWave;
     const int nblk = (a.Skv + kKV - 1) / kKV;
+
+    // ---- Q fragments, resident: tile u, K=32 step ks covers dims 32ks + 8g .. +7 (loaded first,
+    // so their latency overlaps the set-up below) ----
+    bf16x8_t qf[kQT][3];
+#pragma unroll
+    for (int u = 0; u < kQT; ++u) {
+        const int q = q_base + u * 16 + lr;
+#pragma unroll
+        for (int ks = 0; ks < 3; ++ks) {
+            const int d0 = ks * 32 + g * 8;
+            bf16x8_t f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) f[e] = static_cast<__bf16>(0.0f);
+            if (q < a.Sq && d0 < D)
+                f = ld_frag(reinterpret_cast<const char*>(
+                    a.q + (static_cast<int64_t>(b) * a.Sq + q) * a.ld_q + h * D + d0));
+            qf[u][ks] = f;
+        }
+    }
 
     // ---- key validity per block (bit i = key 64 blk + i is in range and unmasked) ----
     if (MASKED) {
@@ -211,24 +243,6 @@ __global__ void __launch_bounds__(kThreads, 1) k_flash72(Flash72Args a) {
     const int nlive = nlive_s;
     const bool all_masked = MASKED && all_masked_s != 0;
 
-    // ---- Q fragments, resident: tile u, K=32 step ks covers dims 32ks + 8g .. +7 ----
-    bf16x8_t qf[kQT][3];
-#pragma unroll
-    for (int u = 0; u < kQT; ++u) {
-        const int q = q_base + u * 16 + lr;
-#pragma unroll
-        for (int ks = 0; ks < 3; ++ks) {
-            const int d0 = ks * 32 + g * 8;
-            bf16x8_t f;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) f[e] = static_cast<__bf16>(0.0f);
-            if (q < a.Sq && d0 < D)
-                f = ld_frag(reinterpret_cast<const char*>(
-                    a.q + (static_cast<int64_t>(b) * a.Sq + q) * a.ld_q + h * D + d0));
-            qf[u][ks] = f;
-        }
-    }
-
     // fragment byte offsets within a stage
     const int sw = (lr >> 1) & 7;
     int koff[3];
@@ -255,15 +269,22 @@ __global__ void __launch_bounds__(kThreads, 1) k_flash72(Flash72Args a) {
     for (int u = 0; u < kQT; ++u) mc[u] = -INFINITY;
 
     // ---- the key-block pipeline ----
+    // The Q loads are drained here, where the compiler sees it: otherwise it waits for them
+    // (vmcnt(0), which also drains the DMA in flight) at their first use in every iteration.
+    s_waitcnt<0, 15>();
     const DmaPlan plan = dma_plan(a, b, h, wave, lane);
-    dma_block<MASKED>(smem, a, plan, live[0] * kKV);
-    dma_block<MASKED>(smem + kStage, a, plan, live[min(1, nlive - 1)] * kKV);
+    const int last_full = a.Skv / kKV;   // blocks below this one hold 64 real keys
+    auto issue = [&](char* stage_ptr, int blk) {
+        dma_block(stage_ptr, a, plan, wave, blk * kKV, MASKED && blk >= last_full);
+    };
+    issue(smem, live[0]);
+    issue(smem + kStage, live[min(1, nlive - 1)]);
     int stage = 0;
     for (int jj = 0; jj < nlive; ++jj) {
         wait_and_join<kDmaPerWave>();
         {
             const int s2 = stage == 0 ? 2 : stage - 1;
-            dma_block<MASKED>(smem + s2 * kStage, a, plan, live[min(jj + 2, nlive - 1)] * kKV);
+            issue(smem + s2 * kStage, live[min(jj + 2, nlive - 1)]);
         }
         const char* cur = smem + stage * kStage;
         const int blk = live[jj];
@@ -366,7 +387,7 @@ __global__ void __launch_bounds__(kThreads, 1) k_flash72(Flash72Args a) {
             }
         stage = stage == 2 ? 0 : stage + 1;
     }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // the trailing copies
+    s_waitcnt<0, 15>();   // the trailing copies
 
     // ---- normalise and store: lane holds out[q][d..d+3], d = 16e + 4g; O^T row 72 is the sum ----
 #pragma unroll

@@ -1,25 +1,25 @@
 // bf16 GEMM for the dit-step on gfx950: out[M,N] = A[M,K] . B[N,K]^T (+bias, activation,
 // fused residual), fp32 accumulation on the MFMA cores.
 //
-// Tile: 256 (M) x 144 (N) x 64 (K) per 256-thread workgroup; wave w owns rows [64w, 64w+64) and
-// all 144 columns as a 4 x 9 grid of 16x16 accumulators (v_mfma_f32_16x16x32_bf16). 144 divides
+// Tile: 256 (M) x 144 (N) x 64 (K) per 512-thread workgroup, one workgroup per CU. 144 divides
 // every DiT output width (1152, 3456, 4608, 28*2304) and 256 divides M = 2*4096, so the
 // 8192-row GEMMs launch exactly 256, 768 and 1024 tiles: whole waves on 256 CUs, where the usual
 // 256x128 tile would leave the last wave of N=1152 one-eighth full.
 //
-// Operand staging: direct global->LDS loads (global_load_lds_dwordx4: each wave instruction
-// writes 1 KiB = eight 128-byte LDS rows without passing through VGPRs) into THREE LDS stages of
-// 50 KiB, so k-tiles are fetched up to three ahead of the one being multiplied (see k_gemm_tn).
+// Waves 0-3 multiply: wave w owns output rows [64w, 64w+64) and all 144 columns as a 4 x 9 grid
+// of 16x16 accumulators (v_mfma_f32_16x16x32_bf16). Waves 4-7 only move the operands: direct
+// global->LDS loads (global_load_lds_dwordx4, 1 KiB per wave instruction, no VGPRs) into THREE
+// LDS stages of 51 KiB, two k-tiles in flight behind the one being multiplied (see k_gemm_tn).
+// A DMA instruction can hold its wave for tens of cycles while the address unit is busy; in a
+// wave of its own that costs the matrix cores nothing.
 //
 // LDS rows are 128 bytes (64 bf16 of K) with the 16-byte chunk c of row r stored at slot
 // c ^ ((r >> 1) & 7): the 16 rows one ds_read_b128 fragment touches then cover all 64 banks
 // exactly once, with no padding (padding would break the 1 KiB contiguity of a DMA write).
 //
-// The MFMA is issued with the weight fragment as its first operand, so the accumulator layout
-// puts four consecutive OUTPUT COLUMNS of one row in each lane: the epilogue reads bias,
-// residual and gate and writes the result with 8-byte accesses. Epilogues are template
-// specialisations, so each instantiation is straight-line code and the accumulators stay in
-// registers.
+// The MFMA is issued with the weight fragment as its first operand, so each lane's accumulator
+// holds four consecutive OUTPUT COLUMNS of one row. The epilogue stages the fp32 tile in LDS and
+// all 512 threads apply bias, activation, residual and gate and store 16 bytes at a time.
 //
 // Tile order is XCD-aware: workgroup i runs on XCD i%8, so tiles are renumbered so that each XCD
 // gets a contiguous band of M-tiles x N-tiles, walked 4 M-tiles at a time, whose A and B panels
@@ -131,54 +131,13 @@ __device__ __forceinline__ uint4 pack8(const float (&f)[8]) {
     return make_uint4(w[0], w[1], w[2], w[3]);
 }
 
-// Eight consecutive columns [n, n+8) of row m, all in range and 16-byte aligned: the epilogue
-// for one 16-byte store.
-template <int ACT, int MODE>
-__device__ __forceinline__ void store_oct(const Epi& e, bf16_t* out, int64_t m, int64_t n,
-                                          int64_t N, const float (&acc)[8]) {
-    float v[8], t[8];
-    if (e.bias) {
-        unpack8(*reinterpret_cast<const uint4*>(e.bias + n), t);
-#pragma unroll
-        for (int r = 0; r < 8; ++r) v[r] = __fadd_rn(acc[r], t[r]);
-    } else {
-#pragma unroll
-        for (int r = 0; r < 8; ++r) v[r] = acc[r];
-    }
-#pragma unroll
-    for (int r = 0; r < 8; ++r) v[r] = act_fast<ACT>(v[r]);
-    if (MODE != EPI_STORE && e.round_mid) {
-#pragma unroll
-        for (int r = 0; r < 8; ++r) v[r] = round_bf16(v[r]);
-    }
-    if (MODE == EPI_ROW_ADD) {
-        unpack8(*reinterpret_cast<const uint4*>(e.row_add + (m % e.row_add_period) * N + n), t);
-#pragma unroll
-        for (int r = 0; r < 8; ++r) v[r] = __fadd_rn(v[r], t[r]);
-    }
-    if (MODE == EPI_RESIDUAL || MODE == EPI_GATED) {
-        float res[8];
-        unpack8(*reinterpret_cast<const uint4*>(e.residual + m * e.ld_out + n), res);
-        if (MODE == EPI_GATED) {
-            unpack8(*reinterpret_cast<const uint4*>(e.gate + (m / e.gate_rows) * N + n), t);
-#pragma unroll
-            for (int r = 0; r < 8; ++r) v[r] = __fadd_rn(__fmul_rn(v[r], t[r]), res[r]);
-        } else {
-#pragma unroll
-            for (int r = 0; r < 8; ++r) v[r] = __fadd_rn(res[r], v[r]);
-        }
-    }
-    *reinterpret_cast<uint4*>(out + m * e.ld_out + n) = pack8(v);
-}
-
 // ---- the MFMA tile kernel ----------------------------------------------------------------------
 
 // Wait until at most N vector-memory operations of this wave are outstanding and every LDS
 // operation has completed.
 template <int N>
 __device__ __forceinline__ void wait_vm_lgkm0() {
-    static_assert(N >= 0 && N < 64, "vmcnt range");
-    asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" : : "n"(N) : "memory");
+    s_waitcnt<N, 0>();
 }
 
 // One global_load_lds_dwordx4: lane L's 16 bytes at `src` land at LDS address lds + 16 L, where
@@ -389,20 +348,82 @@ __device__ __forceinline__ void store_tile(const char* smem, const Epi& e, bf16_
         }
         return;
     }
-    constexpr int kChunks = BN / 8;   // 18 per row
-    for (int c = threadIdx.x; c < BM * kChunks; c += kWgThreads) {
-        const int r = c / kChunks, ch = c - r * kChunks;
-        const int64_t m = m0 + r, n = n0 + ch * 8;
-        if (m < M && n < N) {
-            float v[8];
-            const f32x4_t lo = *reinterpret_cast<const f32x4_t*>(ctile + r * kCRow + ch * 8);
-            const f32x4_t hi = *reinterpret_cast<const f32x4_t*>(ctile + r * kCRow + ch * 8 + 4);
+    // A thread keeps one 8-column chunk (18 per row, 28 rows per pass over 504 threads) for the
+    // whole tile, so bias and gate are loaded once. Rows go in batches of kBatch: every load of a
+    // batch (LDS tile, residual, row_add) is issued before its first store, since the compiler
+    // may not move a load above a store that could alias it.
+    constexpr int kChunks = BN / 8;
+    constexpr int kRowStep = kWgThreads / kChunks;   // 28
+    constexpr int kBatch = 5;
+    const int ch = threadIdx.x % kChunks;
+    const int r0 = threadIdx.x / kChunks;
+    const int64_t n = n0 + ch * 8;
+    if (r0 >= kRowStep || n >= N) return;
+    float bias[8];
+    if (e.bias) unpack8(*reinterpret_cast<const uint4*>(e.bias + n), bias);
+    else
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                v[q] = lo[q];
-                v[4 + q] = hi[q];
+        for (int q = 0; q < 8; ++q) bias[q] = 0.f;
+    // gate rows are whole batches of tokens: one gate row per tile unless the tile straddles two
+    const int64_t m_last = min(m0 + BM, M) - 1;
+    const bool gate_uniform = MODE == EPI_GATED && m0 / e.gate_rows == m_last / e.gate_rows;
+    float gate_t[8];
+    if (gate_uniform) unpack8(*reinterpret_cast<const uint4*>(e.gate + (m0 / e.gate_rows) * N + n), gate_t);
+    for (int rb = r0; rb < BM; rb += kBatch * kRowStep) {
+        float v[kBatch][8];
+        uint4 res[kBatch], gat[kBatch];
+#pragma unroll
+        for (int i = 0; i < kBatch; ++i) {
+            const int r = rb + i * kRowStep;
+            const int64_t m = m0 + r;
+            if (r < BM && m < M) {
+                const f32x4_t lo = *reinterpret_cast<const f32x4_t*>(ctile + r * kCRow + ch * 8);
+                const f32x4_t hi = *reinterpret_cast<const f32x4_t*>(ctile + r * kCRow + ch * 8 + 4);
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    v[i][q] = lo[q];
+                    v[i][4 + q] = hi[q];
+                }
+                if (MODE == EPI_RESIDUAL || MODE == EPI_GATED)
+                    res[i] = *reinterpret_cast<const uint4*>(e.residual + m * e.ld_out + n);
+                if (MODE == EPI_ROW_ADD)
+                    res[i] = *reinterpret_cast<const uint4*>(e.row_add + (m % e.row_add_period) * N + n);
+                if (MODE == EPI_GATED && !gate_uniform)
+                    gat[i] = *reinterpret_cast<const uint4*>(e.gate + (m / e.gate_rows) * N + n);
             }
-            store_oct<ACT, MODE>(e, out, m, n, N, v);
+        }
+#pragma unroll
+        for (int i = 0; i < kBatch; ++i) {
+            const int r = rb + i * kRowStep;
+            const int64_t m = m0 + r;
+            if (r >= BM || m >= M) continue;
+            float x[8], t[8];
+#pragma unroll
+            for (int q = 0; q < 8; ++q) x[q] = act_fast<ACT>(e.bias ? __fadd_rn(v[i][q], bias[q]) : v[i][q]);
+            if (MODE != EPI_STORE && e.round_mid)
+#pragma unroll
+                for (int q = 0; q < 8; ++q) x[q] = round_bf16(x[q]);
+            if (MODE == EPI_ROW_ADD) {
+                unpack8(res[i], t);
+#pragma unroll
+                for (int q = 0; q < 8; ++q) x[q] = __fadd_rn(x[q], t[q]);
+            }
+            if (MODE == EPI_RESIDUAL) {
+                unpack8(res[i], t);
+#pragma unroll
+                for (int q = 0; q < 8; ++q) x[q] = __fadd_rn(t[q], x[q]);
+            }
+            if (MODE == EPI_GATED) {
+                float gq[8];
+                if (gate_uniform)
+#pragma unroll
+                    for (int q = 0; q < 8; ++q) gq[q] = gate_t[q];
+                else unpack8(gat[i], gq);
+                unpack8(res[i], t);
+#pragma unroll
+                for (int q = 0; q < 8; ++q) x[q] = __fadd_rn(__fmul_rn(x[q], gq[q]), t[q]);
+            }
+            *reinterpret_cast<uint4*>(out + m * e.ld_out + n) = pack8(x);
         }
     }
 }
