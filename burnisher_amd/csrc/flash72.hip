@@ -3,19 +3,27 @@
 //   out = softmax(scale * Q K^T, key mask) V over head-last [batch, seq, heads, 72] Q and K, and
 //   V supplied TRANSPOSED: vt[((b * heads + h) * 72 + d) * vt_ld + kv], zero past kv_len.
 //
-// Workgroup: 4 waves, 256 queries of one (batch, head); wave w owns queries 64w..64w+63 as four
-// 16-query tiles. Keys stream in blocks of 64 through three LDS stages filled by direct
-// global->LDS loads (global_load_lds_dwordx4), two blocks in flight behind the one in use.
+// Workgroup: 8 waves, 512 queries of one (batch, head); wave w owns queries 64w..64w+63 as four
+// 16-query tiles. Keys stream in blocks of 64 through FOUR LDS stages filled by direct
+// global->LDS loads (global_load_lds_dwordx4).
 //
 // Both products run on v_mfma_f32_16x16x32_bf16 with the score matrix TRANSPOSED:
 //   S^T[kv, q]  = K[kv, :] . Q[q, :]^T      A = K fragment (LDS), B = Q fragment (registers)
 //   O^T[d, q]  += V^T[d, kv] . P^T[kv, q]   A = V^T fragment (LDS), B = P (registers)
-// The S^T accumulator gives each lane four consecutive keys of one query; two such tiles are
-// exactly that lane's 8-element B operand of the second product, with the keys in an order the
-// V^T fragment reads in the same order, so P never leaves registers. head_dim 72 is padded to
-// 96 for the score product (the padding lanes of K are zeroed in registers, Q's in its load) and
-// to 80 for the output: V^T rows 72..79 sit in LDS with row 72 all ONES, so O^T row 72 is the
-// softmax denominator sum_kv P[kv] for free, accumulated from the same bf16 P as the numerator.
+// The S^T accumulator gives each lane four consecutive keys of one query. One v_permlane16_swap
+// between the two score tiles of a 32-key chunk hands every lane EIGHT consecutive keys (the
+// 8-key groups in the order 0, 2, 1, 3 across the lane groups), which is its B operand of the
+// second product as it stands; the matching V^T fragment is one 16-byte LDS read. head_dim 72 is
+// padded to 96 for the score product (Q is zero in the padding, so whatever finite K bytes sit
+// there vanish) and to 80 for the output: V^T rows 72..79 sit in LDS with row 72 all ONES, so O^T
+// row 72 is the softmax denominator sum_kv P[kv], accumulated from the same bf16 P as the
+// numerator.
+//
+// Schedule: a wave alternates a matrix phase (the output product of block j-1, then the scores of
+// block j: 88 MFMAs) and a vector phase (softmax of block j: maximum, exp2, conversion to bf16).
+// Waves 0-3 and 4-7 run one phase apart, separated by a workgroup barrier per phase, so on every
+// SIMD one wave's exponentials overlap the other wave's MFMAs. Waves 4-7 also issue the DMA, at
+// the end of their vector phases.
 //
 // Softmax: scores stay fp32; exp2(s * scale * log2e - m) with the running maximum m kept in those
 // units. The maximum is only moved (and O rescaled by exp2(m_old - m_new)) when a block's maximum
@@ -36,10 +44,10 @@ namespace bh {
 namespace {
 
 constexpr int D = 72;
-constexpr int kWaves = 4;
+constexpr int kWaves = 8;
 constexpr int kThreads = kWaves * 64;
 constexpr int kQPerWave = 64;
-constexpr int kQPerWg = kWaves * kQPerWave;   // 256
+constexpr int kQPerWg = kWaves * kQPerWave;   // 512
 constexpr int kKV = 64;                       // keys per block
 constexpr int kQT = 4;                        // 16-query tiles per wave
 constexpr int kKT = 4;                        // 16-key tiles per block
@@ -49,6 +57,8 @@ constexpr int kVRows = 80;                    // 72 dims + the ones row + zero r
 constexpr int kVBytes = kVRows * 128;         // 128 bytes = 64 keys per V^T row
 constexpr int kSpareBytes = 2 * 1024;
 constexpr int kStage = kKBytes + kVBytes + kSpareBytes;   // 21504
+constexpr int kStages = 4;
+constexpr int kDmaWaves = 4;                  // waves 4-7 issue the DMA
 constexpr int kDmaPerWave = 5;                // 9 K + 9 V^T + 2 spare blocks over 4 waves
 constexpr int kMaxBlocks = 256;               // kv_len <= 16384 (the 2048px token count)
 constexpr float kRescaleThreshold = 8.0f;     // log2 units
@@ -85,52 +95,56 @@ __device__ __forceinline__ void dma16(const void* src, const char* lds) {
 // joins the workgroup; the empty asm statements keep every LDS access on its side.
 template <int N>
 __device__ __forceinline__ void wait_and_join() {
+    // sched_barrier: no instruction, MFMAs included, is moved across (the memory clobbers only
+    // pin memory operations), so each phase's work stays between its two barriers
+    __builtin_amdgcn_sched_barrier(0);
     asm volatile("" ::: "memory");
     s_waitcnt<N, 0>();
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
 }
 
 // The key blocks stream into `stage` as K rows (144 bytes each, contiguous) in DMA blocks 0..8
 // and V^T rows 0..71 (128 bytes = the block's 64 keys, 16-byte chunk c of row d stored at slot
-// c ^ ((d >> 1) & 7)) in blocks 9..17, spread over the waves: instruction i of wave w carries
-// block 4i + w. Blocks 18-19 re-load block 0 into the spare area so every wave issues exactly
-// kDmaPerWave instructions. Which kind an instruction is depends only on (i, wave), so the
-// branch on it is scalar. DmaPlan holds this lane's element offset for each instruction at key
-// block 0 (for K items including its row's stride), so a block costs one 64-bit add per
-// instruction, plus a clamp of the row for the partial last block of a masked run.
+// c ^ ((d >> 1) & 7)) in blocks 9..17, spread over the four DMA waves: instruction i of DMA wave
+// w carries block 4i + w. Blocks 18-19 re-load block 0 into the spare area so every wave issues
+// exactly kDmaPerWave instructions. Which kind an instruction is depends only on (i, wave), so
+// the branch on it is scalar. DmaPlan holds this lane's element offset for each instruction at
+// key 0, relative to the (b, h) base of K or V^T, in 32 bits (the launcher checks that it
+// fits); a block then costs one add per instruction.
 struct DmaPlan {
-    int64_t off[kDmaPerWave];
-    int krow[kDmaPerWave];       // K items: the row within the block
+    int off[kDmaPerWave];
 };
 
 __device__ __forceinline__ bool dma_is_v(int i, int wave) {
-    const int item = i * kWaves + wave;
+    const int item = i * kDmaWaves + wave;
     return item >= 9 && item < 18;
 }
 __device__ __forceinline__ int dma_dst(int i, int wave) {
-    const int item = i * kWaves + wave;
+    const int item = i * kDmaWaves + wave;
     return item < 9 ? item * 1024 : item < 18 ? kKBytes + (item - 9) * 1024
                                               : kKBytes + kVBytes + (item - 18) * 1024;
 }
+// K items: this lane's row within the block
+__device__ __forceinline__ int dma_krow(int i, int wave, int lane) {
+    const int item = i * kDmaWaves + wave;
+    return ((item < 9 ? item : 0) * 64 + lane) / 9;
+}
 
-__device__ __forceinline__ DmaPlan dma_plan(const Flash72Args& a, int b, int h, int wave, int lane) {
+__device__ __forceinline__ DmaPlan dma_plan(const Flash72Args& a, int wave, int lane) {
     DmaPlan p;
 #pragma unroll
     for (int i = 0; i < kDmaPerWave; ++i) {
-        const int item = i * kWaves + wave;            // wave-uniform
+        const int item = i * kDmaWaves + wave;
         if (dma_is_v(i, wave)) {
-            const int vi = item - 9;
-            const int d = vi * 8 + (lane >> 3);
+            const int d = (item - 9) * 8 + (lane >> 3);
             const int c = (lane & 7) ^ ((d >> 1) & 7);
-            p.off[i] = ((static_cast<int64_t>(b) * a.H + h) * D + d) * a.vt_ld + c * 8;
-            p.krow[i] = 0;
+            p.off[i] = d * static_cast<int>(a.vt_ld) + c * 8;
         } else {
-            const int ki = item < 9 ? item : 0;        // spares (18, 19) re-load K block 0
-            const int lg = ki * 64 + lane;
+            const int lg = (item < 9 ? item : 0) * 64 + lane;   // spares (18, 19) re-load block 0
             const int row = lg / 9, ch = lg - row * 9;
-            p.off[i] = (static_cast<int64_t>(b) * a.Skv + row) * a.ld_k + h * D + ch * 8;
-            p.krow[i] = row;
+            p.off[i] = row * static_cast<int>(a.ld_k) + ch * 8;
         }
     }
     return p;
@@ -139,18 +153,19 @@ __device__ __forceinline__ DmaPlan dma_plan(const Flash72Args& a, int b, int h, 
 // Key block starting at key kv0 into `stage`. `partial`: the block runs past the last key, whose
 // row then stands in for the missing ones (their scores are masked).
 __device__ __forceinline__ void dma_block(char* stage, const Flash72Args& a, const DmaPlan& p,
-                                          int wave, int kv0, bool partial) {
-    const int64_t kstep = static_cast<int64_t>(kv0) * a.ld_k;
+                                          const bf16_t* kbh, const bf16_t* vbh, int wave, int lane,
+                                          int kv0, bool partial) {
 #pragma unroll
     for (int i = 0; i < kDmaPerWave; ++i) {
         const bf16_t* src;
         if (dma_is_v(i, wave)) {
-            src = a.vt + p.off[i] + kv0;
+            src = vbh + (p.off[i] + kv0);
         } else if (!partial) {
-            src = a.k + p.off[i] + kstep;
+            src = kbh + (p.off[i] + kv0 * static_cast<int>(a.ld_k));
         } else {
-            const int key = min(kv0 + p.krow[i], a.Skv - 1);
-            src = a.k + p.off[i] + (static_cast<int64_t>(key) - p.krow[i]) * a.ld_k;
+            const int row = dma_krow(i, wave, lane);
+            const int key = min(kv0 + row, a.Skv - 1);
+            src = kbh + (p.off[i] + (key - row) * static_cast<int>(a.ld_k));
         }
         dma16(src, stage + dma_dst(i, wave));
     }
@@ -167,9 +182,182 @@ __device__ __forceinline__ bf16x8_t ld_frag(const char* p) {
     return *reinterpret_cast<const bf16x8_t*>(p);
 }
 
+// Per-wave state of the pipeline.
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+struct WaveState {
+    bf16x8_t qf[kQT][3];       // Q fragments: tile u, K=32 step ks covers dims 32ks + 8g .. +7
+    f32x4_t o[5][kQT];         // O^T accumulators: rows 16e + 4g .. +3 (row 72 = denominator)
+    f32x4_t s[kKT][kQT];       // S^T of the current block: key 16t + 4g + r, query 16u + lr
+    bf16x8_t pf[kQT][2];       // P of the previous block, as the second product's B operand
+    float mc[kQT];             // running maximum (scaled, log2 units), per query of the lane
+};
+
+// The matrix phase: O^T += V^T P^T for the block whose P is in w.pf (OUT: 40 MFMAs, V^T from
+// `vstage`), then the scores of the next block (SCORES: 48 MFMAs, K from `kstage`) into w.s.
+//   output: for each V^T fragment (row block e, 32-key chunk cc), four MFMAs (query tiles u);
+//           `vbase[cc]`: this lane's byte offset of its V^T chunk at row block 0 (e adds 16 rows).
+//   scores: three K=32 steps over dims 0..95 (Q zero past 71, so whatever finite K bytes sit
+//           there vanish), step-outer so that four independent MFMAs separate the dependent
+//           ones; all three of an accumulator have one shape, which the matrix core forwards
+//           back to back. `kbase`: this lane's byte offset of its K chunk (row lane%16, chunk
+//           lane/16) at key tile 0 (key tile t adds 16 rows, step ks 64 bytes).
+// Fragments are read ahead of their MFMAs: V^T three fragments ahead, K one key tile ahead, the
+// first two K tiles during the last output MFMAs. The sched_group_barrier sequence pins that
+// order (left alone, the scheduler sinks each read next to its first use and the wave waits out
+// the LDS latency in front of every group).
+template <bool OUT, bool SCORES>
+__device__ __forceinline__ void matrix_phase(WaveState& w, const char* vstage, const int (&vbase)[2],
+                                             const char* kstage, int kbase) {
+    constexpr int kVF = 10;   // V^T fragments (e, cc)
+    bf16x8_t vf[kVF];
+    bf16x8_t kf[kKT][3];
+    auto read_v = [&](int i) { vf[i] = ld_frag(vstage + vbase[i & 1] + (i >> 1) * 16 * 128); };
+    auto read_k = [&](int t) {
+#pragma unroll
+        for (int ks = 0; ks < 3; ++ks) kf[t][ks] = ld_frag(kstage + kbase + t * 16 * kKRow + ks * 64);
+    };
+    if (OUT) {
+        read_v(0);
+        read_v(1);
+        read_v(2);
+#pragma unroll
+        for (int i = 0; i < kVF; ++i) {
+#pragma unroll
+            for (int u = 0; u < kQT; ++u)
+                w.o[i >> 1][u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf[i], w.pf[u][i & 1], w.o[i >> 1][u], 0, 0, 0);
+            if (i + 3 < kVF) read_v(i + 3);
+            else if (SCORES && i + 3 - kVF < 2) read_k(i + 3 - kVF);
+        }
+    } else if (SCORES) {
+        read_k(0);
+        read_k(1);
+    }
+    if (SCORES) {
+#pragma unroll
+        for (int t = 0; t < kKT; ++t) {
+#pragma unroll
+            for (int ks = 0; ks < 3; ++ks)
+#pragma unroll
+                for (int u = 0; u < kQT; ++u)
+                    w.s[t][u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                        kf[t][ks], w.qf[u][ks], ks == 0 ? f32x4_t{0.f, 0.f, 0.f, 0.f} : w.s[t][u], 0, 0, 0);
+            if (t + 2 < kKT) read_k(t + 2);
+        }
+    }
+    // the issue order
+    if (OUT) {
+        __builtin_amdgcn_sched_group_barrier(0x100, 3, 0);
+#pragma unroll
+        for (int i = 0; i < kVF; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, kQT, 0);
+            if (i + 3 < kVF) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            else if (SCORES && i + 3 - kVF < 2) __builtin_amdgcn_sched_group_barrier(0x100, 3, 0);
+        }
+    } else if (SCORES) {
+        __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);
+    }
+    if (SCORES) {
+#pragma unroll
+        for (int t = 0; t < kKT; ++t) {
+            if (t + 2 < kKT) {
+#pragma unroll
+                for (int ks = 0; ks < 3; ++ks) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, kQT, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                }
+            } else {
+                __builtin_amdgcn_sched_group_barrier(0x008, 3 * kQT, 0);
+            }
+        }
+    }
+}
+
+__device__ __forceinline__ float lane_max2(float m, bool swap32) {
+    const uint32_t x = __float_as_uint(m);
+    const auto r = swap32 ? __builtin_amdgcn_permlane32_swap(x, x, false, false)
+                          : __builtin_amdgcn_permlane16_swap(x, x, false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+// Softmax of the block whose scores are in w.s: masking, the block maximum (the 64 keys of a
+// query sit in lanes lr, lr+16, lr+32, lr+48), the lazy rescale, P = exp2(s c - m) in bf16,
+// regrouped into w.pf.
+template <bool MASKED>
+__device__ __forceinline__ void softmax(WaveState& w, const Flash72Args& a, int blk,
+                                        unsigned long long bits_all, bool all_masked, int g) {
+    if (MASKED) {
+        const unsigned long long bits = bits_all >> (4 * g);
+        const unsigned long long inrange =
+            (blk * kKV + kKV <= a.Skv) ? ~0ull : (((1ull << (a.Skv - blk * kKV)) - 1ull) >> (4 * g));
+#pragma unroll
+        for (int t = 0; t < kKT; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int bit = 16 * t + r;
+                const bool ok = all_masked ? ((inrange >> bit) & 1ull) : ((bits >> bit) & 1ull);
+#pragma unroll
+                for (int u = 0; u < kQT; ++u) {
+                    const float v = all_masked ? 0.0f : w.s[t][u][r];
+                    w.s[t][u][r] = ok ? v : -INFINITY;
+                }
+            }
+    }
+    float lmc[kQT];
+    bool need = false;
+#pragma unroll
+    for (int u = 0; u < kQT; ++u) {
+        float m = max3(w.s[0][u][0], w.s[0][u][1], w.s[0][u][2]);
+        m = max3(m, w.s[0][u][3], w.s[1][u][0]);
+        m = max3(m, w.s[1][u][1], w.s[1][u][2]);
+        m = max3(m, w.s[1][u][3], w.s[2][u][0]);
+        m = max3(m, w.s[2][u][1], w.s[2][u][2]);
+        m = max3(m, w.s[2][u][3], w.s[3][u][0]);
+        m = max3(m, w.s[3][u][1], w.s[3][u][2]);
+        m = fmaxf(m, w.s[3][u][3]);
+        m = lane_max2(m, true);
+        m = lane_max2(m, false);
+        lmc[u] = m * a.c;
+        need |= lmc[u] > w.mc[u] + kRescaleThreshold;
+    }
+    if (__any(need)) {
+#pragma unroll
+        for (int u = 0; u < kQT; ++u) {
+            const float mn = fmaxf(w.mc[u], lmc[u]);
+            const float alpha = __builtin_amdgcn_exp2f(w.mc[u] - mn);
+            w.mc[u] = mn;
+#pragma unroll
+            for (int e = 0; e < 5; ++e)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) w.o[e][u][r] *= alpha;
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < kQT; ++u)
+#pragma unroll
+        for (int cc = 0; cc < 2; ++cc) {
+            uint32_t x[2], y[2];   // key tiles 2cc and 2cc+1, bf16 pairs of keys (4g, 4g+1), (4g+2, 4g+3)
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                bf16x2_t px, py;   // v_cvt_pk_bf16_f32: round to nearest even (P is finite)
+                px[0] = static_cast<__bf16>(__builtin_amdgcn_exp2f(__builtin_fmaf(w.s[2 * cc][u][2 * h], a.c, -w.mc[u])));
+                px[1] = static_cast<__bf16>(__builtin_amdgcn_exp2f(__builtin_fmaf(w.s[2 * cc][u][2 * h + 1], a.c, -w.mc[u])));
+                py[0] = static_cast<__bf16>(__builtin_amdgcn_exp2f(__builtin_fmaf(w.s[2 * cc + 1][u][2 * h], a.c, -w.mc[u])));
+                py[1] = static_cast<__bf16>(__builtin_amdgcn_exp2f(__builtin_fmaf(w.s[2 * cc + 1][u][2 * h + 1], a.c, -w.mc[u])));
+                x[h] = __builtin_bit_cast(uint32_t, px);
+                y[h] = __builtin_bit_cast(uint32_t, py);
+            }
+            // lane group g then holds keys 32cc + 8 kappa(g) .. +7, kappa = (0, 2, 1, 3)
+            const auto r0 = __builtin_amdgcn_permlane16_swap(x[0], y[0], false, false);
+            const auto r1 = __builtin_amdgcn_permlane16_swap(x[1], y[1], false, false);
+            const uint4 packed = make_uint4(r0[0], r1[0], r0[1], r1[1]);
+            w.pf[u][cc] = *reinterpret_cast<const bf16x8_t*>(&packed);
+        }
+}
+
 template <bool MASKED>
 __global__ void __launch_bounds__(kThreads, 1) k_flash72(Flash72Args a) {
-    __shared__ __attribute__((aligned(1024))) char smem[3 * kStage];
+    __shared__ __attribute__((aligned(1024))) char smem[kStages * kStage];
     __shared__ unsigned long long blk_bits[kMaxBlocks];
     __shared__ int live[kMaxBlocks];
     __shared__ int nlive_s, all_masked_s;
@@ -187,22 +375,20 @@ __global__ void __launch_bounds__(kThreads, 1) k_flash72(Flash72Args a) {
     const int q_base = (bid - bh * a.qblocks) * kQPerWg + wave * kQPerWave;
     const int nblk = (a.Skv + kKV - 1) / kKV;
 
-    // ---- Q fragments, resident: tile u, K=32 step ks covers dims 32ks + 8g .. +7 (loaded first,
-    // so their latency overlaps the set-up below) ----
-    bf16x8_t qf[kQT][3];
+    WaveState w;
+    // Q fragments first, so their latency overlaps the set-up below
 #pragma unroll
     for (int u = 0; u < kQT; ++u) {
         const int q = q_base + u * 16 + lr;
+        const bf16_t* qrow = a.q + (static_cast<int64_t>(b) * a.Sq + q) * a.ld_q + h * D;
 #pragma unroll
         for (int ks = 0; ks < 3; ++ks) {
             const int d0 = ks * 32 + g * 8;
             bf16x8_t f;
 #pragma unroll
             for (int e = 0; e < 8; ++e) f[e] = static_cast<__bf16>(0.0f);
-            if (q < a.Sq && d0 < D)
-                f = ld_frag(reinterpret_cast<const char*>(
-                    a.q + (static_cast<int64_t>(b) * a.Sq + q) * a.ld_q + h * D + d0));
-            qf[u][ks] = f;
+            if (q < a.Sq && d0 < D) f = ld_frag(reinterpret_cast<const char*>(qrow + d0));
+            w.qf[u][ks] = f;
         }
     }
 
@@ -221,10 +407,10 @@ __global__ void __launch_bounds__(kThreads, 1) k_flash72(Flash72Args a) {
         }
     }
     // V^T rows 72..79 of every stage: the ones row and zero padding (never written by the DMA)
-    for (int i = threadIdx.x; i < 3 * 8 * 128 / 16; i += kThreads) {
-        const int st = i / 64, w = i - st * 64;   // 64 16-byte words per stage
-        const uint32_t one = w < 8 ? 0x3f803f80u : 0u;
-        *reinterpret_cast<uint4*>(smem + st * kStage + kKBytes + 72 * 128 + w * 16) =
+    for (int i = threadIdx.x; i < kStages * 8 * 128 / 16; i += kThreads) {
+        const int st = i / 64, x = i - st * 64;   // 64 16-byte words per stage
+        const uint32_t one = x < 8 ? 0x3f803f80u : 0u;
+        *reinterpret_cast<uint4*>(smem + st * kStage + kKBytes + 72 * 128 + x * 16) =
             make_uint4(one, one, one, one);
     }
     __syncthreads();
@@ -240,159 +426,91 @@ __global__ void __launch_bounds__(kThreads, 1) k_flash72(Flash72Args a) {
         all_masked_s = all_masked ? 1 : 0;
     }
     __syncthreads();
-    const int nlive = nlive_s;
+    const int n = nlive_s;
     const bool all_masked = MASKED && all_masked_s != 0;
 
     // fragment byte offsets within a stage
-    const int sw = (lr >> 1) & 7;
-    int koff[3];
+    const int kbase = lr * kKRow + g * 16;   // K step 2, g >= 1: the next row's finite bytes (Q is 0)
+    int vbase[2];
+    {
+        const int kappa = ((g & 1) << 1) | (g >> 1);
+        const int sw = (lr >> 1) & 7;
 #pragma unroll
-    for (int ks = 0; ks < 3; ++ks) koff[ks] = lr * kKRow + (ks * 4 + g) * 16;
-    // ks = 2 covers dims 64..95 and only g = 0 (dims 64..71) is real: Q is zero in the other
-    // lanes, and the K bytes read there are the next row's (or, past the last row, V^T's) finite
-    // values, so their products vanish without zeroing K.
-    int voff[2][2];
-#pragma unroll
-    for (int cc = 0; cc < 2; ++cc) {
-        const int q1 = cc * 4 + (g >> 1);
-        voff[cc][0] = kKBytes + lr * 128 + ((q1 ^ sw) << 4) + (g & 1) * 8;
-        voff[cc][1] = kKBytes + lr * 128 + (((q1 + 2) ^ sw) << 4) + (g & 1) * 8;
+        for (int cc = 0; cc < 2; ++cc) vbase[cc] = kKBytes + lr * 128 + (((cc * 4 + kappa) ^ sw) << 4);
     }
-
-    f32x4_t o[5][kQT];
 #pragma unroll
     for (int e = 0; e < 5; ++e)
 #pragma unroll
-        for (int u = 0; u < kQT; ++u) o[e][u] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    float mc[kQT];
+        for (int u = 0; u < kQT; ++u) w.o[e][u] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int u = 0; u < kQT; ++u) mc[u] = -INFINITY;
+    for (int u = 0; u < kQT; ++u) w.mc[u] = -INFINITY;
 
-    // ---- the key-block pipeline ----
     // The Q loads are drained here, where the compiler sees it: otherwise it waits for them
-    // (vmcnt(0), which also drains the DMA in flight) at their first use in every iteration.
+    // (vmcnt(0), which also drains the DMA in flight) at their first use in every phase.
     s_waitcnt<0, 15>();
-    const DmaPlan plan = dma_plan(a, b, h, wave, lane);
-    const int last_full = a.Skv / kKV;   // blocks below this one hold 64 real keys
-    auto issue = [&](char* stage_ptr, int blk) {
-        dma_block(stage_ptr, a, plan, wave, blk * kKV, MASKED && blk >= last_full);
-    };
-    issue(smem, live[0]);
-    issue(smem + kStage, live[min(1, nlive - 1)]);
-    int stage = 0;
-    for (int jj = 0; jj < nlive; ++jj) {
-        wait_and_join<kDmaPerWave>();
-        {
-            const int s2 = stage == 0 ? 2 : stage - 1;
-            issue(smem + s2 * kStage, live[min(jj + 2, nlive - 1)]);
-        }
-        const char* cur = smem + stage * kStage;
-        const int blk = live[jj];
 
-        // S^T tiles: s[t][u][r] = score of key 64 blk + 16t + 4g + r, query tile u column lr
-        f32x4_t s[kKT][kQT];
-#pragma unroll
-        for (int t = 0; t < kKT; ++t) {
-            bf16x8_t kf[3];
-#pragma unroll
-            for (int ks = 0; ks < 3; ++ks) kf[ks] = ld_frag(cur + t * 16 * kKRow + koff[ks]);
-#pragma unroll
-            for (int u = 0; u < kQT; ++u) {
-                f32x4_t acc = f32x4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                for (int ks = 0; ks < 3; ++ks)
-                    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[ks], qf[u][ks], acc, 0, 0, 0);
-                s[t][u] = acc;
-            }
+    // ---- the phases ----
+    // Phase p is bracketed by workgroup barriers. Block j (position j of the live list) sits in
+    // stage j % 4. Waves 0-3 multiply in even phases (2j: output of block j-1, scores of block
+    // j) and run the softmax of block j in phase 2j+1; waves 4-7 are one phase later (matrix in
+    // 2j+1, softmax of block j in 2j+2). Block j's K is read in phases 2j, 2j+1 and its V^T in
+    // 2j+2, 2j+3; in phase 2j+2 waves 4-7 load block j+3 into stage (j+3) % 4, which held block
+    // j-1, last read in phase 2j+1 (a DMA instruction can hold its wave while the address unit
+    // is busy, which costs less at the end of the vector phase than in front of the MFMAs).
+    // Before each even phase 2j they wait until block j has landed (block j+1 may still be in
+    // flight), so every block has four phases to arrive. Past the last block the loads repeat
+    // it, which keeps every wait count identical.
+    auto stage_of = [&](int j) -> char* { return smem + (j & (kStages - 1)) * kStage; };
+    auto bits_of = [&](int j) -> unsigned long long { return MASKED ? blk_bits[live[j]] : ~0ull; };
+    if (wave < kWaves - kDmaWaves) {
+        wait_and_join<63>();                                     // phase 0
+        matrix_phase<false, true>(w, nullptr, vbase, stage_of(0), kbase);
+        for (int j = 1; j < n; ++j) {
+            wait_and_join<63>();                                 // phase 2j-1
+            softmax<MASKED>(w, a, live[j - 1], bits_of(j - 1), all_masked, g);
+            wait_and_join<63>();                                 // phase 2j
+            matrix_phase<true, true>(w, stage_of(j - 1), vbase, stage_of(j), kbase);
         }
-
-        if (MASKED) {
-            const unsigned long long bits = blk_bits[blk] >> (4 * g);
-            const unsigned long long inrange =
-                (blk * kKV + kKV <= a.Skv) ? ~0ull
-                                           : (((1ull << (a.Skv - blk * kKV)) - 1ull) >> (4 * g));
-#pragma unroll
-            for (int t = 0; t < kKT; ++t)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const int bit = 16 * t + r;
-                    const bool ok = all_masked ? ((inrange >> bit) & 1ull) : ((bits >> bit) & 1ull);
-#pragma unroll
-                    for (int u = 0; u < kQT; ++u) {
-                        const float v = all_masked ? 0.0f : s[t][u][r];
-                        s[t][u][r] = ok ? v : -INFINITY;
-                    }
-                }
+        wait_and_join<63>();                                     // phase 2n-1
+        softmax<MASKED>(w, a, live[n - 1], bits_of(n - 1), all_masked, g);
+        wait_and_join<63>();                                     // phase 2n
+        matrix_phase<true, false>(w, stage_of(n - 1), vbase, nullptr, kbase);
+        wait_and_join<63>();                                     // phase 2n+1
+    } else {
+        const int dw = wave - (kWaves - kDmaWaves);
+        const bf16_t* kbh = a.k + static_cast<int64_t>(b) * a.Skv * a.ld_k + h * D;
+        const bf16_t* vbh = a.vt + (static_cast<int64_t>(b) * a.H + h) * D * a.vt_ld;
+        const int last_full = a.Skv / kKV;   // blocks below this one hold 64 real keys
+        const DmaPlan plan = dma_plan(a, dw, lane);
+        auto issue = [&](int j) {
+            const int blk = live[min(j, n - 1)];
+            dma_block(stage_of(j), a, plan, kbh, vbh, dw, lane, blk * kKV, MASKED && blk >= last_full);
+        };
+        issue(0);
+        issue(1);
+        wait_and_join<kDmaPerWave>();                            // phase 0
+        issue(2);
+        wait_and_join<63>();                                     // phase 1
+        matrix_phase<false, true>(w, nullptr, vbase, stage_of(0), kbase);
+        wait_and_join<kDmaPerWave>();                            // phase 2
+        softmax<MASKED>(w, a, live[0], bits_of(0), all_masked, g);
+        issue(3);
+        for (int j = 1; j < n; ++j) {
+            wait_and_join<63>();                                 // phase 2j+1
+            matrix_phase<true, true>(w, stage_of(j - 1), vbase, stage_of(j), kbase);
+            wait_and_join<kDmaPerWave>();                        // phase 2j+2
+            softmax<MASKED>(w, a, live[j], bits_of(j), all_masked, g);
+            issue(j + 3);
         }
-
-        // block maximum per query (the 64 keys of a query sit in lanes lr, lr+16, lr+32, lr+48)
-        float lmc[kQT];
-        bool need = false;
-#pragma unroll
-        for (int u = 0; u < kQT; ++u) {
-            float m = max3(s[0][u][0], s[0][u][1], s[0][u][2]);
-            m = max3(m, s[0][u][3], s[1][u][0]);
-            m = max3(m, s[1][u][1], s[1][u][2]);
-            m = max3(m, s[1][u][3], s[2][u][0]);
-            m = max3(m, s[2][u][1], s[2][u][2]);
-            m = max3(m, s[2][u][3], s[3][u][0]);
-            m = max3(m, s[3][u][1], s[3][u][2]);
-            m = max3(m, s[3][u][3], s[3][u][3]);
-            const float m16 = __shfl_xor(m, 16, 64);
-            m = max3(m, m16, m16);
-            const float m32 = __shfl_xor(m, 32, 64);
-            m = max3(m, m32, m32);
-            lmc[u] = m * a.c;
-            need |= lmc[u] > mc[u] + kRescaleThreshold;
-        }
-        if (__any(need)) {
-#pragma unroll
-            for (int u = 0; u < kQT; ++u) {
-                const float mn = fmaxf(mc[u], lmc[u]);
-                const float alpha = __builtin_amdgcn_exp2f(mc[u] - mn);
-                mc[u] = mn;
-#pragma unroll
-                for (int e = 0; e < 5; ++e)
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) o[e][u][r] *= alpha;
-            }
-        }
-
-        // P = exp2(s c - m), to bf16, as the B operand of O^T += V^T P^T (two 32-key chunks)
-        bf16x8_t pf[kQT][2];
-#pragma unroll
-        for (int u = 0; u < kQT; ++u)
-#pragma unroll
-            for (int cc = 0; cc < 2; ++cc)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    pf[u][cc][r] = static_cast<__bf16>(
-                        __builtin_amdgcn_exp2f(__builtin_fmaf(s[2 * cc][u][r], a.c, -mc[u])));
-                    pf[u][cc][4 + r] = static_cast<__bf16>(
-                        __builtin_amdgcn_exp2f(__builtin_fmaf(s[2 * cc + 1][u][r], a.c, -mc[u])));
-                }
-
-#pragma unroll
-        for (int e = 0; e < 5; ++e)
-#pragma unroll
-            for (int cc = 0; cc < 2; ++cc) {
-                const char* vrow = cur + e * 16 * 128;
-                const uint2 lo = *reinterpret_cast<const uint2*>(vrow + voff[cc][0]);
-                const uint2 hi = *reinterpret_cast<const uint2*>(vrow + voff[cc][1]);
-                const uint4 packed = make_uint4(lo.x, lo.y, hi.x, hi.y);
-                const bf16x8_t vf = *reinterpret_cast<const bf16x8_t*>(&packed);
-#pragma unroll
-                for (int u = 0; u < kQT; ++u)
-                    o[e][u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pf[u][cc], o[e][u], 0, 0, 0);
-            }
-        stage = stage == 2 ? 0 : stage + 1;
+        wait_and_join<63>();                                     // phase 2n+1
+        matrix_phase<true, false>(w, stage_of(n - 1), vbase, nullptr, kbase);
+        s_waitcnt<0, 15>();   // the trailing copies
     }
-    s_waitcnt<0, 15>();   // the trailing copies
 
     // ---- normalise and store: lane holds out[q][d..d+3], d = 16e + 4g; O^T row 72 is the sum ----
 #pragma unroll
     for (int u = 0; u < kQT; ++u) {
-        const float l = __shfl(o[4][u][0], 32 + lr, 64);
+        const float l = __shfl(w.o[4][u][0], 32 + lr, 64);
         const int q = q_base + u * 16 + lr;
         if (q >= a.Sq) continue;
         bf16_t* dst = a.out + (static_cast<int64_t>(b) * a.Sq + q) * a.ld_o + h * D;
@@ -400,12 +518,12 @@ __global__ void __launch_bounds__(kThreads, 1) k_flash72(Flash72Args a) {
         for (int e = 0; e < 5; ++e) {
             const int d = e * 16 + g * 4;
             if (d >= D) continue;
-            uint2 w;
-            w.x = static_cast<uint32_t>(f2bf(__fdiv_rn(o[e][u][0], l))) |
-                  (static_cast<uint32_t>(f2bf(__fdiv_rn(o[e][u][1], l))) << 16);
-            w.y = static_cast<uint32_t>(f2bf(__fdiv_rn(o[e][u][2], l))) |
-                  (static_cast<uint32_t>(f2bf(__fdiv_rn(o[e][u][3], l))) << 16);
-            *reinterpret_cast<uint2*>(dst + d) = w;
+            uint2 x;
+            x.x = static_cast<uint32_t>(f2bf(__fdiv_rn(w.o[e][u][0], l))) |
+                  (static_cast<uint32_t>(f2bf(__fdiv_rn(w.o[e][u][1], l))) << 16);
+            x.y = static_cast<uint32_t>(f2bf(__fdiv_rn(w.o[e][u][2], l))) |
+                  (static_cast<uint32_t>(f2bf(__fdiv_rn(w.o[e][u][3], l))) << 16);
+            *reinterpret_cast<uint2*>(dst + d) = x;
         }
     }
 }
@@ -454,6 +572,8 @@ void launch_flash72(const bf16_t* q, int64_t ld_q, const bf16_t* k, int64_t ld_k
     require(kv_len > 0, "attention: kv_len must be positive");
     require(kv_len <= kMaxBlocks * kKV, "attention (head_dim 72): kv_len above 16384");
     require(vt_ld >= flash72_vt_ld(kv_len), "attention (head_dim 72): V^T rows too short");
+    require(kv_len * ld_k < (int64_t{1} << 31) && D * vt_ld < (int64_t{1} << 31),
+            "attention (head_dim 72): one (batch, head) slice of K or V^T spans 2^31 elements");
     Flash72Args a;
     a.q = q;
     a.k = k;
