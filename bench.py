@@ -13,6 +13,8 @@ The JSON line also carries:
   roofline      the dominant kernel (largest share of step time): algorithmic FLOP per launch
                 over its average launch duration, timed live with HIP events around each of its
                 launches in the timed region, against the 2.5166 PFLOP/s dense bf16 MFMA peak;
+                `traffic` is its HBM bytes per launch from the committed rocprofv3 counter
+                summary (profiles/flash72_self_1024_traffic.md);
   step          the whole step's algorithmic FLOP (the reference's accounting,
                 eval/burnscore/geometry.py:275-367) over the measured step time, same peak;
   kernels       per-class time of one separately profiled step (not the timed region);
@@ -39,6 +41,21 @@ REFERENCE_5090_MS = 97.85          # eval/cells/BG-1/reference.json:28 (RTX 5090
 HW = {512: 64, 1024: 128, 2048: 256}
 
 
+# HBM bytes per launch of a kernel, from the rocprofv3 FETCH_SIZE / WRITE_SIZE summaries committed
+# under profiles/ (counter passes cannot run inside this timed program).
+TRAFFIC_PROFILES = {"attention_self": ROOT / "profiles" / "flash72_self_1024_traffic.md"}
+
+
+def traffic_bytes(kernel: str, resolution: int):
+    path = TRAFFIC_PROFILES.get(kernel)
+    if resolution != 1024 or path is None or not path.exists():
+        return None
+    for line in path.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch:"):
+            return int(line.split(":", 1)[1])
+    return None
+
+
 def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
@@ -53,7 +70,35 @@ def parse() -> argparse.Namespace:
     p.add_argument("--batch", type=int, default=2)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--cpu-threads", type=int, default=0)
+    p.add_argument("--probe", choices=["attention_self"],
+                   help="for counter collection: run a 256 MiB device copy (calibration) and the "
+                        "named kernel at the dit-step shape three times each, then exit")
     return p.parse_args()
+
+
+def probe(kernel: str) -> int:
+    """Launches for rocprofv3 --pmc passes (FETCH_SIZE / WRITE_SIZE): a copy of known size, then
+    the kernel, three times each."""
+    import torch
+
+    import burnisher_amd as bh
+
+    bh.check(bh.lib().bh_init(0), "bh_init")
+    gen = torch.Generator(device="cuda").manual_seed(0)
+    src = torch.ones(128 << 20, device="cuda", dtype=torch.bfloat16)   # 256 MiB
+    dst = torch.empty_like(src)
+    batch, tokens, heads, head_dim = 2, 4096, 16, 72
+    q, k, v = (torch.randn(batch, tokens, heads * head_dim, device="cuda", generator=gen).bfloat16()
+               for _ in range(3))
+    out = torch.empty_like(q)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        dst.copy_(src)
+        bh.call("bh_attention", q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), batch,
+                heads, tokens, tokens, head_dim, 0.0, None, None, 0, bh.BF16, None)
+    torch.cuda.synchronize()
+    log(f"probe {kernel}: done")
+    return 0
 
 
 def cpu_baseline(wl, threads: int) -> dict:
@@ -79,6 +124,8 @@ def cpu_baseline(wl, threads: int) -> dict:
 
 def main() -> int:
     args = parse()
+    if args.probe:
+        return probe(args.probe)
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
               "(the dit-step would shard on the CFG batch, see DESIGN.md)", file=sys.stderr)
@@ -179,7 +226,11 @@ def main() -> int:
                    "layers": wl.cfg["num_layers"], "engine": "bh_dit_forward (fused plan)"},
         "roofline": {"bound": "mfma", "kernel": dominant,
                      "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                     "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+                     "traffic": traffic_bytes(dominant, args.resolution),
+                     "traffic_basis": "HBM bytes per launch: rocprofv3 FETCH_SIZE (x2.000) + "
+                                      "WRITE_SIZE (x1.000), each scaled by a 256 MiB copy; "
+                                      "profiles/flash72_self_1024_traffic.md",
                      "avg_launch_us": round(avg_launch_ms * 1e3, 2), "launches": dn.value,
                      "flop_per_launch": work_per_launch},
         "step": {"flop": flops["total"], "tflops": round(step_tflops, 2),

@@ -29,18 +29,46 @@ template <> struct Io<bf16_t> {
     static __device__ __forceinline__ void st(bf16_t* p, int64_t i, float v) { p[i] = f2bf(v); }
 };
 
+// Sum over the 64 lanes of a wave, in VALU cross-lane operations (no LDS round trips): DPP
+// within groups of 4, 8 and 16 lanes, then v_permlane16_swap / v_permlane32_swap across them.
+// Lanes can finish with sums in different orders, so lane 0's total is broadcast: every lane
+// returns the same value.
+template <int CTRL>
+__device__ __forceinline__ double dpp_d(double v) {
+    const uint64_t u = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = __builtin_amdgcn_update_dpp(0u, static_cast<uint32_t>(u), CTRL, 0xf, 0xf, true);
+    const uint32_t hi = __builtin_amdgcn_update_dpp(0u, static_cast<uint32_t>(u >> 32), CTRL, 0xf, 0xf, true);
+    return __builtin_bit_cast(double, (static_cast<uint64_t>(hi) << 32) | lo);
+}
+template <bool SWAP32>
+__device__ __forceinline__ double swap_sum_d(double v) {
+    const uint64_t u = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = static_cast<uint32_t>(u), hi = static_cast<uint32_t>(u >> 32);
+    const auto l = SWAP32 ? __builtin_amdgcn_permlane32_swap(lo, lo, false, false)
+                          : __builtin_amdgcn_permlane16_swap(lo, lo, false, false);
+    const auto h = SWAP32 ? __builtin_amdgcn_permlane32_swap(hi, hi, false, false)
+                          : __builtin_amdgcn_permlane16_swap(hi, hi, false, false);
+    return __builtin_bit_cast(double, (static_cast<uint64_t>(h[0]) << 32) | l[0]) +
+           __builtin_bit_cast(double, (static_cast<uint64_t>(h[1]) << 32) | l[1]);
+}
 __device__ __forceinline__ double wave_sum(double v) {
-#pragma unroll
-    for (int o = kWave / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
-    return v;
+    v += dpp_d<0xB1>(v);    // quad_perm [1, 0, 3, 2]
+    v += dpp_d<0x4E>(v);    // quad_perm [2, 3, 0, 1]
+    v += dpp_d<0x141>(v);   // row_half_mirror: the other quad of the 8
+    v += dpp_d<0x140>(v);   // row_mirror: the other 8 of the 16
+    v = swap_sum_d<false>(v);
+    v = swap_sum_d<true>(v);
+    const uint64_t u = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(u));
+    const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(u >> 32));
+    return __builtin_bit_cast(double, (static_cast<uint64_t>(hi) << 32) | lo);
 }
 
 // 8 bf16 <-> 8 floats through one 16-byte access.
 struct V8 {
     float f[8];
 };
-__device__ __forceinline__ V8 load8(const bf16_t* p) {
-    const uint4 raw = *reinterpret_cast<const uint4*>(p);
+__device__ __forceinline__ V8 unpack_v8(const uint4 raw) {
     V8 r;
     const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
 #pragma unroll
@@ -49,6 +77,9 @@ __device__ __forceinline__ V8 load8(const bf16_t* p) {
         r.f[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
     }
     return r;
+}
+__device__ __forceinline__ V8 load8(const bf16_t* p) {
+    return unpack_v8(*reinterpret_cast<const uint4*>(p));
 }
 __device__ __forceinline__ void store8(bf16_t* p, const V8& v) {
     uint32_t w[4];
@@ -139,24 +170,44 @@ __global__ void __launch_bounds__(256) k_norm_modulate(
     if (row >= rows) return;
     const int nvec = static_cast<int>(cols / 8);
     const bf16_t* xr = x + row * cols;
-    V8 v[NV];
+    // The row stays packed (bf16) in registers and is unpacked where it is used: a small
+    // register footprint keeps enough rows in flight to cover the memory latency.
+    uint4 xv[NV];
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
         const int vi = lane + j * kWave;
-        if (vi < nvec) v[j] = load8(xr + vi * 8);
+        xv[j] = vi < nvec ? *reinterpret_cast<const uint4*>(xr + vi * 8) : make_uint4(0, 0, 0, 0);
+    }
+    const int64_t b = row / tokens;
+    // precomputed shift and scale are loaded before the statistics, so their latency overlaps
+    uint4 shr[NV], scr[NV];
+    if (PRE) {
+#pragma unroll
+        for (int j = 0; j < NV; ++j) {
+            const int vi = lane + j * kWave;
+            if (vi < nvec) {
+                shr[j] = *reinterpret_cast<const uint4*>(shift_src + b * cols + vi * 8);
+                scr[j] = *reinterpret_cast<const uint4*>(scale_src + b * cols + vi * 8);
+            }
+        }
     }
     float fmean, inv;
-    row_stats<NV>(v, nvec, lane, cols, eps, &fmean, &inv);
-    const int64_t b = row / tokens;
+    {
+        V8 v[NV];
+#pragma unroll
+        for (int j = 0; j < NV; ++j) v[j] = unpack_v8(xv[j]);
+        row_stats<NV>(v, nvec, lane, cols, eps, &fmean, &inv);
+    }
     bf16_t* orow = out + row * cols;
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
         const int vi = lane + j * kWave;
         if (vi >= nvec) continue;
+        const V8 xj = unpack_v8(xv[j]);
         V8 sh, sc;
         if (PRE) {
-            sh = load8(shift_src + b * cols + vi * 8);
-            sc = load8(scale_src + b * cols + vi * 8);
+            sh = unpack_v8(shr[j]);
+            sc = unpack_v8(scr[j]);
         } else {
             const V8 ms = load8(mod + b * mod_stride + (shift_src - mod) + vi * 8);
             const V8 mc = load8(mod + b * mod_stride + (scale_src - mod) + vi * 8);
@@ -172,7 +223,7 @@ __global__ void __launch_bounds__(256) k_norm_modulate(
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
             // normed is stored (rounded) by the norm op before modulate reads it.
-            const float nrm = round_bf16(__fmul_rn(__fsub_rn(v[j].f[e], fmean), inv));
+            const float nrm = round_bf16(__fmul_rn(__fsub_rn(xj.f[e], fmean), inv));
             o.f[e] = __fadd_rn(__fmul_rn(nrm, __fadd_rn(1.0f, sc.f[e])), sh.f[e]);
         }
         store8(orow + vi * 8, o);
