@@ -58,6 +58,7 @@ constexpr int kVBytes = kVRows * 128;         // 128 bytes = 64 keys per V^T row
 constexpr int kSpareBytes = 2 * 1024;
 constexpr int kStage = kKBytes + kVBytes + kSpareBytes;   // 21504
 constexpr int kStages = 4;
+constexpr int kResidentBlocks = 7;            // key blocks a resident launch holds (kv_len <= 448)
 constexpr int kDmaWaves = 4;                  // waves 4-7 issue the DMA
 constexpr int kDmaPerWave = 5;                // 9 K + 9 V^T + 2 spare blocks over 4 waves
 constexpr int kMaxBlocks = 256;               // kv_len <= 16384 (the 2048px token count)
@@ -169,6 +170,28 @@ __device__ __forceinline__ void dma_block(char* stage, const Flash72Args& a, con
         }
         dma16(src, stage + dma_dst(i, wave));
     }
+}
+
+// DMA item `item` (0..19) of the key block at kv0 into `stage`, any wave: items 0..8 are K, 9..17
+// V^T, 18..19 spares (see dma_block). Used by the resident variant's one-time prologue.
+__device__ __forceinline__ void dma_item(char* stage, const Flash72Args& a, const bf16_t* kbh,
+                                         const bf16_t* vbh, int item, int lane, int kv0,
+                                         bool partial) {
+    const bf16_t* src;
+    int dst;
+    if (item >= 9 && item < 18) {
+        const int d = (item - 9) * 8 + (lane >> 3);
+        const int c = (lane & 7) ^ ((d >> 1) & 7);
+        src = vbh + (d * static_cast<int>(a.vt_ld) + c * 8 + kv0);
+        dst = kKBytes + (item - 9) * 1024;
+    } else {
+        const int lg = (item < 9 ? item : 0) * 64 + lane;
+        const int row = lg / 9, ch = lg - row * 9;
+        const int key = partial ? min(kv0 + row, a.Skv - 1) : kv0 + row;
+        src = kbh + (key * static_cast<int>(a.ld_k) + ch * 8);
+        dst = item < 9 ? item * 1024 : kKBytes + kVBytes + (item - 18) * 1024;
+    }
+    dma16(src, stage + dst);
 }
 
 // Three-input maximum (v_max3_f32). This file is compiled with -fno-honor-nans: with IEEE NaN
@@ -355,9 +378,13 @@ __device__ __forceinline__ void softmax(WaveState& w, const Flash72Args& a, int 
         }
 }
 
-template <bool MASKED>
+// RESIDENT (kv_len <= 448): every key block is loaded once, up front, into a stage of its own;
+// after one barrier each wave runs its blocks through without further synchronisation (the two
+// waves of a SIMD drift apart, so one's softmax overlaps the other's MFMAs).
+template <bool MASKED, bool RESIDENT>
 __global__ void __launch_bounds__(kThreads, 1) k_flash72(Flash72Args a) {
-    __shared__ __attribute__((aligned(1024))) char smem[kStages * kStage];
+    constexpr int kNumStages = RESIDENT ? kResidentBlocks : kStages;
+    __shared__ __attribute__((aligned(1024))) char smem[kNumStages * kStage];
     __shared__ unsigned long long blk_bits[kMaxBlocks];
     __shared__ int live[kMaxBlocks];
     __shared__ int nlive_s, all_masked_s;
@@ -407,7 +434,7 @@ __global__ void __launch_bounds__(kThreads, 1) k_flash72(Flash72Args a) {
         }
     }
     // V^T rows 72..79 of every stage: the ones row and zero padding (never written by the DMA)
-    for (int i = threadIdx.x; i < kStages * 8 * 128 / 16; i += kThreads) {
+    for (int i = threadIdx.x; i < kNumStages * 8 * 128 / 16; i += kThreads) {
         const int st = i / 64, x = i - st * 64;   // 64 16-byte words per stage
         const uint32_t one = x < 8 ? 0x3f803f80u : 0u;
         *reinterpret_cast<uint4*>(smem + st * kStage + kKBytes + 72 * 128 + x * 16) =
@@ -460,8 +487,28 @@ __global__ void __launch_bounds__(kThreads, 1) k_flash72(Flash72Args a) {
     // Before each even phase 2j they wait until block j has landed (block j+1 may still be in
     // flight), so every block has four phases to arrive. Past the last block the loads repeat
     // it, which keeps every wait count identical.
-    auto stage_of = [&](int j) -> char* { return smem + (j & (kStages - 1)) * kStage; };
     auto bits_of = [&](int j) -> unsigned long long { return MASKED ? blk_bits[live[j]] : ~0ull; };
+    if (RESIDENT) {
+        const bf16_t* kbh = a.k + static_cast<int64_t>(b) * a.Skv * a.ld_k + h * D;
+        const bf16_t* vbh = a.vt + (static_cast<int64_t>(b) * a.H + h) * D * a.vt_ld;
+        const int last_full = a.Skv / kKV;
+        for (int j = 0; j < n; ++j) {
+            const int blk = live[j];
+            for (int item = wave; item < 20; item += kWaves)
+                dma_item(smem + j * kStage, a, kbh, vbh, item, lane, blk * kKV,
+                         MASKED && blk >= last_full);
+        }
+        wait_and_join<0>();
+        auto res_stage = [&](int j) -> char* { return smem + j * kStage; };
+        matrix_phase<false, true>(w, nullptr, vbase, res_stage(0), kbase);
+        softmax<MASKED>(w, a, live[0], bits_of(0), all_masked, g);
+        for (int j = 1; j < n; ++j) {
+            matrix_phase<true, true>(w, res_stage(j - 1), vbase, res_stage(j), kbase);
+            softmax<MASKED>(w, a, live[j], bits_of(j), all_masked, g);
+        }
+        matrix_phase<true, false>(w, res_stage(n - 1), vbase, nullptr, kbase);
+    } else {
+    auto stage_of = [&](int j) -> char* { return smem + (j & (kStages - 1)) * kStage; };
     if (wave < kWaves - kDmaWaves) {
         wait_and_join<63>();                                     // phase 0
         matrix_phase<false, true>(w, nullptr, vbase, stage_of(0), kbase);
@@ -505,6 +552,7 @@ __global__ void __launch_bounds__(kThreads, 1) k_flash72(Flash72Args a) {
         wait_and_join<63>();                                     // phase 2n+1
         matrix_phase<true, false>(w, stage_of(n - 1), vbase, nullptr, kbase);
         s_waitcnt<0, 15>();   // the trailing copies
+    }
     }
 
     // ---- normalise and store: lane holds out[q][d..d+3], d = 16e + 4g; O^T row 72 is the sum ----
@@ -594,8 +642,12 @@ void launch_flash72(const bf16_t* q, int64_t ld_q, const bf16_t* k, int64_t ld_k
     const int grid = a.B * a.H * a.qblocks;
     const double flops = 4.0 * batch * heads * static_cast<double>(q_len) * kv_len * D;
     ProfileScope ps(q_len == kv_len ? K_ATTN_SELF : K_ATTN_CROSS, s, flops);
-    if (key_mask || kv_len % kKV != 0) k_flash72<true><<<grid, kThreads, 0, s>>>(a);
-    else k_flash72<false><<<grid, kThreads, 0, s>>>(a);
+    const bool masked = key_mask || kv_len % kKV != 0;
+    const bool resident = kv_len <= kResidentBlocks * kKV;
+    if (masked && resident) k_flash72<true, true><<<grid, kThreads, 0, s>>>(a);
+    else if (masked) k_flash72<true, false><<<grid, kThreads, 0, s>>>(a);
+    else if (resident) k_flash72<false, true><<<grid, kThreads, 0, s>>>(a);
+    else k_flash72<false, false><<<grid, kThreads, 0, s>>>(a);
     launch_check("attention (flash, head_dim 72)");
 }
 
