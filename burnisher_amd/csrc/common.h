@@ -34,17 +34,20 @@ __host__ __device__ inline float bf2f(bf16_t v) {
 #endif
 }
 
-// Round-to-nearest-even, NaN kept NaN (dtype.h:64-72 semantics).
+// Round-to-nearest-even, NaN kept NaN (dtype.h:64-72 semantics). On the device this is the
+// hardware conversion (v_cvt_pk_bf16_f32, the same rounding, a NaN stays a quiet NaN): the
+// integer form's NaN test compiles to a divergent branch per value, which made every bf16 store
+// epilogue branch-bound.
 __host__ __device__ inline bf16_t f2bf(float f) {
-    uint32_t u;
 #if defined(__HIP_DEVICE_COMPILE__)
-    u = __float_as_uint(f);
+    return __builtin_bit_cast(bf16_t, static_cast<__bf16>(f));
 #else
+    uint32_t u;
     __builtin_memcpy(&u, &f, 4);
-#endif
     if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<bf16_t>((u >> 16) | 0x0040u);
     u += 0x7fffu + ((u >> 16) & 1u);
     return static_cast<bf16_t>(u >> 16);
+#endif
 }
 
 // What a store through the tensor dtype does to a float.
