@@ -17,9 +17,12 @@
 // c ^ ((r >> 1) & 7): the 16 rows one ds_read_b128 fragment touches then cover all 64 banks
 // exactly once, with no padding (padding would break the 1 KiB contiguity of a DMA write).
 //
-// The MFMA is issued with the weight fragment as its first operand, so each lane's accumulator
-// holds four consecutive OUTPUT COLUMNS of one row. The epilogue stages the fp32 tile in LDS and
-// all 512 threads apply bias, activation, residual and gate and store 16 bytes at a time.
+// The kernel is persistent (one workgroup per CU walking its tiles) and the k-tile pipeline
+// runs on across tile boundaries, so the first k-tiles of a CU's next tile load while its
+// consumers store the last one. The consumers store straight from the accumulators: the
+// producers load A rows and B rows in a permuted order (a_row, b_col) chosen so that each lane
+// ends up holding 8 consecutive output columns of 4 consecutive rows, which it finishes (bias,
+// activation, residual, gate) and writes 16 bytes at a time, with no trip through LDS.
 //
 // Tile order is XCD-aware: workgroup i runs on XCD i%8, so tiles are renumbered so that each XCD
 // gets a contiguous band of M-tiles x N-tiles, walked 4 M-tiles at a time, whose A and B panels
@@ -29,6 +32,8 @@
 // (ops_cpu.cpp:60-66); products of bf16 are exact in fp32, so results differ only by fp32
 // accumulation rounding before the single bf16 rounding at the store.
 #include "common.h"
+
+#include <atomic>
 
 namespace bh {
 namespace {
@@ -158,41 +163,82 @@ __device__ __forceinline__ void dma16(const void* src, const char* lds) {
 }
 #pragma clang diagnostic pop
 
-struct TileArgs {
+// ---- which global rows the producers load into which LDS rows ----------------------------------
+//
+// The MFMA is issued with the weight fragment first, so lane (lr = lane % 16, hi = lane / 16) of
+// consumer wave w ends a tile with acc[i][j][t] = C[LDS row 64w + 16i + lr][LDS column 16j + 4hi + t].
+// The producers fill LDS in an order that makes those registers directly storable:
+//  - A: LDS row 64w + 16i + lr holds tile row 64w + 4lr + i, so a lane's four rows are four
+//    consecutive tokens (the transposed V store writes them as one 8-byte run of a V^T row);
+//  - B: LDS row 16j + 4hi + t holds tile column 32(j/2) + 8hi + 4(j%2) + t for j < 8 and
+//    128 + 4hi + t for j = 8. A lane then owns columns 32p + 8hi .. +7 (accumulators j = 2p and
+//    2p+1, p < 4) and 128 + 4hi .. +3 (j = 8) of each of its rows: one 16-byte store per row and
+//    p, and the four lanes of a row cover 64 contiguous bytes.
+__device__ __forceinline__ int a_row(int r) {
+    return (r & ~63) | ((r & 15) << 2) | ((r >> 4) & 3);
+}
+__device__ __forceinline__ int b_col(int n) {
+    const int j = n >> 4, hi = (n >> 2) & 3, t = n & 3;
+    return j < 8 ? ((j >> 1) << 5) | (hi << 3) | ((j & 1) << 2) | t : 128 + (hi << 2) + t;
+}
+
+constexpr int kDmaItems = BM / 32 + (BN / 8 + 3) / 4;   // 13 per wave per k-tile
+
+// Tile v of the launch -> (tm, tn). Workgroup b runs on XCD b % 8 and, persistent, takes tiles
+// b, b + G, b + 2G, ... (G = grid, a multiple of 8 whenever T is), so tiles are renumbered to
+// give each XCD a contiguous band of the M x N tile grid, walked `group_m` M-tiles at a time,
+// whose A and B panels share that XCD's L2.
+__device__ __forceinline__ void tile_origin(int v, int tiles_m, int tiles_n, int group_m,
+                                            int64_t& m0, int64_t& n0) {
+    const int T = tiles_m * tiles_n;
+    if ((T & 7) == 0) v = (v & 7) * (T >> 3) + (v >> 3);
+    const int group_size = group_m * tiles_n;
+    const int g = v / group_size;
+    const int first_m = g * group_m;
+    const int gm = min(tiles_m - first_m, group_m);
+    const int in_group = v - g * group_size;
+    m0 = static_cast<int64_t>(first_m + in_group % gm) * BM;
+    n0 = static_cast<int64_t>(in_group / gm) * BN;
+}
+
+struct Operands {
     const bf16_t* A;
     const bf16_t* B;
     int64_t M, N, K;
-    int64_t m0, n0;
-    int wave, lane;
 };
 
-// DMA item r (0..12) of dma_tile(): r < 8 is A row block 4r + wave, r >= 8 is B row block
-// 4(r-8) + wave, or for the one that does not exist (waves 2-3, r = 12) a duplicate of the last B
-// row block into the stage's spare block.
-__device__ __forceinline__ void dma_item(char* stage, const TileArgs& t, int64_t k0, int r) {
-    const int sub = t.lane >> 3, slot = t.lane & 7;
-    if (r < BM / 32) {
-        const int rb = r * 4 + t.wave;
-        const int row_in = rb * 8 + sub;
-        const int c = slot ^ ((row_in >> 1) & 7);
-        const int64_t row = min(t.m0 + row_in, t.M - 1);
-        dma16(t.A + row * t.K + k0 + c * 8, stage + rb * 1024);
-    } else {
-        const int rb = (r - BM / 32) * 4 + t.wave;
-        const int row_in = min(rb, BN / 8 - 1) * 8 + sub;
-        const int c = slot ^ ((row_in >> 1) & 7);
-        const int64_t row = min(t.n0 + row_in, t.N - 1);
-        // rb == 18 (waves 2-3, last item) lands in the spare block
-        dma16(t.B + row * t.K + k0 + c * 8, stage + kABytes + min(rb, BN / 8) * 1024);
+// This lane's source address (at k = 0) for each of the wave's 13 DMA items of a tile: items
+// r < 8 are A row blocks 4r + wave, r >= 8 are B row blocks 4(r-8) + wave; the one B block that
+// does not exist (waves 2-3, r = 12) repeats the last into the stage's spare block. Each lane
+// moves 16 bytes: LDS row rb*8 + lane/8, swizzled chunk lane%8. Rows past M or N re-read the
+// last valid row; their results are never stored.
+__device__ __forceinline__ void dma_sources(const bf16_t* (&src)[kDmaItems], const Operands& o,
+                                            int64_t m0, int64_t n0, int wave, int lane) {
+    const int sub = lane >> 3, slot = lane & 7;
+#pragma unroll
+    for (int r = 0; r < kDmaItems; ++r) {
+        if (r < BM / 32) {
+            const int row_in = (r * 4 + wave) * 8 + sub;
+            const int c = slot ^ ((row_in >> 1) & 7);
+            const int64_t row = min(m0 + a_row(row_in), o.M - 1);
+            src[r] = o.A + row * o.K + c * 8;
+        } else {
+            const int row_in = min((r - BM / 32) * 4 + wave, BN / 8 - 1) * 8 + sub;
+            const int c = slot ^ ((row_in >> 1) & 7);
+            const int64_t row = min(n0 + b_col(row_in), o.N - 1);
+            src[r] = o.B + row * o.K + c * 8;
+        }
     }
 }
-constexpr int kDmaItems = BM / 32 + (BN / 8 + 3) / 4;   // 13
 
-// The whole k-tile `k0` into one stage: 13 DMA instructions per wave. Rows past M or N re-read
-// the last valid row; their results are never stored.
-__device__ __forceinline__ void dma_tile(char* stage, const TileArgs& t, int64_t k0) {
+// The whole k-tile at `k0` into one stage: 13 DMA instructions per producer wave.
+__device__ __forceinline__ void dma_tile(char* stage, const bf16_t* const (&src)[kDmaItems],
+                                         int64_t k0, int wave) {
 #pragma unroll
-    for (int r = 0; r < kDmaItems; ++r) dma_item(stage, t, k0, r);
+    for (int r = 0; r < kDmaItems; ++r) {
+        const int rb = r < BM / 32 ? r * 4 + wave : min((r - BM / 32) * 4 + wave, BN / 8);
+        dma16(src[r] + k0, stage + (r < BM / 32 ? 0 : kABytes) + rb * 1024);
+    }
 }
 
 // One k-tile of MFMAs for a consumer wave out of `cur`: 4 activation fragments per K=32 half
@@ -238,9 +284,9 @@ __device__ __forceinline__ void consume_tile(f32x4_t (&acc)[kMT][kNT], const cha
     __builtin_amdgcn_sched_group_barrier(0x008, kMT * kNT, 0);
 }
 
-// Waits until this wave has at most N DMA operations outstanding and none of its LDS reads, then
-// joins the workgroup. The empty asm statements are compiler-level memory barriers: no LDS read
-// or DMA may be moved across the wait and the hardware barrier.
+// Waits until this wave has at most N vector-memory operations outstanding and none of its LDS
+// reads, then joins the workgroup. The empty asm statements are compiler-level memory barriers:
+// no LDS read or DMA may be moved across the wait and the hardware barrier.
 template <int N>
 __device__ __forceinline__ void wait_and_join() {
     asm volatile("" ::: "memory");
@@ -249,69 +295,283 @@ __device__ __forceinline__ void wait_and_join() {
     asm volatile("" ::: "memory");
 }
 
-// The kernel is warp-specialised: waves 0-3 are consumers (LDS fragment reads and MFMAs, one
-// per SIMD), waves 4-7 producers (the DMA). A wave issues in order and a DMA instruction holds
-// its wave until the address unit accepts it; in a single-role wave that stall delays the
-// wave's MFMAs, here it only delays the producer, and the consumer on the same SIMD keeps the
-// matrix core busy.
+// The kernel is persistent and warp-specialised: each workgroup walks its tiles, waves 0-3
+// (consumers: LDS fragment reads, MFMAs, the epilogue straight from the accumulators, one per
+// SIMD) and waves 4-7 (producers: the DMA). A wave issues in order and a DMA instruction holds its
+// wave until the address unit accepts it; in a single-role wave that stall delays the wave's
+// MFMAs, here it only delays the producer, and the consumer on the same SIMD keeps the matrix
+// core busy.
 //
-// Per k-tile kt (stage kt % 3), every wave:
-//   producers: wait until tile kt has landed (tile kt+1 may still be in flight)
+// The workgroup's k-tiles are numbered g = 0 .. total-1 across all its tiles (stage g % 3). Per g,
+// every wave:
+//   producers: wait until k-tile g has landed (g+1 may still be in flight)
 //   consumers: wait until their LDS reads of the previous stage are done
 //   barrier
-//   producers: DMA tile kt+2 -> stage (kt+2) % 3 (it held tile kt-1, which every consumer
-//              finished reading before the barrier)
-//   consumers: multiply stage kt % 3
-// so two k-tiles are in flight behind the one being multiplied. The last two steps load a copy
-// of the last k-tile into the stage nobody will read again, which keeps every step's wait count
-// identical.
+//   producers: DMA k-tile g+2 -> stage (g+2) % 3 (it held g-1, which every consumer finished
+//              reading before the barrier)
+//   consumers: multiply stage g % 3; after a tile's last k-tile, its epilogue
+// so while the consumers store one tile, the first two k-tiles of the next are already loading.
+// The last two steps load a copy of the last k-tile into stages nobody reads again, which keeps
+// every step's wait count identical.
 constexpr int kConsumers = 4;
 constexpr int kWgThreads = 2 * kConsumers * 64;   // 512
 
-// The output tile is staged in LDS as fp32 before the epilogue: rows of 144 floats padded to
-// 148 (592 bytes), which makes the consumers' 16-byte writes of 16 rows land on disjoint banks.
+__device__ __forceinline__ void produce(char* smem, const Operands& o, int KT, int my_tiles,
+                                        int tiles_m, int tiles_n, int group_m, int wave, int lane) {
+    const int total = my_tiles * KT;
+    const bf16_t* src[kDmaItems];
+    int it = 0, kt = 0;   // the next k-tile to issue
+    int64_t m0, n0;
+    tile_origin(blockIdx.x, tiles_m, tiles_n, group_m, m0, n0);
+    dma_sources(src, o, m0, n0, wave, lane);
+    auto advance = [&]() {
+        if (++kt == KT) {
+            kt = 0;
+            ++it;
+            tile_origin(blockIdx.x + it * gridDim.x, tiles_m, tiles_n, group_m, m0, n0);
+            dma_sources(src, o, m0, n0, wave, lane);
+        }
+    };
+    dma_tile(smem, src, 0, wave);
+    if (total > 1) advance();
+    dma_tile(smem + kStageBytes, src, static_cast<int64_t>(kt) * BK, wave);
+    int stage = 0;
+    for (int g = 0; g < total; ++g) {
+        wait_and_join<kDmaItems>();
+        if (g + 2 < total) advance();
+        const int s2 = stage == 0 ? 2 : stage - 1;   // (g + 2) % 3
+        dma_tile(smem + s2 * kStageBytes, src, static_cast<int64_t>(kt) * BK, wave);
+        stage = stage == 2 ? 0 : stage + 1;
+    }
+    wait_and_join<0>();   // the trailing copies have landed before the LDS holds the output
+}
+
+// ---- the epilogue, straight from the accumulators ----------------------------------------------
+
+template <int W> struct RawT;
+template <> struct RawT<8> { using type = uint4; };
+template <> struct RawT<4> { using type = uint2; };
+template <int W> using Raw = typename RawT<W>::type;
+
+template <int W>
+__device__ __forceinline__ Raw<W> ld_raw(const bf16_t* p) {
+    return *reinterpret_cast<const Raw<W>*>(p);
+}
+__device__ __forceinline__ void unpack(const uint4& r, float (&f)[8]) { unpack8(r, f); }
+__device__ __forceinline__ void unpack(const uint2& r, float (&f)[4]) {
+    f[0] = __uint_as_float(r.x << 16);
+    f[1] = __uint_as_float(r.x & 0xffff0000u);
+    f[2] = __uint_as_float(r.y << 16);
+    f[3] = __uint_as_float(r.y & 0xffff0000u);
+}
+__device__ __forceinline__ uint32_t pack2(float a, float b) {
+    return static_cast<uint32_t>(f2bf(a)) | (static_cast<uint32_t>(f2bf(b)) << 16);
+}
+__device__ __forceinline__ void pack(const float (&f)[8], uint4& r) { r = pack8(f); }
+__device__ __forceinline__ void pack(const float (&f)[4], uint2& r) {
+    r = make_uint2(pack2(f[0], f[1]), pack2(f[2], f[3]));
+}
+
+// Chunk p of a lane's row: columns 32p + 8hi .. +7 from accumulators 2p, 2p+1 (p < 4), or
+// 128 + 4hi .. +3 from accumulator 8 (p = 4).
+template <int P> constexpr int kW = P < 4 ? 8 : 4;
+template <int P>
+__device__ __forceinline__ int chunk_col(int hi) { return P < 4 ? 32 * P + 8 * hi : 128 + 4 * hi; }
+template <int P>
+__device__ __forceinline__ float acc_at(const f32x4_t (&acc)[kMT][kNT], int i, int q) {
+    if constexpr (P < 4) return q < 4 ? acc[i][2 * P][q] : acc[i][2 * P + 1][q - 4];
+    else return acc[i][8][q];
+}
+
+// Everything chunk p of a lane's four rows reads besides the accumulators, loaded one chunk ahead
+// of its stores (the compiler keeps loads below earlier stores that may alias them; the residual
+// IS the output in the engine's in-place updates). Stores start as early as they can: at the end
+// of a tile every CU stores at once and the epilogue runs at the memory's write rate, so a later
+// first store (all loads first) measured slower.
+template <int MODE, int W>
+struct ChunkIn {
+    Raw<W> bias, gate;
+    Raw<W> row[kMT];    // residual or row_add
+};
+
+template <int MODE, int P>
+__device__ __forceinline__ void chunk_load(ChunkIn<MODE, kW<P>>& in, const Epi& e, int64_t M,
+                                           int64_t N, int64_t mb, int64_t n0, int hi,
+                                           bool gate_uniform) {
+    constexpr int W = kW<P>;
+    const int64_t n = n0 + chunk_col<P>(hi);
+    if (n >= N) return;
+    if (e.bias) in.bias = ld_raw<W>(e.bias + n);
+    if (MODE == EPI_GATED && gate_uniform) in.gate = ld_raw<W>(e.gate + (mb / e.gate_rows) * N + n);
+#pragma unroll
+    for (int i = 0; i < kMT; ++i) {
+        const int64_t m = mb + i;
+        if (m >= M) continue;
+        if (MODE == EPI_RESIDUAL || MODE == EPI_GATED)
+            in.row[i] = ld_raw<W>(e.residual + m * e.ld_out + n);
+        if (MODE == EPI_ROW_ADD) in.row[i] = ld_raw<W>(e.row_add + (m % e.row_add_period) * N + n);
+    }
+}
+
+template <int ACT, int MODE, int P>
+__device__ __forceinline__ void chunk_store(const f32x4_t (&acc)[kMT][kNT],
+                                            const ChunkIn<MODE, kW<P>>& in, const Epi& e,
+                                            bf16_t* out, int64_t M, int64_t N, int64_t mb,
+                                            int64_t n0, int hi, bool gate_uniform) {
+    constexpr int W = kW<P>;
+    const int64_t n = n0 + chunk_col<P>(hi);
+    if (n >= N) return;
+    float b[W], gt[W];
+    if (e.bias) unpack(in.bias, b);
+    if (MODE == EPI_GATED && gate_uniform) unpack(in.gate, gt);
+#pragma unroll
+    for (int i = 0; i < kMT; ++i) {
+        const int64_t m = mb + i;
+        if (m >= M) continue;
+        float x[W], t[W];
+#pragma unroll
+        for (int q = 0; q < W; ++q) {
+            const float v = acc_at<P>(acc, i, q);
+            x[q] = act_fast<ACT>(e.bias ? __fadd_rn(v, b[q]) : v);
+        }
+        if (MODE != EPI_STORE && e.round_mid)
+#pragma unroll
+            for (int q = 0; q < W; ++q) x[q] = round_bf16(x[q]);
+        if (MODE == EPI_ROW_ADD) {
+            unpack(in.row[i], t);
+#pragma unroll
+            for (int q = 0; q < W; ++q) x[q] = __fadd_rn(x[q], t[q]);
+        }
+        if (MODE == EPI_RESIDUAL) {
+            unpack(in.row[i], t);
+#pragma unroll
+            for (int q = 0; q < W; ++q) x[q] = __fadd_rn(t[q], x[q]);
+        }
+        if (MODE == EPI_GATED) {
+            float gq[W];
+            if (gate_uniform) {
+#pragma unroll
+                for (int q = 0; q < W; ++q) gq[q] = gt[q];
+            } else {   // a tile across two gate rows (not in the DiT: gate rows are 4096 tokens)
+                unpack(ld_raw<W>(e.gate + (m / e.gate_rows) * N + n), gq);
+            }
+            unpack(in.row[i], t);
+#pragma unroll
+            for (int q = 0; q < W; ++q) x[q] = __fadd_rn(__fmul_rn(x[q], gq[q]), t[q]);
+        }
+        Raw<W> r;
+        pack(x, r);
+        *reinterpret_cast<Raw<W>*>(out + m * e.ld_out + n) = r;
+    }
+}
+
+// V columns of the fused QKV projection go to V^T (vt[(blk*B + b)*heads + h)*72 + d][token]):
+// a lane's four rows are four consecutive tokens, so each of its columns is one 8-byte store,
+// and the 16 lanes of a column group write 128 contiguous bytes of one V^T row.
+template <int ACT, int P>
+__device__ __forceinline__ void vt_chunk(const f32x4_t (&acc)[kMT][kNT], const Epi& e, int64_t M,
+                                         int64_t N, int64_t mb, int64_t n0, int hi) {
+    constexpr int W = kW<P>;
+    const int col = chunk_col<P>(hi);
+    if (n0 + col >= N) return;
+    float b[W];
+    if (e.bias) unpack(ld_raw<W>(e.bias + n0 + col), b);
+    const int64_t batches = M / e.vt_seq;
+    const int64_t bt = mb / e.vt_seq, tok = mb - bt * e.vt_seq;
+    const bool whole = tok + kMT <= e.vt_seq && mb + kMT <= M;
+    const int vbase = static_cast<int>(n0 % e.vt_period - e.vt_col0) + col;
+    const int64_t blk = n0 / e.vt_period;
+#pragma unroll
+    for (int q = 0; q < W; ++q) {
+        const int vc = vbase + q;
+        const int h = vc / 72, dd = vc - h * 72;   // the vt store is built for head_dim 72
+        float v[kMT];
+#pragma unroll
+        for (int i = 0; i < kMT; ++i) {
+            const float a = acc_at<P>(acc, i, q);
+            v[i] = act_fast<ACT>(e.bias ? __fadd_rn(a, b[q]) : a);
+        }
+        if (whole) {
+            uint2 r;
+            pack(v, r);
+            *reinterpret_cast<uint2*>(e.vt + (((blk * batches + bt) * e.vt_heads + h) * 72 + dd) *
+                                                 e.vt_ld + tok) = r;
+        } else {
+#pragma unroll
+            for (int i = 0; i < kMT; ++i) {
+                const int64_t m = mb + i;
+                if (m >= M) break;
+                const int64_t bj = m / e.vt_seq, tj = m - bj * e.vt_seq;
+                e.vt[(((blk * batches + bj) * e.vt_heads + h) * 72 + dd) * e.vt_ld + tj] = f2bf(v[i]);
+            }
+        }
+    }
+}
+
+template <int ACT, int MODE>
+__device__ __forceinline__ void epilogue(const f32x4_t (&acc)[kMT][kNT], const Epi& e,
+                                         bf16_t* out, int64_t M, int64_t N, int64_t m0,
+                                         int64_t n0, int wave, int lane) {
+    const int lr = lane & 15, hi = lane >> 4;
+    const int64_t mb = m0 + wave * 64 + lr * 4;   // this lane's rows: mb .. mb+3
+    if (MODE == EPI_STORE && e.vt && n0 % e.vt_period >= e.vt_col0) {
+        vt_chunk<ACT, 0>(acc, e, M, N, mb, n0, hi);
+        vt_chunk<ACT, 1>(acc, e, M, N, mb, n0, hi);
+        vt_chunk<ACT, 2>(acc, e, M, N, mb, n0, hi);
+        vt_chunk<ACT, 3>(acc, e, M, N, mb, n0, hi);
+        vt_chunk<ACT, 4>(acc, e, M, N, mb, n0, hi);
+        return;
+    }
+    // gate rows are whole batches of tokens: one gate row per tile unless the tile straddles two
+    const int64_t m_last = min(m0 + BM, M) - 1;
+    const bool gu = MODE == EPI_GATED && m0 / e.gate_rows == m_last / e.gate_rows;
+    ChunkIn<MODE, 8> c0, c1, c2, c3;
+    ChunkIn<MODE, 4> c4;
+    chunk_load<MODE, 0>(c0, e, M, N, mb, n0, hi, gu);
+    chunk_load<MODE, 1>(c1, e, M, N, mb, n0, hi, gu);
+    chunk_store<ACT, MODE, 0>(acc, c0, e, out, M, N, mb, n0, hi, gu);
+    chunk_load<MODE, 2>(c2, e, M, N, mb, n0, hi, gu);
+    chunk_store<ACT, MODE, 1>(acc, c1, e, out, M, N, mb, n0, hi, gu);
+    chunk_load<MODE, 3>(c3, e, M, N, mb, n0, hi, gu);
+    chunk_store<ACT, MODE, 2>(acc, c2, e, out, M, N, mb, n0, hi, gu);
+    chunk_load<MODE, 4>(c4, e, M, N, mb, n0, hi, gu);
+    chunk_store<ACT, MODE, 3>(acc, c3, e, out, M, N, mb, n0, hi, gu);
+    chunk_store<ACT, MODE, 4>(acc, c4, e, out, M, N, mb, n0, hi, gu);
+}
+
+// ---- the last tile's epilogue, staged through LDS ------------------------------------------------
+//
+// After a workgroup's last tile nothing more is loaded, so the whole LDS is free: the consumers
+// park the fp32 tile there and all 512 threads finish it with full-row 16-byte stores (18
+// consecutive lanes per 288-byte output row). When every CU ends its last tile at the same moment
+// (one tile per CU), this epilogue is a burst of HBM traffic, and full rows keep it at the write
+// bandwidth. Rows are 148 floats; 4-float groups are XOR-swizzled by row so the consumers'
+// writes (16 rows 4 apart per quarter-wave) land on disjoint banks.
 constexpr int kCRow = BN + 4;
 static_assert(BM * kCRow * 4 <= 3 * kStageBytes, "fp32 output tile must fit in the stages");
 
-// Consumer wave: the k-loop, then its 64 x 144 accumulators into the LDS output tile.
-__device__ __forceinline__ void consume(char* smem, int KT, int wave, int lane) {
-    const int lr = lane & 15, sw = (lane >> 1) & 7, hi = lane >> 4;
-    const int off0 = lr * kRowBytes + ((hi ^ sw) * 16);
-    const int off1 = lr * kRowBytes + (((4 + hi) ^ sw) * 16);
+__device__ __forceinline__ int ctile_at(int row, int col) {
+    return row * kCRow + (col ^ (((row >> 4) & 3) << 2));
+}
 
-    f32x4_t acc[kMT][kNT];
-#pragma unroll
-    for (int i = 0; i < kMT; ++i)
-#pragma unroll
-        for (int j = 0; j < kNT; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-
-    int stage = 0;
-    for (int kt = 0; kt < KT; ++kt) {
-        wait_and_join<63>();   // only this wave's LDS reads (it issues no DMA)
-        consume_tile(acc, smem + stage * kStageBytes, wave, off0, off1);
-        stage = stage == 2 ? 0 : stage + 1;
-    }
-    wait_and_join<63>();   // every wave is done with the stages (producers drained their DMA)
-
-    // lane holds C[row][col..col+3] for each (i, j)
+__device__ __forceinline__ void park_tile(const f32x4_t (&acc)[kMT][kNT], char* smem, int wave,
+                                          int lane) {
     float* ctile = reinterpret_cast<float*>(smem);
+    const int lr = lane & 15, hi = lane >> 4;
 #pragma unroll
     for (int i = 0; i < kMT; ++i)
 #pragma unroll
         for (int j = 0; j < kNT; ++j) {
-            const int row = wave * 64 + i * 16 + lr, col = j * 16 + hi * 4;
-            *reinterpret_cast<f32x4_t*>(ctile + row * kCRow + col) = acc[i][j];
+            const int row = wave * 64 + lr * 4 + i, col = b_col(j * 16 + hi * 4);
+            *reinterpret_cast<f32x4_t*>(ctile + ctile_at(row, col)) = acc[i][j];
         }
 }
 
-// All 512 threads: the fp32 tile out of LDS, through the epilogue, to global memory in 16-byte
-// stores, 18 consecutive lanes per 288-byte output row (the MFMA layout itself would store
-// 8-byte pieces of 16 rows at a time, which runs at about half the write bandwidth).
 template <int ACT, int MODE>
-__device__ __forceinline__ void store_tile(const char* smem, const Epi& e, bf16_t* out, int64_t M,
-                                           int64_t N, int64_t m0, int64_t n0) {
+__device__ __forceinline__ void store_staged(const char* smem, const Epi& e, bf16_t* out,
+                                             int64_t M, int64_t N, int64_t m0, int64_t n0) {
     const float* ctile = reinterpret_cast<const float*>(smem);
-    if (e.vt && n0 % e.vt_period >= e.vt_col0) {
+    if (MODE == EPI_STORE && e.vt && n0 % e.vt_period >= e.vt_col0) {
         // V columns: 8 consecutive tokens of one column per 16-byte store, consecutive threads
         // along the token axis of one V^T row. A thread keeps its 8-row group (512 threads over
         // 32 groups), so its batch and token are worked out once.
@@ -332,8 +592,8 @@ __device__ __forceinline__ void store_tile(const char* smem, const Epi& e, bf16_
             float v[8];
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
-                v[j] = ctile[(rg * 8 + j) * kCRow + col];
-                if (e.bias) v[j] = __fadd_rn(v[j], bias);
+                const float a = ctile[ctile_at(rg * 8 + j, col)];
+                v[j] = act_fast<ACT>(e.bias ? __fadd_rn(a, bias) : a);
             }
             const int64_t hrow = ((blk * batches + b) * e.vt_heads + h) * 72 + dd;
             if (whole) {
@@ -371,14 +631,14 @@ __device__ __forceinline__ void store_tile(const char* smem, const Epi& e, bf16_
     if (gate_uniform) unpack8(*reinterpret_cast<const uint4*>(e.gate + (m0 / e.gate_rows) * N + n), gate_t);
     for (int rb = r0; rb < BM; rb += kBatch * kRowStep) {
         float v[kBatch][8];
-        uint4 res[kBatch], gat[kBatch];
+        uint4 res[kBatch];
 #pragma unroll
         for (int i = 0; i < kBatch; ++i) {
             const int r = rb + i * kRowStep;
             const int64_t m = m0 + r;
             if (r < BM && m < M) {
-                const f32x4_t lo = *reinterpret_cast<const f32x4_t*>(ctile + r * kCRow + ch * 8);
-                const f32x4_t hi = *reinterpret_cast<const f32x4_t*>(ctile + r * kCRow + ch * 8 + 4);
+                const f32x4_t lo = *reinterpret_cast<const f32x4_t*>(ctile + ctile_at(r, ch * 8));
+                const f32x4_t hi = *reinterpret_cast<const f32x4_t*>(ctile + ctile_at(r, ch * 8 + 4));
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
                     v[i][q] = lo[q];
@@ -388,8 +648,6 @@ __device__ __forceinline__ void store_tile(const char* smem, const Epi& e, bf16_
                     res[i] = *reinterpret_cast<const uint4*>(e.residual + m * e.ld_out + n);
                 if (MODE == EPI_ROW_ADD)
                     res[i] = *reinterpret_cast<const uint4*>(e.row_add + (m % e.row_add_period) * N + n);
-                if (MODE == EPI_GATED && !gate_uniform)
-                    gat[i] = *reinterpret_cast<const uint4*>(e.gate + (m / e.gate_rows) * N + n);
             }
         }
 #pragma unroll
@@ -418,7 +676,8 @@ __device__ __forceinline__ void store_tile(const char* smem, const Epi& e, bf16_
                 if (gate_uniform)
 #pragma unroll
                     for (int q = 0; q < 8; ++q) gq[q] = gate_t[q];
-                else unpack8(gat[i], gq);
+                else   // a tile across two gate rows (not in the DiT: gate rows are 4096 tokens)
+                    unpack8(*reinterpret_cast<const uint4*>(e.gate + (m / e.gate_rows) * N + n), gq);
                 unpack8(res[i], t);
 #pragma unroll
                 for (int q = 0; q < 8; ++q) x[q] = __fadd_rn(__fmul_rn(x[q], gq[q]), t[q]);
@@ -429,59 +688,59 @@ __device__ __forceinline__ void store_tile(const char* smem, const Epi& e, bf16_
 }
 
 template <int ACT, int MODE>
+__device__ __forceinline__ void consume(char* smem, const Epi& e, bf16_t* out, int64_t M,
+                                        int64_t N, int KT, int my_tiles, int tiles_m, int tiles_n,
+                                        int group_m, int wave, int lane) {
+    const int lr = lane & 15, sw = (lane >> 1) & 7, hi = lane >> 4;
+    const int off0 = lr * kRowBytes + ((hi ^ sw) * 16);
+    const int off1 = lr * kRowBytes + (((4 + hi) ^ sw) * 16);
+    int stage = 0;
+    for (int it = 0; it < my_tiles; ++it) {
+        f32x4_t acc[kMT][kNT];
+#pragma unroll
+        for (int i = 0; i < kMT; ++i)
+#pragma unroll
+            for (int j = 0; j < kNT; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        for (int kt = 0; kt < KT; ++kt) {
+            wait_and_join<63>();   // only this wave's LDS reads (its stores need not wait)
+            consume_tile(acc, smem + stage * kStageBytes, wave, off0, off1);
+            stage = stage == 2 ? 0 : stage + 1;
+        }
+        if (it + 1 < my_tiles) {
+            int64_t m0, n0;
+            tile_origin(blockIdx.x + it * gridDim.x, tiles_m, tiles_n, group_m, m0, n0);
+            epilogue<ACT, MODE>(acc, e, out, M, N, m0, n0, wave, lane);
+        } else {
+            wait_and_join<63>();   // the producers' trailing copies have landed
+            park_tile(acc, smem, wave, lane);
+        }
+    }
+}
+
+template <int ACT, int MODE>
 __global__ void __launch_bounds__(kWgThreads, 1)
 k_gemm_tn(const bf16_t* __restrict__ A, const bf16_t* __restrict__ B, bf16_t* out, int64_t M,
           int64_t N, int64_t K, Epi e, int tiles_m, int tiles_n, int group_m) {
     __shared__ __attribute__((aligned(1024))) char smem[3 * kStageBytes];
-
-    // ---- tile selection: XCD-contiguous bands, grouped by `group_m` M-tiles ----
     const int T = tiles_m * tiles_n;
-    int bid = blockIdx.x;
-    if ((T & 7) == 0) bid = (bid & 7) * (T >> 3) + (bid >> 3);
-    const int group_size = group_m * tiles_n;
-    const int g = bid / group_size;
-    const int first_m = g * group_m;
-    const int gm = min(tiles_m - first_m, group_m);
-    const int in_group = bid - g * group_size;
-    const int tm = first_m + in_group % gm;
-    const int tn = in_group / gm;
-
+    const int my_tiles = (T - static_cast<int>(blockIdx.x) + static_cast<int>(gridDim.x) - 1) /
+                         static_cast<int>(gridDim.x);
     // The wave index through readfirstlane: the compiler then knows it is uniform, so the role
     // branch and the DMA's LDS address are scalar.
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     const int KT = static_cast<int>(K / BK);
-
     if (wave >= kConsumers) {
-        // ---- producer ----
-        TileArgs t;
-        t.A = A;
-        t.B = B;
-        t.M = M;
-        t.N = N;
-        t.K = K;
-        t.m0 = static_cast<int64_t>(tm) * BM;
-        t.n0 = static_cast<int64_t>(tn) * BN;
-        t.wave = wave - kConsumers;
-        t.lane = lane;
-        dma_tile(smem, t, 0);
-        dma_tile(smem + kStageBytes, t, static_cast<int64_t>(min(1, KT - 1)) * BK);
-        int stage = 0;
-        for (int kt = 0; kt < KT; ++kt) {
-            wait_and_join<kDmaItems>();
-            const int s2 = stage == 0 ? 2 : stage - 1;   // (kt + 2) % 3
-            dma_tile(smem + s2 * kStageBytes, t, static_cast<int64_t>(min(kt + 2, KT - 1)) * BK);
-            stage = stage == 2 ? 0 : stage + 1;
-        }
-        wait_and_join<0>();   // the two trailing copies have landed before LDS is reused below
+        produce(smem, Operands{A, B, M, N, K}, KT, my_tiles, tiles_m, tiles_n, group_m,
+                wave - kConsumers, lane);
     } else {
-        consume(smem, KT, wave, lane);
+        consume<ACT, MODE>(smem, e, out, M, N, KT, my_tiles, tiles_m, tiles_n, group_m, wave, lane);
     }
-    wait_and_join<63>();   // the staged output tile is complete and visible
-    store_tile<ACT, MODE>(smem, e, out, M, N, static_cast<int64_t>(tm) * BM,
-                          static_cast<int64_t>(tn) * BN);
+    wait_and_join<63>();   // the parked tile is complete and visible
+    int64_t m0, n0;
+    tile_origin(blockIdx.x + (my_tiles - 1) * gridDim.x, tiles_m, tiles_n, group_m, m0, n0);
+    store_staged<ACT, MODE>(smem, e, out, M, N, m0, n0);
 }
-
 
 // ---- small M: one wave per output column, both operands read with 16-byte loads ----
 constexpr int kGemvMaxM = 8;
@@ -642,6 +901,22 @@ __global__ void __launch_bounds__(256) k_gemm_smallk(const bf16_t* __restrict__ 
     *reinterpret_cast<uint4*>(out + static_cast<int64_t>(m) * e.ld_out + n0) = pack8(v);
 }
 
+// Compute units of the current device, looked up once per device.
+int device_cus() {
+    static std::atomic<int> cus[64] = {};
+    int dev = 0;
+    hip_check(hipGetDevice(&dev), "hipGetDevice");
+    require(dev >= 0 && dev < 64, "gemm: device index out of range");
+    int n = cus[dev].load(std::memory_order_relaxed);
+    if (n == 0) {
+        hip_check(hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev),
+                  "hipDeviceGetAttribute");
+        require(n > 0, "gemm: device reports no compute units");
+        cus[dev].store(n, std::memory_order_relaxed);
+    }
+    return n;
+}
+
 bool aligned(const void* p, int bytes) {
     return (reinterpret_cast<uintptr_t>(p) % bytes) == 0;
 }
@@ -651,8 +926,12 @@ void launch_tn(const bf16_t* a, const bf16_t* b, bf16_t* out, int64_t m, int64_t
                const Epi& e, hipStream_t s) {
     const int tiles_m = static_cast<int>((m + BM - 1) / BM);
     const int tiles_n = static_cast<int>((n + BN - 1) / BN);
-    k_gemm_tn<ACT, MODE><<<tiles_m * tiles_n, kWgThreads, 0, s>>>(a, b, out, m, n, k, e, tiles_m,
-                                                                 tiles_n, 4);
+    const int tiles = tiles_m * tiles_n;
+    // One persistent workgroup per CU (the LDS stages allow no second one); with the tile count
+    // a multiple of 8, so is the grid, which the XCD banding relies on.
+    int grid = min(tiles, device_cus() & ~7);
+    if (grid < 8) grid = min(tiles, device_cus());
+    k_gemm_tn<ACT, MODE><<<grid, kWgThreads, 0, s>>>(a, b, out, m, n, k, e, tiles_m, tiles_n, 4);
 }
 
 template <int ACT>
@@ -701,7 +980,7 @@ void launch_gemm_bf16(const bf16_t* a, const bf16_t* b, const bf16_t* bias, bf16
                     ep.vt_col0 < ep.vt_period && ep.vt_seq > 0 && m % ep.vt_seq == 0 &&
                     ep.vt_ld >= ep.vt_seq && ep.vt_heads > 0 && ep.vt_dim > 0 &&
                     ep.vt_dim == 72 && (ep.vt_period - ep.vt_col0) == int64_t{ep.vt_heads} * 72 &&
-                    ep.vt_ld % 8 == 0 && aligned(ep.vt, 16),
+                    ep.vt_ld % 8 == 0 && ep.vt_seq % 4 == 0 && aligned(ep.vt, 16),
                 "gemm: transposed V store geometry");
     }
     const int mode = ep.residual ? (ep.gate ? EPI_GATED : EPI_RESIDUAL)
@@ -730,7 +1009,7 @@ void launch_gemm_bf16(const bf16_t* a, const bf16_t* b, const bf16_t* bias, bf16
         launch_check("gemm (small K)");
         return;
     }
-    if (!k8 || k % BK != 0 || !vec) {
+    if (!k8 || k % BK != 0 || !vec || k == 0) {
         ProfileScope ps(K_GEMM, s, flops);
         const int64_t total = m * n;
         k_gemm_fused_small<<<static_cast<int>((total + 255) / 256), 256, 0, s>>>(a, b, out, m, n,

@@ -67,7 +67,9 @@ GEMM_SHAPES = [(13, 11, 40), (37, 150, 64), (2, 6912, 1152), (5, 1152, 256), (60
                (1024, 1152, 1152), (512, 3456, 1152), (512, 4608, 1152), (256, 1152, 4608),
                (1024, 32, 1152), (2048, 1152, 16), (300, 200, 72),
                # the MFMA kernel with ragged M and N tiles, and k-tile counts of 1, 2 and 5
-               (37, 152, 128), (777, 296, 320), (300, 1152, 64)]
+               (37, 152, 128), (777, 296, 320), (300, 1152, 64),
+               # more tiles than CUs: the persistent loop, whole and ragged tile grids
+               (3072, 3456, 128), (4100, 2312, 64)]
 
 
 @pytest.mark.parametrize("shape", GEMM_SHAPES, ids=lambda s: "x".join(map(str, s)))
