@@ -212,7 +212,14 @@ void launch_chunk(const void* mod, const void* table, void* out, int64_t batch, 
 // Every chunk of every layer at once: out[l][c6][b][ch] = mod[b, c6*ch_n + ch] + tables[l][c6, ch]
 // where tables is `layers` pointers to [6, channels] tables.
 void launch_chunk_all(const bf16_t* mod, const bf16_t* const* tables_dev, bf16_t* out,
-                      int64_t layers, int64_t batch, int64_t channels, hipStream_t s);
+                      float* out_f32, int64_t layers, int64_t batch, int64_t channels,
+                      hipStream_t s);
+// LayerNorm + modulate with float shift and 1 + scale rows ([batch, channels], as k_chunk_all
+// writes them); channels a multiple of 128, at most 4096.
+bool norm_modulate_f32_supported(int64_t channels);
+void launch_norm_modulate_f32(const bf16_t* x, const float* shift, const float* scale1,
+                              bf16_t* out, int64_t batch, int64_t tokens, int64_t channels,
+                              float eps, hipStream_t s);
 void launch_patch(const void* in, void* out, int64_t batch, int64_t channels, int64_t grid,
                   int64_t patch, bool inverse, bool f32, hipStream_t s);
 // Cos-first sinusoidal timestep embedding, fp64, rounded to bf16, broadcast to `batch` rows

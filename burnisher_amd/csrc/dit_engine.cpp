@@ -111,6 +111,7 @@ struct bh_dit {
 
     DevBuf pos_table, patches, x, normed, modded, q, k, v, qkv, ctx, proj, q2, kc, vc, ff0;
     DevBuf temb, h_t, emb_t, silu_t, modulation, cap_h, cap, kv_all, chunks, tables_dev;
+    DevBuf chunks_f32;   // the chunks as floats, scales as 1 + scale (fused norm kernel)
     DevBuf shift, scale, gate, zero, tokens;
     DevBuf w_qkv, b_qkv, w_kv, b_kv;   // repacked weights (fused plan)
     DevBuf vt_self, vt_cross;         // V transposed for the attention kernel (fused plan)
@@ -121,6 +122,10 @@ struct bh_dit {
     DevBuf make(int64_t elems) {
         workspace += elems * 2;
         return DevBuf(static_cast<size_t>(elems) * 2);
+    }
+    DevBuf make_f32(int64_t elems) {
+        workspace += elems * 4;
+        return DevBuf(static_cast<size_t>(elems) * 4);
     }
 };
 
@@ -295,7 +300,7 @@ void forward_fused(bh_dit& e, const void* latent, double t, const void* caption,
     {
         ProfileScope ps(K_ELEMENTWISE, s, 2.0 * (B * 6 * d + L * 6 * d + L * 6 * B * d));
         launch_chunk_all(e.modulation.bf(), static_cast<const bf16_t* const*>(e.tables_dev.p),
-                         e.chunks.bf(), L, B, d, s);
+                         e.chunks.bf(), static_cast<float*>(e.chunks_f32.p), L, B, d, s);
     }
     const float scale = 1.0f / std::sqrt(static_cast<float>(Dh));
     const bool mask_f32 = mask_dtype == BH_F32;
@@ -305,13 +310,17 @@ void forward_fused(bh_dit& e, const void* latent, double t, const void* caption,
         const bf16_t* shift_msa = ch, *scale_msa = ch + B * d, *gate_msa = ch + 2 * B * d;
         const bf16_t* shift_mlp = ch + 3 * B * d, *scale_mlp = ch + 4 * B * d;
         const bf16_t* gate_mlp = ch + 5 * B * d;
+        const float* chf = static_cast<const float*>(e.chunks_f32.p) + l * 6 * B * d;
         const bf16_t* wqkv = e.w_qkv.bf() + l * 3 * d * d;
         const bf16_t* bqkv = e.b_qkv.bf() + l * 3 * d;
 
         // 1. self-attention
         {
             ProfileScope ps(K_NORM, s, 4.0 * M * d);
-            launch_norm_modulate_pre(e.x.bf(), shift_msa, scale_msa, e.modded.bf(), B, N, d, eps, s);
+            if (e.chunks_f32.p)
+                launch_norm_modulate_f32(e.x.bf(), chf, chf + B * d, e.modded.bf(), B, N, d, eps, s);
+            else
+                launch_norm_modulate_pre(e.x.bf(), shift_msa, scale_msa, e.modded.bf(), B, N, d, eps, s);
         }
         {   // Q and K into the [M, 3d] buffer; at head_dim 72, V straight into V^T for the
             // attention kernel (other widths keep V in the buffer for the generic attention)
@@ -365,7 +374,11 @@ void forward_fused(bh_dit& e, const void* latent, double t, const void* caption,
         // 3. feed-forward
         {
             ProfileScope ps(K_NORM, s, 4.0 * M * d);
-            launch_norm_modulate_pre(e.x.bf(), shift_mlp, scale_mlp, e.modded.bf(), B, N, d, eps, s);
+            if (e.chunks_f32.p)
+                launch_norm_modulate_f32(e.x.bf(), chf + 3 * B * d, chf + 4 * B * d, e.modded.bf(), B,
+                                         N, d, eps, s);
+            else
+                launch_norm_modulate_pre(e.x.bf(), shift_mlp, scale_mlp, e.modded.bf(), B, N, d, eps, s);
         }
         {
             SubclassScope sc(K_GEMM_FF0);
@@ -482,6 +495,7 @@ int bh_dit_create(const bh_dit_config* cfg, const bh_dit_weights* w, int64_t bat
             e->q2 = e->make(M * d);
             e->kv_all = e->make(e->Mcap * L * 2 * d);
             e->chunks = e->make(L * 6 * B * d);
+            if (norm_modulate_f32_supported(d)) e->chunks_f32 = e->make_f32(L * 6 * B * d);
             // the head_dim-72 attention reads V transposed, written by the projections' epilogue
             e->vt72 = c.head_dim == 72 && e->N <= 16384 && caption_len <= 16384 && d % 144 == 0;
             if (e->vt72) {

@@ -230,6 +230,114 @@ __global__ void __launch_bounds__(256) k_norm_modulate(
     }
 }
 
+// The engine's LayerNorm + modulate, every lane busy: a row of C = 512 NV + 128 NP channels is
+// NV 16-byte vectors per lane (lane L holds vectors L, L+64, ...) plus NP 4-byte pairs per lane
+// after them (C = 1152: two vectors and one pair, 18 channels per lane, where 16-byte vectors
+// alone would leave three quarters of the lanes idle in the third vector). Shift and 1 + scale
+// arrive as floats (k_chunk_all), so per channel the output costs only the oracle's own
+// operations. One row per wave: all rows are in flight at once (a wave walking two rows with the
+// next one prefetched measured slower).
+
+template <int NV, int NP>
+struct NormRow {
+    static constexpr int kE = NV * 8 + NP * 2;   // channels per lane
+    uint32_t raw[kE / 2];
+    __device__ __forceinline__ void load(const bf16_t* xr, int lane) {
+        constexpr int pair0 = NV * 8 * kWave;
+#pragma unroll
+        for (int j = 0; j < NV; ++j) {
+            const uint4 r = *reinterpret_cast<const uint4*>(xr + (lane + j * kWave) * 8);
+            raw[4 * j] = r.x;
+            raw[4 * j + 1] = r.y;
+            raw[4 * j + 2] = r.z;
+            raw[4 * j + 3] = r.w;
+        }
+#pragma unroll
+        for (int p = 0; p < NP; ++p)
+            raw[4 * NV + p] = *reinterpret_cast<const uint32_t*>(xr + pair0 + (p * kWave + lane) * 2);
+    }
+};
+
+template <int NV, int NP>
+__global__ void __launch_bounds__(256) k_norm_mod_dense(
+    const bf16_t* __restrict__ x, const float* __restrict__ shift, const float* __restrict__ scale1,
+    bf16_t* __restrict__ out, int64_t rows, int64_t tokens, int cols, float eps) {
+    using Row = NormRow<NV, NP>;
+    constexpr int kE = Row::kE;
+    constexpr int pair0 = NV * 8 * kWave;   // first channel of the pairs
+    const int lane = threadIdx.x % kWave;
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * (blockDim.x / kWave) + threadIdx.x / kWave;
+    if (row >= rows) return;
+    Row cur;
+    cur.load(x + row * cols, lane);
+    {
+        const int64_t b = row / tokens;
+        float sh[kE], sc[kE];
+#pragma unroll
+        for (int j = 0; j < NV; ++j) {
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int c = (lane + j * kWave) * 8 + 4 * h;
+                const float4 a = *reinterpret_cast<const float4*>(shift + b * cols + c);
+                const float4 m = *reinterpret_cast<const float4*>(scale1 + b * cols + c);
+                sh[8 * j + 4 * h] = a.x; sh[8 * j + 4 * h + 1] = a.y;
+                sh[8 * j + 4 * h + 2] = a.z; sh[8 * j + 4 * h + 3] = a.w;
+                sc[8 * j + 4 * h] = m.x; sc[8 * j + 4 * h + 1] = m.y;
+                sc[8 * j + 4 * h + 2] = m.z; sc[8 * j + 4 * h + 3] = m.w;
+            }
+        }
+#pragma unroll
+        for (int p = 0; p < NP; ++p) {
+            const int c = pair0 + (p * kWave + lane) * 2;
+            const float2 a = *reinterpret_cast<const float2*>(shift + b * cols + c);
+            const float2 m = *reinterpret_cast<const float2*>(scale1 + b * cols + c);
+            sh[8 * NV + 2 * p] = a.x; sh[8 * NV + 2 * p + 1] = a.y;
+            sc[8 * NV + 2 * p] = m.x; sc[8 * NV + 2 * p + 1] = m.y;
+        }
+        float v[kE];
+#pragma unroll
+        for (int i = 0; i < kE / 2; ++i) {
+            v[2 * i] = __uint_as_float(cur.raw[i] << 16);
+            v[2 * i + 1] = __uint_as_float(cur.raw[i] & 0xffff0000u);
+        }
+        // statistics exactly as the oracle forms them: fp64 mean, fp64 sum of squared deviations
+        double sum = 0.0;
+#pragma unroll
+        for (int e = 0; e < kE; ++e) sum += static_cast<double>(v[e]);
+        const double mean = wave_sum(sum) / static_cast<double>(cols);
+        double q = 0.0;
+#pragma unroll
+        for (int e = 0; e < kE; ++e) {
+            const double d = static_cast<double>(v[e]) - mean;
+            q += d * d;
+        }
+        const double var = wave_sum(q) / static_cast<double>(cols);
+        const float inv = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(static_cast<float>(var), eps)));
+        const float fmean = static_cast<float>(mean);
+        uint32_t o[kE / 2];
+#pragma unroll
+        for (int i = 0; i < kE / 2; ++i) {
+            float r[2];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int e = 2 * i + h;
+                // normed is stored (rounded) by the norm op before modulate reads it
+                const float nrm = round_bf16(__fmul_rn(__fsub_rn(v[e], fmean), inv));
+                r[h] = __fadd_rn(__fmul_rn(nrm, sc[e]), sh[e]);
+            }
+            o[i] = static_cast<uint32_t>(f2bf(r[0])) | (static_cast<uint32_t>(f2bf(r[1])) << 16);
+        }
+        bf16_t* orow = out + row * cols;
+#pragma unroll
+        for (int j = 0; j < NV; ++j)
+            *reinterpret_cast<uint4*>(orow + (lane + j * kWave) * 8) =
+                make_uint4(o[4 * j], o[4 * j + 1], o[4 * j + 2], o[4 * j + 3]);
+#pragma unroll
+        for (int p = 0; p < NP; ++p)
+            *reinterpret_cast<uint32_t*>(orow + pair0 + (p * kWave + lane) * 2) = o[4 * NV + p];
+    }
+}
+
 // ---- modulate (ModulateArgs) ----------------------------------------------------------------
 
 template <typename T>
@@ -302,9 +410,12 @@ __global__ void k_chunk(const T* __restrict__ mod, const T* __restrict__ table, 
     }
 }
 
+// `out_f32` (optional) receives the same chunks as floats for the fused norm kernel, with the
+// scale chunks (1 and 4) already in the form the modulation multiplies by, 1 + scale (the same
+// fp32 addition the modulation would do per element).
 __global__ void k_chunk_all(const bf16_t* __restrict__ mod, const bf16_t* const* __restrict__ tables,
-                            bf16_t* __restrict__ out, int64_t layers, int64_t batch,
-                            int64_t channels) {
+                            bf16_t* __restrict__ out, float* __restrict__ out_f32, int64_t layers,
+                            int64_t batch, int64_t channels) {
     const int64_t per_layer = 6 * batch * channels;
     const int64_t n = layers * per_layer;
     for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < n;
@@ -314,6 +425,7 @@ __global__ void k_chunk_all(const bf16_t* __restrict__ mod, const bf16_t* const*
         const float v = __fadd_rn(bf2f(mod[b * 6 * channels + k * channels + c]),
                                   bf2f(tables[l][k * channels + c]));
         out[i] = f2bf(v);
+        if (out_f32) out_f32[i] = (k == 1 || k == 4) ? __fadd_rn(1.0f, round_bf16(v)) : round_bf16(v);
     }
 }
 
@@ -464,6 +576,41 @@ void launch_norm_modulate_pre(const bf16_t* x, const bf16_t* shift, const bf16_t
                                  batch * tokens, tokens, channels, eps, s);
 }
 
+void launch_norm_modulate_f32(const bf16_t* x, const float* shift, const float* scale1,
+                              bf16_t* out, int64_t batch, int64_t tokens, int64_t channels,
+                              float eps, hipStream_t s) {
+    const int64_t rows = batch * tokens;
+    if (rows == 0) return;
+    require(norm_modulate_f32_supported(channels),
+            "norm_modulate_f32: channels must be a multiple of 128 and at most 4096");
+    require(aligned16(x) && aligned16(out) && aligned16(shift) && aligned16(scale1),
+            "norm_modulate_f32: every operand must be 16-byte aligned");
+    const int nv = static_cast<int>(channels / 512), np = static_cast<int>(channels % 512 / 128);
+    const int grid = static_cast<int>((rows + 3) / 4);
+    const int c = static_cast<int>(channels);
+#define BH_ND(NV, NP)                                                                         \
+    k_norm_mod_dense<NV, NP><<<grid, 256, 0, s>>>(x, shift, scale1, out, rows, tokens, c, eps)
+    switch (nv * 4 + np) {
+#define BH_NV(NV) \
+        case NV * 4 + 0: BH_ND(NV, 0); break; \
+        case NV * 4 + 1: BH_ND(NV, 1); break; \
+        case NV * 4 + 2: BH_ND(NV, 2); break; \
+        case NV * 4 + 3: BH_ND(NV, 3); break;
+        case 1: BH_ND(0, 1); break;
+        case 2: BH_ND(0, 2); break;
+        case 3: BH_ND(0, 3); break;
+        BH_NV(1) BH_NV(2) BH_NV(3) BH_NV(4) BH_NV(5) BH_NV(6) BH_NV(7)
+        default: BH_ND(8, 0); break;
+#undef BH_NV
+    }
+#undef BH_ND
+    launch_check("norm_modulate_f32");
+}
+
+bool norm_modulate_f32_supported(int64_t channels) {
+    return channels > 0 && channels % 128 == 0 && channels <= 4096;
+}
+
 void launch_modulate(const void* x, const void* scale, const void* shift, void* out,
                      int64_t batch, int64_t tokens, int64_t channels, const void* residual,
                      const void* gate, bool f32, hipStream_t s) {
@@ -542,10 +689,11 @@ void launch_chunk(const void* mod, const void* table, void* out, int64_t batch, 
 }
 
 void launch_chunk_all(const bf16_t* mod, const bf16_t* const* tables_dev, bf16_t* out,
-                      int64_t layers, int64_t batch, int64_t channels, hipStream_t s) {
+                      float* out_f32, int64_t layers, int64_t batch, int64_t channels,
+                      hipStream_t s) {
     const int64_t n = layers * 6 * batch * channels;
     if (n == 0) return;
-    k_chunk_all<<<grid_for(n), 256, 0, s>>>(mod, tables_dev, out, layers, batch, channels);
+    k_chunk_all<<<grid_for(n), 256, 0, s>>>(mod, tables_dev, out, out_f32, layers, batch, channels);
     launch_check("chunk_all");
 }
 
