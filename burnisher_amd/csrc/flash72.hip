@@ -26,9 +26,11 @@
 // the end of their vector phases.
 //
 // Softmax: scores stay fp32; exp2(s * scale * log2e - m) with the running maximum m kept in those
-// units. The maximum is only moved (and O rescaled by exp2(m_old - m_new)) when a block's maximum
-// exceeds it by more than 8: any fixed m gives the same normalised result, and the threshold
-// bounds every P by 2^8, far from fp32 range. That keeps the rescale off the common path.
+// units. The first block sets m; a later block moves it (and rescales O by exp2(m_old - m_new))
+// only when one of its scores exceeds it by more than 8: any fixed m gives the same normalised
+// result, and the threshold bounds every P by 2^8, far from fp32 range. The common path then
+// needs no maximum per query at all -- one per lane and a wave vote decide -- which matters
+// because this kernel's vector phase, not its MFMAs, sets the pace.
 //
 // Numerics against the reference oracle (ops_cpu.cpp:84-131): a masked key scores exactly -1e9
 // there, so with any unmasked key in the row its weight exp(-1e9 - max) is exactly 0 -- here it
@@ -308,7 +310,8 @@ __device__ __forceinline__ float lane_max2(float m, bool swap32) {
 // regrouped into w.pf.
 template <bool MASKED>
 __device__ __forceinline__ void softmax(WaveState& w, const Flash72Args& a, int blk,
-                                        unsigned long long bits_all, bool all_masked, int g) {
+                                        unsigned long long bits_all, bool all_masked, int g,
+                                        bool first) {
     if (MASKED) {
         const unsigned long long bits = bits_all >> (4 * g);
         const unsigned long long inrange =
@@ -326,33 +329,72 @@ __device__ __forceinline__ void softmax(WaveState& w, const Flash72Args& a, int 
                 }
             }
     }
-    float lmc[kQT];
-    bool need = false;
-#pragma unroll
-    for (int u = 0; u < kQT; ++u) {
-        float m = max3(w.s[0][u][0], w.s[0][u][1], w.s[0][u][2]);
-        m = max3(m, w.s[0][u][3], w.s[1][u][0]);
-        m = max3(m, w.s[1][u][1], w.s[1][u][2]);
-        m = max3(m, w.s[1][u][3], w.s[2][u][0]);
-        m = max3(m, w.s[2][u][1], w.s[2][u][2]);
-        m = max3(m, w.s[2][u][3], w.s[3][u][0]);
-        m = max3(m, w.s[3][u][1], w.s[3][u][2]);
-        m = fmaxf(m, w.s[3][u][3]);
-        m = lane_max2(m, true);
-        m = lane_max2(m, false);
-        lmc[u] = m * a.c;
-        need |= lmc[u] > w.mc[u] + kRescaleThreshold;
-    }
-    if (__any(need)) {
+    if (first) {
+        // the first block sets the maximum: per query, over its 64 keys (lanes lr + 16 g)
 #pragma unroll
         for (int u = 0; u < kQT; ++u) {
-            const float mn = fmaxf(w.mc[u], lmc[u]);
-            const float alpha = __builtin_amdgcn_exp2f(w.mc[u] - mn);
-            w.mc[u] = mn;
+            float m = max3(w.s[0][u][0], w.s[0][u][1], w.s[0][u][2]);
+            m = max3(m, w.s[0][u][3], w.s[1][u][0]);
+            m = max3(m, w.s[1][u][1], w.s[1][u][2]);
+            m = max3(m, w.s[1][u][3], w.s[2][u][0]);
+            m = max3(m, w.s[2][u][1], w.s[2][u][2]);
+            m = max3(m, w.s[2][u][3], w.s[3][u][0]);
+            m = max3(m, w.s[3][u][1], w.s[3][u][2]);
+            m = fmaxf(m, w.s[3][u][3]);
+            m = lane_max2(m, true);
+            m = lane_max2(m, false);
+            w.mc[u] = m * a.c;
+        }
+    }
+    // x = s c - m in place, in the units of the running maximum
 #pragma unroll
-            for (int e = 0; e < 5; ++e)
+    for (int t = 0; t < kKT; ++t)
 #pragma unroll
-                for (int r = 0; r < 4; ++r) w.o[e][u][r] *= alpha;
+        for (int u = 0; u < kQT; ++u)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) w.s[t][u][r] = __builtin_fmaf(w.s[t][u][r], a.c, -w.mc[u]);
+    if (!first) {
+        // Later blocks move the maximum only when one of their scores exceeds it by more than
+        // the threshold: one maximum over this lane's 64 values and a wave vote decide; the exact
+        // per-query maxima (across lanes) are formed only then.
+        float mx[kKT];
+#pragma unroll
+        for (int t = 0; t < kKT; ++t) {
+            float m = max3(w.s[t][0][0], w.s[t][0][1], w.s[t][0][2]);
+            m = max3(m, w.s[t][0][3], w.s[t][1][0]);
+            m = max3(m, w.s[t][1][1], w.s[t][1][2]);
+            m = max3(m, w.s[t][1][3], w.s[t][2][0]);
+            m = max3(m, w.s[t][2][1], w.s[t][2][2]);
+            m = max3(m, w.s[t][2][3], w.s[t][3][0]);
+            m = max3(m, w.s[t][3][1], w.s[t][3][2]);
+            mx[t] = fmaxf(m, w.s[t][3][3]);
+        }
+        const float m_all = fmaxf(max3(mx[0], mx[1], mx[2]), mx[3]);
+        if (__any(m_all > kRescaleThreshold)) {
+#pragma unroll
+            for (int u = 0; u < kQT; ++u) {
+                float m = max3(w.s[0][u][0], w.s[0][u][1], w.s[0][u][2]);
+                m = max3(m, w.s[0][u][3], w.s[1][u][0]);
+                m = max3(m, w.s[1][u][1], w.s[1][u][2]);
+                m = max3(m, w.s[1][u][3], w.s[2][u][0]);
+                m = max3(m, w.s[2][u][1], w.s[2][u][2]);
+                m = max3(m, w.s[2][u][3], w.s[3][u][0]);
+                m = max3(m, w.s[3][u][1], w.s[3][u][2]);
+                m = fmaxf(m, w.s[3][u][3]);
+                m = lane_max2(m, true);
+                m = lane_max2(m, false);
+                const float dm = fmaxf(m, 0.0f);   // the query's new maximum is mc + dm
+                const float alpha = __builtin_amdgcn_exp2f(-dm);
+                w.mc[u] += dm;
+#pragma unroll
+                for (int e = 0; e < 5; ++e)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) w.o[e][u][r] *= alpha;
+#pragma unroll
+                for (int t = 0; t < kKT; ++t)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) w.s[t][u][r] -= dm;
+            }
         }
     }
 #pragma unroll
@@ -363,10 +405,10 @@ __device__ __forceinline__ void softmax(WaveState& w, const Flash72Args& a, int 
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
                 bf16x2_t px, py;   // v_cvt_pk_bf16_f32: round to nearest even (P is finite)
-                px[0] = static_cast<__bf16>(__builtin_amdgcn_exp2f(__builtin_fmaf(w.s[2 * cc][u][2 * h], a.c, -w.mc[u])));
-                px[1] = static_cast<__bf16>(__builtin_amdgcn_exp2f(__builtin_fmaf(w.s[2 * cc][u][2 * h + 1], a.c, -w.mc[u])));
-                py[0] = static_cast<__bf16>(__builtin_amdgcn_exp2f(__builtin_fmaf(w.s[2 * cc + 1][u][2 * h], a.c, -w.mc[u])));
-                py[1] = static_cast<__bf16>(__builtin_amdgcn_exp2f(__builtin_fmaf(w.s[2 * cc + 1][u][2 * h + 1], a.c, -w.mc[u])));
+                px[0] = static_cast<__bf16>(__builtin_amdgcn_exp2f(w.s[2 * cc][u][2 * h]));
+                px[1] = static_cast<__bf16>(__builtin_amdgcn_exp2f(w.s[2 * cc][u][2 * h + 1]));
+                py[0] = static_cast<__bf16>(__builtin_amdgcn_exp2f(w.s[2 * cc + 1][u][2 * h]));
+                py[1] = static_cast<__bf16>(__builtin_amdgcn_exp2f(w.s[2 * cc + 1][u][2 * h + 1]));
                 x[h] = __builtin_bit_cast(uint32_t, px);
                 y[h] = __builtin_bit_cast(uint32_t, py);
             }
@@ -501,10 +543,10 @@ __global__ void __launch_bounds__(kThreads, 1) k_flash72(Flash72Args a) {
         wait_and_join<0>();
         auto res_stage = [&](int j) -> char* { return smem + j * kStage; };
         matrix_phase<false, true>(w, nullptr, vbase, res_stage(0), kbase);
-        softmax<MASKED>(w, a, live[0], bits_of(0), all_masked, g);
+        softmax<MASKED>(w, a, live[0], bits_of(0), all_masked, g, true);
         for (int j = 1; j < n; ++j) {
             matrix_phase<true, true>(w, res_stage(j - 1), vbase, res_stage(j), kbase);
-            softmax<MASKED>(w, a, live[j], bits_of(j), all_masked, g);
+            softmax<MASKED>(w, a, live[j], bits_of(j), all_masked, g, false);
         }
         matrix_phase<true, false>(w, res_stage(n - 1), vbase, nullptr, kbase);
     } else {
@@ -514,12 +556,12 @@ __global__ void __launch_bounds__(kThreads, 1) k_flash72(Flash72Args a) {
         matrix_phase<false, true>(w, nullptr, vbase, stage_of(0), kbase);
         for (int j = 1; j < n; ++j) {
             wait_and_join<63>();                                 // phase 2j-1
-            softmax<MASKED>(w, a, live[j - 1], bits_of(j - 1), all_masked, g);
+            softmax<MASKED>(w, a, live[j - 1], bits_of(j - 1), all_masked, g, j == 1);
             wait_and_join<63>();                                 // phase 2j
             matrix_phase<true, true>(w, stage_of(j - 1), vbase, stage_of(j), kbase);
         }
         wait_and_join<63>();                                     // phase 2n-1
-        softmax<MASKED>(w, a, live[n - 1], bits_of(n - 1), all_masked, g);
+        softmax<MASKED>(w, a, live[n - 1], bits_of(n - 1), all_masked, g, n == 1);
         wait_and_join<63>();                                     // phase 2n
         matrix_phase<true, false>(w, stage_of(n - 1), vbase, nullptr, kbase);
         wait_and_join<63>();                                     // phase 2n+1
@@ -540,13 +582,13 @@ __global__ void __launch_bounds__(kThreads, 1) k_flash72(Flash72Args a) {
         wait_and_join<63>();                                     // phase 1
         matrix_phase<false, true>(w, nullptr, vbase, stage_of(0), kbase);
         wait_and_join<kDmaPerWave>();                            // phase 2
-        softmax<MASKED>(w, a, live[0], bits_of(0), all_masked, g);
+        softmax<MASKED>(w, a, live[0], bits_of(0), all_masked, g, true);
         issue(3);
         for (int j = 1; j < n; ++j) {
             wait_and_join<63>();                                 // phase 2j+1
             matrix_phase<true, true>(w, stage_of(j - 1), vbase, stage_of(j), kbase);
             wait_and_join<kDmaPerWave>();                        // phase 2j+2
-            softmax<MASKED>(w, a, live[j], bits_of(j), all_masked, g);
+            softmax<MASKED>(w, a, live[j], bits_of(j), all_masked, g, false);
             issue(j + 3);
         }
         wait_and_join<63>();                                     // phase 2n+1
