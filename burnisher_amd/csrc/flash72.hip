@@ -1,7 +1,8 @@
 // Flash attention at head_dim 72 (PixArt-Sigma: 16 heads x 72) on gfx950.
 //
 //   out = softmax(scale * Q K^T, key mask) V over head-last [batch, seq, heads, 72] Q and K, and
-//   V supplied TRANSPOSED: vt[((b * heads + h) * 72 + d) * vt_ld + kv], zero past kv_len.
+//   V supplied TRANSPOSED: vt[((b * heads + h) * 72 + d) * vt_ld + vt_pos(kv)], zero past
+//   kv_len (vt_pos, common.h: keys permuted within 32-key chunks, runs of four kept).
 //
 // Workgroup: 8 waves, 512 queries of one (batch, head); wave w owns queries 64w..64w+63 as four
 // 16-query tiles. Keys stream in blocks of 64 through FOUR LDS stages filled by direct
@@ -10,10 +11,10 @@
 // Both products run on v_mfma_f32_16x16x32_bf16 with the score matrix TRANSPOSED:
 //   S^T[kv, q]  = K[kv, :] . Q[q, :]^T      A = K fragment (LDS), B = Q fragment (registers)
 //   O^T[d, q]  += V^T[d, kv] . P^T[kv, q]   A = V^T fragment (LDS), B = P (registers)
-// The S^T accumulator gives each lane four consecutive keys of one query. One v_permlane16_swap
-// between the two score tiles of a 32-key chunk hands every lane EIGHT consecutive keys (the
-// 8-key groups in the order 0, 2, 1, 3 across the lane groups), which is its B operand of the
-// second product as it stands; the matching V^T fragment is one 16-byte LDS read. head_dim 72 is
+// The S^T accumulator gives each lane four consecutive keys of one query per 16-key tile; with
+// the two tiles of a 32-key chunk, lane group g holds keys 4g..4g+3 and 16+4g..16+4g+3, which
+// is its B operand of the second product as it stands, because V^T keeps exactly those eight
+// keys together (vt_pos): the matching V^T fragment is one 16-byte LDS read. head_dim 72 is
 // padded to 96 for the score product (Q is zero in the padding, so whatever finite K bytes sit
 // there vanish) and to 80 for the output: V^T rows 72..79 sit in LDS with row 72 all ONES, so O^T
 // row 72 is the softmax denominator sum_kv P[kv], accumulated from the same bf16 P as the
@@ -412,10 +413,8 @@ __device__ __forceinline__ void softmax(WaveState& w, const Flash72Args& a, int 
                 x[h] = __builtin_bit_cast(uint32_t, px);
                 y[h] = __builtin_bit_cast(uint32_t, py);
             }
-            // lane group g then holds keys 32cc + 8 kappa(g) .. +7, kappa = (0, 2, 1, 3)
-            const auto r0 = __builtin_amdgcn_permlane16_swap(x[0], y[0], false, false);
-            const auto r1 = __builtin_amdgcn_permlane16_swap(x[1], y[1], false, false);
-            const uint4 packed = make_uint4(r0[0], r1[0], r0[1], r1[1]);
+            // keys 32cc + 4g .. +3 and 32cc + 16 + 4g .. +3: V^T's slots 8g .. 8g+7 of the chunk
+            const uint4 packed = make_uint4(x[0], x[1], y[0], y[1]);
             w.pf[u][cc] = *reinterpret_cast<const bf16x8_t*>(&packed);
         }
 }
@@ -502,10 +501,9 @@ __global__ void __launch_bounds__(kThreads, 1) k_flash72(Flash72Args a) {
     const int kbase = lr * kKRow + g * 16;   // K step 2, g >= 1: the next row's finite bytes (Q is 0)
     int vbase[2];
     {
-        const int kappa = ((g & 1) << 1) | (g >> 1);
         const int sw = (lr >> 1) & 7;
 #pragma unroll
-        for (int cc = 0; cc < 2; ++cc) vbase[cc] = kKBytes + lr * 128 + (((cc * 4 + kappa) ^ sw) << 4);
+        for (int cc = 0; cc < 2; ++cc) vbase[cc] = kKBytes + lr * 128 + (((cc * 4 + g) ^ sw) << 4);
     }
 #pragma unroll
     for (int e = 0; e < 5; ++e)
@@ -619,7 +617,7 @@ __global__ void __launch_bounds__(kThreads, 1) k_flash72(Flash72Args a) {
 }
 
 // V [batch, kv_len, ld_v] (head h at columns 72h..72h+71) -> V^T rows of vt_ld keys, zero-padded
-// past kv_len. One workgroup per (b, h, 64-key block), through LDS.
+// past kv_len, keys in vt_pos order. One workgroup per (b, h, 64-key block), through LDS.
 __global__ void __launch_bounds__(256) k_transpose_v72(const bf16_t* __restrict__ v, int64_t ld_v,
                                                        int B, int H, int Skv, bf16_t* vt,
                                                        int64_t vt_ld) {
@@ -637,7 +635,7 @@ __global__ void __launch_bounds__(256) k_transpose_v72(const bf16_t* __restrict_
     __syncthreads();
     for (int i = threadIdx.x; i < D * kKV; i += 256) {
         const int d = i / kKV, r = i - d * kKV;
-        if (kv0 + r < vt_ld) vt[((static_cast<int64_t>(b) * H + h) * D + d) * vt_ld + kv0 + r] = tile[r][d];
+        if (kv0 + r < vt_ld) vt[((static_cast<int64_t>(b) * H + h) * D + d) * vt_ld + vt_pos(kv0 + r)] = tile[r][d];
     }
 }
 

@@ -465,7 +465,7 @@ __device__ __forceinline__ void chunk_store(const f32x4_t (&acc)[kMT][kNT],
     }
 }
 
-// V columns of the fused QKV projection go to V^T (vt[(blk*B + b)*heads + h)*72 + d][token]):
+// V columns of the fused QKV projection go to V^T (vt[(blk*B + b)*heads + h)*72 + d][vt_pos(token)]):
 // a lane's four rows are four consecutive tokens, so each of its columns is one 8-byte store,
 // and the 16 lanes of a column group write 128 contiguous bytes of one V^T row.
 template <int ACT, int P>
@@ -495,14 +495,14 @@ __device__ __forceinline__ void vt_chunk(const f32x4_t (&acc)[kMT][kNT], const E
             uint2 r;
             pack(v, r);
             *reinterpret_cast<uint2*>(e.vt + (((blk * batches + bt) * e.vt_heads + h) * 72 + dd) *
-                                                 e.vt_ld + tok) = r;
+                                                 e.vt_ld + vt_pos(tok)) = r;
         } else {
 #pragma unroll
             for (int i = 0; i < kMT; ++i) {
                 const int64_t m = mb + i;
                 if (m >= M) break;
                 const int64_t bj = m / e.vt_seq, tj = m - bj * e.vt_seq;
-                e.vt[(((blk * batches + bj) * e.vt_heads + h) * 72 + dd) * e.vt_ld + tj] = f2bf(v[i]);
+                e.vt[(((blk * batches + bj) * e.vt_heads + h) * 72 + dd) * e.vt_ld + vt_pos(tj)] = f2bf(v[i]);
             }
         }
     }
@@ -596,12 +596,14 @@ __device__ __forceinline__ void store_staged(const char* smem, const Epi& e, bf1
                 v[j] = act_fast<ACT>(e.bias ? __fadd_rn(a, bias) : a);
             }
             const int64_t hrow = ((blk * batches + b) * e.vt_heads + h) * 72 + dd;
-            if (whole) {
-                *reinterpret_cast<uint4*>(e.vt + hrow * e.vt_ld + tok) = pack8(v);
+            if (whole) {   // two runs of four keys (vt_pos keeps runs of four together)
+                const uint4 p8 = pack8(v);
+                *reinterpret_cast<uint2*>(e.vt + hrow * e.vt_ld + vt_pos(tok)) = make_uint2(p8.x, p8.y);
+                *reinterpret_cast<uint2*>(e.vt + hrow * e.vt_ld + vt_pos(tok + 4)) = make_uint2(p8.z, p8.w);
             } else {
                 for (int j = 0; j < 8 && m + j < M; ++j) {
                     const int64_t bj = (m + j) / e.vt_seq, tj = (m + j) - bj * e.vt_seq;
-                    e.vt[(((blk * batches + bj) * e.vt_heads + h) * 72 + dd) * e.vt_ld + tj] =
+                    e.vt[(((blk * batches + bj) * e.vt_heads + h) * 72 + dd) * e.vt_ld + vt_pos(tj)] =
                         f2bf(v[j]);
                 }
             }
@@ -980,7 +982,7 @@ void launch_gemm_bf16(const bf16_t* a, const bf16_t* b, const bf16_t* bias, bf16
                     ep.vt_col0 < ep.vt_period && ep.vt_seq > 0 && m % ep.vt_seq == 0 &&
                     ep.vt_ld >= ep.vt_seq && ep.vt_heads > 0 && ep.vt_dim > 0 &&
                     ep.vt_dim == 72 && (ep.vt_period - ep.vt_col0) == int64_t{ep.vt_heads} * 72 &&
-                    ep.vt_ld % 8 == 0 && ep.vt_seq % 4 == 0 && aligned(ep.vt, 16),
+                    ep.vt_ld % 32 == 0 && ep.vt_seq % 4 == 0 && aligned(ep.vt, 16),
                 "gemm: transposed V store geometry");
     }
     const int mode = ep.residual ? (ep.gate ? EPI_GATED : EPI_RESIDUAL)
