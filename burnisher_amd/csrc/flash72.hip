@@ -23,8 +23,8 @@
 // Schedule: a wave alternates a matrix phase (the output product of block j-1, then the scores of
 // block j: 88 MFMAs) and a vector phase (softmax of block j: maximum, exp2, conversion to bf16).
 // Waves 0-3 and 4-7 run one phase apart, separated by a workgroup barrier per phase, so on every
-// SIMD one wave's exponentials overlap the other wave's MFMAs. Waves 4-7 also issue the DMA, at
-// the end of their vector phases.
+// SIMD one wave's exponentials overlap the other wave's MFMAs. Waves 0-3 also issue the DMA, at
+// the end of their matrix phases (the shorter ones).
 //
 // Softmax: scores stay fp32; exp2(s * scale * log2e - m) with the running maximum m kept in those
 // units. The first block sets m; a later block moves it (and rescales O by exp2(m_old - m_new))
@@ -62,7 +62,7 @@ constexpr int kSpareBytes = 2 * 1024;
 constexpr int kStage = kKBytes + kVBytes + kSpareBytes;   // 21504
 constexpr int kStages = 4;
 constexpr int kResidentBlocks = 7;            // key blocks a resident launch holds (kv_len <= 448)
-constexpr int kDmaWaves = 4;                  // waves 4-7 issue the DMA
+constexpr int kDmaWaves = 4;                  // waves 0-3 issue the DMA
 constexpr int kDmaPerWave = 5;                // 9 K + 9 V^T + 2 spare blocks over 4 waves
 constexpr int kMaxBlocks = 256;               // kv_len <= 16384 (the 2048px token count)
 constexpr float kRescaleThreshold = 8.0f;     // log2 units
@@ -521,12 +521,13 @@ __global__ void __launch_bounds__(kThreads, 1) k_flash72(Flash72Args a) {
     // stage j % 4. Waves 0-3 multiply in even phases (2j: output of block j-1, scores of block
     // j) and run the softmax of block j in phase 2j+1; waves 4-7 are one phase later (matrix in
     // 2j+1, softmax of block j in 2j+2). Block j's K is read in phases 2j, 2j+1 and its V^T in
-    // 2j+2, 2j+3; in phase 2j+2 waves 4-7 load block j+3 into stage (j+3) % 4, which held block
-    // j-1, last read in phase 2j+1 (a DMA instruction can hold its wave while the address unit
-    // is busy, which costs less at the end of the vector phase than in front of the MFMAs).
-    // Before each even phase 2j they wait until block j has landed (block j+1 may still be in
-    // flight), so every block has four phases to arrive. Past the last block the loads repeat
-    // it, which keeps every wait count identical.
+    // 2j+2, 2j+3. Waves 0-3 also load: at the end of phase 2j they issue block j+2 into stage
+    // (j+2) % 4, which held block j-2, last read in phase 2j-1. The vector phases are the longer
+    // ones, so the DMA instructions (which can hold their wave while the address unit is busy)
+    // go where the wave would otherwise wait at the barrier. Before each even phase 2j waves 0-3
+    // wait until block j has landed (block j+1 may still be in flight), so every block has three
+    // phases to arrive. Past the last block the loads repeat it, which keeps every wait count
+    // identical.
     auto bits_of = [&](int j) -> unsigned long long { return MASKED ? blk_bits[live[j]] : ~0ull; };
     if (RESIDENT) {
         const bf16_t* kbh = a.k + static_cast<int64_t>(b) * a.Skv * a.ld_k + h * D;
@@ -549,49 +550,48 @@ __global__ void __launch_bounds__(kThreads, 1) k_flash72(Flash72Args a) {
         matrix_phase<true, false>(w, res_stage(n - 1), vbase, nullptr, kbase);
     } else {
     auto stage_of = [&](int j) -> char* { return smem + (j & (kStages - 1)) * kStage; };
-    if (wave < kWaves - kDmaWaves) {
-        wait_and_join<63>();                                     // phase 0
+    if (wave < kDmaWaves) {
+        // waves 0-3: the matrix phase in even phases, then the DMA of block j+2
+        const bf16_t* kbh = a.k + static_cast<int64_t>(b) * a.Skv * a.ld_k + h * D;
+        const bf16_t* vbh = a.vt + (static_cast<int64_t>(b) * a.H + h) * D * a.vt_ld;
+        const int last_full = a.Skv / kKV;   // blocks below this one hold 64 real keys
+        const DmaPlan plan = dma_plan(a, wave, lane);
+        auto issue = [&](int j) {
+            const int blk = live[min(j, n - 1)];
+            dma_block(stage_of(j), a, plan, kbh, vbh, wave, lane, blk * kKV, MASKED && blk >= last_full);
+        };
+        issue(0);
+        issue(1);
+        wait_and_join<kDmaPerWave>();                            // phase 0: block 0 has landed
         matrix_phase<false, true>(w, nullptr, vbase, stage_of(0), kbase);
+        issue(2);
         for (int j = 1; j < n; ++j) {
             wait_and_join<63>();                                 // phase 2j-1
             softmax<MASKED>(w, a, live[j - 1], bits_of(j - 1), all_masked, g, j == 1);
-            wait_and_join<63>();                                 // phase 2j
+            wait_and_join<kDmaPerWave>();                        // phase 2j: block j has landed
             matrix_phase<true, true>(w, stage_of(j - 1), vbase, stage_of(j), kbase);
+            issue(j + 2);
         }
         wait_and_join<63>();                                     // phase 2n-1
         softmax<MASKED>(w, a, live[n - 1], bits_of(n - 1), all_masked, g, n == 1);
         wait_and_join<63>();                                     // phase 2n
         matrix_phase<true, false>(w, stage_of(n - 1), vbase, nullptr, kbase);
         wait_and_join<63>();                                     // phase 2n+1
+        s_waitcnt<0, 15>();   // the trailing copies
     } else {
-        const int dw = wave - (kWaves - kDmaWaves);
-        const bf16_t* kbh = a.k + static_cast<int64_t>(b) * a.Skv * a.ld_k + h * D;
-        const bf16_t* vbh = a.vt + (static_cast<int64_t>(b) * a.H + h) * D * a.vt_ld;
-        const int last_full = a.Skv / kKV;   // blocks below this one hold 64 real keys
-        const DmaPlan plan = dma_plan(a, dw, lane);
-        auto issue = [&](int j) {
-            const int blk = live[min(j, n - 1)];
-            dma_block(stage_of(j), a, plan, kbh, vbh, dw, lane, blk * kKV, MASKED && blk >= last_full);
-        };
-        issue(0);
-        issue(1);
-        wait_and_join<kDmaPerWave>();                            // phase 0
-        issue(2);
+        wait_and_join<63>();                                     // phase 0
         wait_and_join<63>();                                     // phase 1
         matrix_phase<false, true>(w, nullptr, vbase, stage_of(0), kbase);
-        wait_and_join<kDmaPerWave>();                            // phase 2
+        wait_and_join<63>();                                     // phase 2
         softmax<MASKED>(w, a, live[0], bits_of(0), all_masked, g, true);
-        issue(3);
         for (int j = 1; j < n; ++j) {
             wait_and_join<63>();                                 // phase 2j+1
             matrix_phase<true, true>(w, stage_of(j - 1), vbase, stage_of(j), kbase);
-            wait_and_join<kDmaPerWave>();                        // phase 2j+2
+            wait_and_join<63>();                                 // phase 2j+2
             softmax<MASKED>(w, a, live[j], bits_of(j), all_masked, g, false);
-            issue(j + 3);
         }
         wait_and_join<63>();                                     // phase 2n+1
         matrix_phase<true, false>(w, stage_of(n - 1), vbase, nullptr, kbase);
-        s_waitcnt<0, 15>();   // the trailing copies
     }
     }
 
