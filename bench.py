@@ -1,6 +1,8 @@
 """bench.py -- the dit-step on one MI355X: ms per step at 1024px bf16, and the MFMA roofline.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--resolution 1024] [--no-cpu]
+    python bench.py --kernels          # the isolated kernels at 1024px shapes, one line each
+    python bench.py --probe NAME       # one kernel three times after a copy, for rocprofv3 --pmc
 
 One step is one PixArt-Sigma dit-step forward (28 blocks, hidden 1152, 16 heads x 72, MLP 4608)
 at batch 2 (classifier-free guidance) over a 128x128x4 latent (4096 image tokens) and a
@@ -70,34 +72,119 @@ def parse() -> argparse.Namespace:
     p.add_argument("--batch", type=int, default=2)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--cpu-threads", type=int, default=0)
-    p.add_argument("--probe", choices=["attention_self"],
+    p.add_argument("--probe", choices=sorted(KERNEL_SHAPES),
                    help="for counter collection: run a 256 MiB device copy (calibration) and the "
                         "named kernel at the dit-step shape three times each, then exit")
+    p.add_argument("--kernels", action="store_true",
+                   help="time the isolated kernels at 1024px shapes (GEMMs, self- and "
+                        "cross-attention, LayerNorm+modulate); one JSON line per kernel")
     return p.parse_args()
 
 
+def make_kernel(name: str):
+    """One isolated kernel of the 1024px dit-step on seeded synthetic
+    operands: returns (launch, algorithmic work per launch, unit of that work)."""
+    import torch
+
+    import burnisher_amd as bh
+
+    gen = torch.Generator(device="cuda").manual_seed(0)
+    randn = lambda *shape, std=1.0: (torch.randn(*shape, device="cuda", generator=gen) * std).bfloat16()
+    kind, dims = KERNEL_SHAPES[name]
+    if kind == "gemm":
+        m, n, k = dims
+        a, w, bias = randn(m, k), randn(n, k, std=0.02), randn(n, std=0.02)
+        out = torch.empty(m, n, device="cuda", dtype=torch.bfloat16)
+        launch = lambda: bh.call("bh_gemm", a.data_ptr(), w.data_ptr(), bias.data_ptr(),
+                                 out.data_ptr(), m, n, k, 1, 0, bh.BF16, None)
+        return launch, 2.0 * m * n * k, "flop", (a, w, bias, out)
+    if kind == "attention":
+        batch, heads, sq, skv, dh = dims
+        q, k, v = randn(batch, sq, heads * dh), randn(batch, skv, heads * dh), randn(batch, skv, heads * dh)
+        out = torch.empty_like(q)
+        mask = None
+        if sq != skv:   # the caption mask of the workload: row 0 keeps 75 tokens, row 1 keeps 150
+            mask = torch.zeros(batch, skv, device="cuda")
+            mask[0, :75] = 1
+            mask[1, :150] = 1
+        launch = lambda: bh.call("bh_attention", q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                                 out.data_ptr(), batch, heads, sq, skv, dh, 0.0, None,
+                                 None if mask is None else mask.data_ptr(), bh.F32, bh.BF16, None)
+        return launch, 4.0 * batch * heads * sq * skv * dh, "flop", (q, k, v, out, mask)
+    rows, cols = dims   # op-level LayerNorm + chunk + modulate (bh_norm_modulate): read x, write
+                        # the result
+    x = randn(rows, cols)
+    mod = randn(2, 6 * cols, std=0.02)
+    table = randn(6, cols, std=0.02)
+    out = torch.empty_like(x)
+    launch = lambda: bh.call("bh_norm_modulate", x.data_ptr(), mod.data_ptr(), 6, 0, 1,
+                             table.data_ptr(), 0, 1, out.data_ptr(), 2, rows // 2, cols, 1e-6,
+                             None)
+    return launch, 2.0 * rows * cols * 2, "bytes", (x, mod, table, out)
+
+
+# the isolated kernels of BASELINE.json configs[1] (and the dit-step's norm), 1024px shapes
+KERNEL_SHAPES = {
+    "gemm_proj": ("gemm", (8192, 1152, 1152)),
+    "gemm_qkv": ("gemm", (8192, 3456, 1152)),
+    "gemm_ff0": ("gemm", (8192, 4608, 1152)),
+    "gemm_ff2": ("gemm", (8192, 1152, 4608)),
+    "attention_self": ("attention", (2, 16, 4096, 4096, 72)),
+    "attention_cross": ("attention", (2, 16, 4096, 300, 72)),
+    "norm_modulate": ("norm", (8192, 1152)),
+}
+
+
 def probe(kernel: str) -> int:
-    """Launches for rocprofv3 --pmc passes (FETCH_SIZE / WRITE_SIZE): a copy of known size, then
-    the kernel, three times each."""
+    """Launches for rocprofv3 --pmc passes: a copy of known size, then the kernel, three times
+    each."""
     import torch
 
     import burnisher_amd as bh
 
     bh.check(bh.lib().bh_init(0), "bh_init")
-    gen = torch.Generator(device="cuda").manual_seed(0)
     src = torch.ones(128 << 20, device="cuda", dtype=torch.bfloat16)   # 256 MiB
     dst = torch.empty_like(src)
-    batch, tokens, heads, head_dim = 2, 4096, 16, 72
-    q, k, v = (torch.randn(batch, tokens, heads * head_dim, device="cuda", generator=gen).bfloat16()
-               for _ in range(3))
-    out = torch.empty_like(q)
+    launch, _, _, keep = make_kernel(kernel)
     torch.cuda.synchronize()
     for _ in range(3):
         dst.copy_(src)
-        bh.call("bh_attention", q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), batch,
-                heads, tokens, tokens, head_dim, 0.0, None, None, 0, bh.BF16, None)
+        launch()
     torch.cuda.synchronize()
     log(f"probe {kernel}: done")
+    return 0
+
+
+def kernels(iters: int) -> int:
+    """The isolated kernels: average launch time over `iters` launches between HIP events after
+    three warm-up launches; FLOP kernels against the dense bf16 MFMA peak, the norm against HBM."""
+    import torch
+
+    import burnisher_amd as bh
+
+    bh.check(bh.lib().bh_init(0), "bh_init")
+    for name in KERNEL_SHAPES:
+        launch, work, unit, keep = make_kernel(name)
+        for _ in range(3):
+            launch()
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        start.record()
+        for _ in range(iters):
+            launch()
+        stop.record()
+        torch.cuda.synchronize()
+        us = start.elapsed_time(stop) / iters * 1e3
+        rate = work / (us * 1e-6)
+        line = {"kernel": name, "shape": list(KERNEL_SHAPES[name][1]), "us_per_launch": round(us, 2)}
+        if unit == "flop":
+            line.update({"tflops": round(rate / 1e12, 1), "peak": PEAK_BF16_TFLOPS,
+                         "frac": round(rate / 1e12 / PEAK_BF16_TFLOPS, 4), "bound": "mfma"})
+        else:
+            line.update({"gbs": round(rate / 1e9, 1), "peak": PEAK_HBM_GBS,
+                         "frac": round(rate / 1e9 / PEAK_HBM_GBS, 4), "bound": "hbm"})
+        print(json.dumps(line), flush=True)
+        del keep
     return 0
 
 
@@ -126,6 +213,8 @@ def main() -> int:
     args = parse()
     if args.probe:
         return probe(args.probe)
+    if args.kernels:
+        return kernels(max(args.steps, 10))
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
               "(the dit-step would shard on the CFG batch, see DESIGN.md)", file=sys.stderr)
