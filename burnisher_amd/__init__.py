@@ -66,6 +66,30 @@ class DitWeights(ctypes.Structure):
         ("blocks", ctypes.POINTER(DitBlockWeights))]
 
 
+class SchedConfig(ctypes.Structure):
+    _fields_ = [("num_train_timesteps", ctypes.c_int), ("beta_start", ctypes.c_double),
+                ("beta_end", ctypes.c_double), ("beta_schedule", ctypes.c_char_p),
+                ("solver_order", ctypes.c_int), ("algorithm_type", ctypes.c_char_p),
+                ("solver_type", ctypes.c_char_p), ("prediction_type", ctypes.c_char_p),
+                ("timestep_spacing", ctypes.c_char_p), ("lower_order_final", ctypes.c_int)]
+
+    @classmethod
+    def pinned(cls, **overrides) -> "SchedConfig":
+        """The PixArt-Sigma configuration (scheduler.h:21-30), optionally changed field by field."""
+        fields = dict(num_train_timesteps=1000, beta_start=0.0001, beta_end=0.02,
+                      beta_schedule=b"linear", solver_order=2, algorithm_type=b"dpmsolver++",
+                      solver_type=b"midpoint", prediction_type=b"epsilon",
+                      timestep_spacing=b"linspace", lower_order_final=1)
+        fields.update(overrides)
+        return cls(**fields)
+
+
+class SchedCoefficients(ctypes.Structure):
+    _fields_ = [("order", ctypes.c_int)] + [
+        (f, ctypes.c_double) for f in ("sigma_s0", "sigma_t", "sigma_vp_s0", "sigma_vp_t",
+                                       "alpha_t", "alpha_s0", "exp_neg_h", "r0")]
+
+
 # ---- loading -------------------------------------------------------------------------------
 
 _lib = None
@@ -98,6 +122,23 @@ SIGNATURES = {
     "bh_profile_enable": ([_I], _I),
     "bh_profile_read": ([_I, ctypes.POINTER(_D), ctypes.POINTER(_I64), ctypes.POINTER(_D)], _I),
     "bh_fill_normal_bf16": ([_V, _I64, ctypes.c_uint64, ctypes.c_char_p, _F], _I),
+    "bh_repeat": ([_V, _V, _I64, _I64, _I, _V], _I),
+    "bh_guidance": ([_V, _V, _I64, _I64, _I64, _F, _I, _V], _I),
+    "bh_sched_config_default": ([ctypes.POINTER(SchedConfig)], None),
+    "bh_sched_create": ([ctypes.POINTER(SchedConfig), ctypes.POINTER(_V)], _I),
+    "bh_sched_set_timesteps": ([_V, _I], _I),
+    "bh_sched_steps": ([_V], _I),
+    "bh_sched_timestep": ([_V, _I], _I64),
+    "bh_sched_sigma": ([_V, _I], _D),
+    "bh_sched_init_noise_sigma": ([_V], _D),
+    "bh_sched_get_coefficients": ([_V, _I, ctypes.POINTER(SchedCoefficients)], _I),
+    "bh_sched_reserve": ([_V, _I64, _I], _I),
+    "bh_sched_step": ([_V, _V, _I, _V, _I64, _I, _V], _I),
+    "bh_sched_reset": ([_V], _I),
+    "bh_sched_destroy": ([_V], None),
+    "bh_denoiser_create": ([_V, _V, _I, _F, ctypes.POINTER(_V)], _I),
+    "bh_denoiser_run": ([_V, _V, _V, _V, _I, _I, _V], _I),
+    "bh_denoiser_destroy": ([_V], None),
 }
 
 

@@ -50,7 +50,10 @@ def sources() -> list[Path]:
 # rescaled by VALU multiplies, and in the default AGPR form every rescale and loop iteration
 # copies all 80 of them between the register files), and it is compiled without IEEE NaN rules
 # so a maximum over MFMA results is one v_max3 per two inputs, not a quieting v_max per input.
-EXTRA_FLAGS = {"flash72.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form", "-fno-honor-nans"]}
+# denoise.hip evaluates the guidance combine and the solver update in fp64 exactly as the
+# reference's x86-64 build does, which forms no multiply-add.
+EXTRA_FLAGS = {"flash72.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form", "-fno-honor-nans"],
+               "denoise.hip": ["-ffp-contract=off"]}
 
 
 def _compile(src: Path) -> Path:

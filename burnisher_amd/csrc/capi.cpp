@@ -110,6 +110,8 @@ thread_local int g_gemm_subclass = -1;
 
 }  // namespace
 
+bool profiling_enabled() { return profiler().mask != 0; }
+
 ProfileScope::ProfileScope(int cls, hipStream_t stream, double work, int also)
     : cls_(cls), also_(also), stream_(stream), work_(work) {
     Profiler& p = profiler();

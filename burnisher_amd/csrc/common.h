@@ -13,6 +13,8 @@
 #include <stdexcept>
 #include <string>
 
+#include "../../include/burnisher_hip.h"
+
 namespace bh {
 
 using bf16_t = uint16_t;
@@ -140,6 +142,16 @@ struct ProfileScope {
     double work_;
     int slot_ = -1;
 };
+
+// True while bh_profile_enable has a nonzero mask (launches are then bracketed by events).
+bool profiling_enabled();
+
+// Geometry of a dit-step engine, for the denoise loop (dit_engine.cpp).
+struct DitGeometry {
+    int64_t batch, in_channels, out_channels, latent_hw;
+    int mode;
+};
+DitGeometry dit_geometry(const bh_dit* e);
 
 // Engine hint: which engine GEMM is running, so its launch is also credited to a sub-class.
 void set_gemm_subclass(int cls);

@@ -129,6 +129,10 @@ struct bh_dit {
     }
 };
 
+DitGeometry bh::dit_geometry(const bh_dit* e) {
+    return DitGeometry{e->B, e->cfg.in_channels, e->cfg.out_channels, e->latent, e->mode};
+}
+
 namespace {
 
 void check_weights(const bh_dit_config& c, const bh_dit_weights& w) {

@@ -217,6 +217,102 @@ int bh_dit_forward(bh_dit* e, const void* latent, double timestep, const void* c
 int64_t bh_dit_workspace_bytes(const bh_dit* e);
 void bh_dit_destroy(bh_dit* e);
 
+/* ---- the denoise loop around the dit-step (pipeline.cpp:104-131) -------------------------- */
+
+/* RepeatArgs (ops.h:217-222): out[r*inner + i] = in[i] for r in [0, outer). A copy, exact in
+ * either dtype. Replaces the reference `repeat_cuda` (src/cuda/ops_cuda.cu:1033-1049). */
+int bh_repeat(const void* in, void* out, int64_t outer, int64_t inner, int dtype, void* stream);
+
+/* GuidanceArgs (ops.h:224-237): prediction [2, out_channels, spatial] -> out [channels, spatial],
+ *   out = u + scale * (c - u),  u = prediction[0, ch, s] (negative prompt), c = prediction[1, ch, s],
+ * evaluated in fp64 and rounded once (ops_cpu.cpp:361-369). Only the first `channels` of the
+ * `out_channels` are read: the learned-variance half is discarded. Replaces `guidance_cuda`
+ * (src/cuda/ops_cuda.cu:1051-1073). */
+int bh_guidance(const void* prediction, void* out, int64_t out_channels, int64_t channels,
+                int64_t spatial, float scale, int dtype, void* stream);
+
+/* SchedulerConfig (scheduler.h:20-31). Only the pinned configuration is implemented, and the
+ * others are refused with the reference's reasons (dpm_solver.cpp:19-53, 55-61):
+ * algorithm "dpmsolver++", solver "midpoint", prediction "epsilon", spacing "linspace";
+ * beta_schedule "linear" or "scaled_linear". */
+typedef struct bh_sched_config {
+    int num_train_timesteps;      /* 1000 */
+    double beta_start;            /* 1e-4 */
+    double beta_end;              /* 0.02 */
+    const char* beta_schedule;    /* "linear" */
+    int solver_order;             /* 2 (>= 1) */
+    const char* algorithm_type;   /* "dpmsolver++" */
+    const char* solver_type;      /* "midpoint" */
+    const char* prediction_type;  /* "epsilon" */
+    const char* timestep_spacing; /* "linspace" */
+    int lower_order_final;        /* 1 */
+} bh_sched_config;
+
+/* DPMSolverMultistep::StepCoefficients (scheduler.h:52-69): the Karras sigmas (sigma_*), the
+ * variance-preserving ones (sigma_vp_*), alpha, exp(-h) = sigma_t / sigma_s0 and r0 = h0 / h
+ * (0 for a first-order step). */
+typedef struct bh_sched_coefficients {
+    int order;
+    double sigma_s0, sigma_t;
+    double sigma_vp_s0, sigma_vp_t;
+    double alpha_t, alpha_s0;
+    double exp_neg_h;
+    double r0;
+} bh_sched_coefficients;
+
+/* DPM-Solver++ 2M (src/sched/dpm_solver.cpp), with its state split the MI355X way: the schedule,
+ * the step order and the fp64 coefficients are host scalars computed exactly as the reference
+ * does; the sample, the model output and the x0 history stay in device memory and one kernel per
+ * step applies the update in fp64 with the reference's rounding (dpm_solver.cpp:89-162). */
+typedef struct bh_sched bh_sched;
+
+/* The pinned PixArt-Sigma configuration (scheduler.h:21-30). */
+void bh_sched_config_default(bh_sched_config* cfg);
+/* DPMSolverMultistep(cfg) (dpm_solver.cpp:19-53). Host memory only. */
+int bh_sched_create(const bh_sched_config* cfg, bh_sched** out);
+/* set_timesteps (dpm_solver.cpp:55-75): steps >= 1; also resets the step history. */
+int bh_sched_set_timesteps(bh_sched* s, int steps);
+int bh_sched_steps(const bh_sched* s);
+/* timestep(i) and sigma(i) (scheduler.h:39-40); sigma has steps + 1 entries, the last 0.
+ * Out of range: -1 and NaN, with bh_last_error set. */
+int64_t bh_sched_timestep(const bh_sched* s, int i);
+double bh_sched_sigma(const bh_sched* s, int i);
+double bh_sched_init_noise_sigma(const bh_sched* s);
+/* coefficients(i) (dpm_solver.cpp:100-123), from the current step history. */
+int bh_sched_get_coefficients(const bh_sched* s, int i, bh_sched_coefficients* out);
+/* Sizes the device x0 history for `numel` elements of `dtype` (two buffers). This call
+ * allocates; bh_sched_step allocates only when no reservation of its size and dtype exists. */
+int bh_sched_reserve(bh_sched* s, int64_t numel, int dtype);
+/* step(model_output, i, sample) (dpm_solver.cpp:89-98, 125-162): `sample` [numel] is updated in place
+ * from the epsilon prediction `model_output` [numel], both device pointers of `dtype`. Keeps the
+ * last two x0 predictions on the device. Asynchronous on `stream`. */
+int bh_sched_step(bh_sched* s, const void* model_output, int i, void* sample, int64_t numel,
+                  int dtype, void* stream);
+/* reset (dpm_solver.cpp:84-87): forget the history; the next step is first order. */
+int bh_sched_reset(bh_sched* s);
+void bh_sched_destroy(bh_sched* s);
+
+/* Pipeline::generate's denoise loop (pipeline.cpp:104-131) with every step on the device: per
+ * step repeat -> bh_dit_forward at timestep(i) -> guidance -> bh_sched_step, with no host copy
+ * and no host synchronisation (the reference copies eps and the latent to the host and back
+ * every step, pipeline.cpp:127-130). */
+typedef struct bh_denoiser bh_denoiser;
+
+/* `e` must have batch 2 when classifier_free_guidance is set (negative prompt first, as the
+ * reference requires, pipeline.cpp:69-75) and batch 1 otherwise; `s` must have timesteps set.
+ * Allocates the batched latent, the prediction, eps and the scheduler's history. Both `e` and
+ * `s` must outlive the denoiser. */
+int bh_denoiser_create(bh_dit* e, bh_sched* s, int classifier_free_guidance,
+                       float guidance_scale, bh_denoiser** out);
+/* Resets the scheduler and runs every step of its schedule on `latent` [1, in_ch, H, W] (bf16,
+ * device, updated in place). With use_graph, the whole loop is captured once into a HIP graph
+ * per (latent, caption, caption_mask, mask_dtype) binding and replayed on later calls; the
+ * schedule and guidance scale are part of the capture, so bh_sched_set_timesteps on `s`
+ * invalidates it. Capture needs the launch profiler off. */
+int bh_denoiser_run(bh_denoiser* d, void* latent, const void* caption, const void* caption_mask,
+                    int mask_dtype, int use_graph, void* stream);
+void bh_denoiser_destroy(bh_denoiser* d);
+
 /* ---- measurement and inputs --------------------------------------------------------------- */
 
 /* Kernel classes timed by the launch profiler. */

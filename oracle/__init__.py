@@ -1,7 +1,7 @@
 """oracle -- TEST INFRASTRUCTURE ONLY: ctypes access to the CPU parity checkers.
 
-  stock()  oracle/_build/libstock.so, the restatement of the reference's `stock` ops and DiT
-           graph (oracle/stock.cpp). Built by `make -C oracle`.
+  stock()  oracle/_build/libstock.so, the restatement of the reference's `stock` ops, DiT
+           graph and DPM-Solver++ sampler (oracle/stock.cpp). Built by `make -C oracle`.
   ref()    oracle/_ref/libref_stock.so, the reference's OWN stock path compiled from
            /root/reference (oracle/ref_shim.cpp + `make -C oracle ref`), or None where it was
            not built (it needs /root/reference at build time).
@@ -35,6 +35,17 @@ _STOCK_SIGS = {
     "stock_position_embedding": ([ctypes.POINTER(_D), _I, _I, _I, _D], _I),
     "stock_timestep_embedding": ([_D, _I, ctypes.POINTER(_F)], _I),
     "stock_dit_forward": ([_V, _V, _I64, _I64, _I64, _V, _D, _V, _V, _I, _V, _I, _I], _I),
+    "stock_repeat": ([_V, _V, _I64, _I64, _I], _I),
+    "stock_guidance": ([_V, _V, _I64, _I64, _I64, _F, _I], _I),
+    "stock_sched_create": ([_V, ctypes.POINTER(_V)], _I),
+    "stock_sched_destroy": ([_V], None),
+    "stock_sched_set_timesteps": ([_V, _I], _I),
+    "stock_sched_steps": ([_V], _I),
+    "stock_sched_timestep": ([_V, _I, ctypes.POINTER(_I64)], _I),
+    "stock_sched_sigma": ([_V, _I, ctypes.POINTER(_D)], _I),
+    "stock_sched_coefficients": ([_V, _I, _V], _I),
+    "stock_sched_step": ([_V, _V, _I, _V, _I64, _I], _I),
+    "stock_sched_reset": ([_V], _I),
 }
 _REF_SIGS = {
     "ref_last_error": ([], ctypes.c_char_p),
@@ -49,6 +60,17 @@ _REF_SIGS = {
     "ref_position_embedding": ([ctypes.POINTER(_D), _I, _I, _I, _D], _I),
     "ref_timestep_embedding": ([_D, _I, ctypes.POINTER(_F)], _I),
     "ref_dit_forward": ([_V, _V, _I64, _I64, _I64, _V, _D, _V, _V, _I, _V, _I], _I),
+    "ref_repeat": ([_V, _V, _I64, _I64, _I], _I),
+    "ref_guidance": ([_V, _V, _I64, _I64, _I64, _F, _I], _I),
+    "ref_sched_create": ([_V, ctypes.POINTER(_V)], _I),
+    "ref_sched_destroy": ([_V], None),
+    "ref_sched_set_timesteps": ([_V, _I], _I),
+    "ref_sched_steps": ([_V], _I),
+    "ref_sched_timestep": ([_V, _I, ctypes.POINTER(_I64)], _I),
+    "ref_sched_sigma": ([_V, _I, ctypes.POINTER(_D)], _I),
+    "ref_sched_coefficients": ([_V, _I, _V], _I),
+    "ref_sched_step": ([_V, _V, _I, _V, _I64, _I], _I),
+    "ref_sched_reset": ([_V], _I),
 }
 
 _stock = None

@@ -13,6 +13,7 @@
 
 #include "burnisher/models.h"
 #include "burnisher/ops.h"
+#include "burnisher/scheduler.h"
 
 #include "../include/burnisher_hip.h"
 
@@ -250,6 +251,79 @@ int ref_dit_forward(const bh_dit_config* cfg, const bh_dit_weights* w, int64_t b
         Tensor out = model.forward(z, timestep, cap, m, ImplSelection::from_request("stock"));
         std::memcpy(image, out.data(), out.nbytes());
     });
+}
+
+
+int ref_repeat(const void* in, void* out, int64_t outer, int64_t inner, int dtype) {
+    return guard([&] {
+        Tensor x = view(in, {inner}, dtype);
+        Tensor y = view(out, {outer * inner}, dtype);
+        RepeatRegistry::instance().get("stock")(RepeatArgs{&x, &y, outer, inner});
+    });
+}
+
+int ref_guidance(const void* pred, void* out, int64_t out_channels, int64_t channels,
+                 int64_t spatial, float scale, int dtype) {
+    return guard([&] {
+        Tensor p = view(pred, {2, out_channels, spatial}, dtype);
+        Tensor y = view(out, {channels, spatial}, dtype);
+        GuidanceRegistry::instance().get("stock")(
+            GuidanceArgs{&p, &y, out_channels, channels, spatial, scale});
+    });
+}
+
+// The reference's own DPMSolverMultistep behind an opaque handle, on host buffers.
+int ref_sched_create(const bh_sched_config* c, void** out) {
+    return guard([&] {
+        SchedulerConfig sc;
+        sc.num_train_timesteps = c->num_train_timesteps;
+        sc.beta_start = c->beta_start;
+        sc.beta_end = c->beta_end;
+        sc.beta_schedule = c->beta_schedule;
+        sc.solver_order = c->solver_order;
+        sc.algorithm_type = c->algorithm_type;
+        sc.solver_type = c->solver_type;
+        sc.prediction_type = c->prediction_type;
+        sc.timestep_spacing = c->timestep_spacing;
+        sc.lower_order_final = c->lower_order_final != 0;
+        *out = new DPMSolverMultistep(sc);
+    });
+}
+
+void ref_sched_destroy(void* h) { delete static_cast<DPMSolverMultistep*>(h); }
+
+int ref_sched_set_timesteps(void* h, int steps) {
+    return guard([&] { static_cast<DPMSolverMultistep*>(h)->set_timesteps(steps); });
+}
+
+int ref_sched_steps(const void* h) { return static_cast<const DPMSolverMultistep*>(h)->steps(); }
+
+int ref_sched_timestep(const void* h, int i, int64_t* out) {
+    return guard([&] { *out = static_cast<const DPMSolverMultistep*>(h)->timestep(i); });
+}
+
+int ref_sched_sigma(const void* h, int i, double* out) {
+    return guard([&] { *out = static_cast<const DPMSolverMultistep*>(h)->sigma(i); });
+}
+
+int ref_sched_coefficients(const void* h, int i, bh_sched_coefficients* out) {
+    return guard([&] {
+        const auto c = static_cast<const DPMSolverMultistep*>(h)->coefficients(i);
+        *out = bh_sched_coefficients{c.order,   c.sigma_s0, c.sigma_t,   c.sigma_vp_s0, c.sigma_vp_t,
+                                     c.alpha_t, c.alpha_s0, c.exp_neg_h, c.r0};
+    });
+}
+
+int ref_sched_step(void* h, const void* eps, int i, void* sample, int64_t n, int dtype) {
+    return guard([&] {
+        Tensor e = view(eps, {n}, dtype);
+        Tensor x = view(sample, {n}, dtype);
+        static_cast<DPMSolverMultistep*>(h)->step(e, i, x);
+    });
+}
+
+int ref_sched_reset(void* h) {
+    return guard([&] { static_cast<DPMSolverMultistep*>(h)->reset(); });
 }
 
 }  // extern "C"

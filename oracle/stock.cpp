@@ -501,6 +501,153 @@ void dit_forward(const bh_dit_config& c, const bh_dit_weights& w, int64_t B, int
     patch_impl(tokens.p(), image, B, c.out_channels, grid, P, true, BF);
 }
 
+// ---- the denoise loop's two ops (ops_cpu.cpp:355-369) -----------------------------------------
+
+void repeat_impl(const void* in, void* out, int64_t outer, int64_t inner, int dt) {
+    View x{in, dt};
+    Out y{out, dt};
+    for (int64_t r = 0; r < outer; ++r)
+        for (int64_t i = 0; i < inner; ++i) y.set(r * inner + i, x.get(i));
+}
+
+// u + scale*(c - u) in double, one rounding to float, then the store (ops_cpu.cpp:361-369).
+void guidance_impl(const void* pred, void* out, int64_t out_channels, int64_t channels,
+                   int64_t spatial, float scale, int dt) {
+    View p{pred, dt};
+    Out y{out, dt};
+    for (int64_t ch = 0; ch < channels; ++ch)
+        for (int64_t s = 0; s < spatial; ++s) {
+            const double u = p.get(ch * spatial + s);
+            const double c = p.get((out_channels + ch) * spatial + s);
+            y.set(ch * spatial + s, static_cast<float>(u + scale * (c - u)));
+        }
+}
+
+// ---- the sampler: DPM-Solver++ 2M, midpoint, epsilon (src/sched/dpm_solver.cpp) -------------
+
+struct Sampler {
+    int train_steps = 1000;
+    int order_cap = 2;          // solver_order
+    bool lower_final = true;    // lower_order_final
+    bool spacing_ok = true;     // timestep_spacing == "linspace", checked by set_timesteps
+    std::vector<double> karras; // sqrt((1 - acp) / acp) per training timestep
+    std::vector<int64_t> ts;    // the inference timesteps
+    std::vector<double> sig;    // karras sigma per inference step, then a final 0
+    std::vector<std::vector<float>> x0s;  // stored x0 predictions, oldest first
+    int warm = 0;               // lower_order_nums_: steps taken, capped at solver_order
+};
+
+bool same(const char* a, const char* b) { return a && std::strcmp(a, b) == 0; }
+
+// The constructor (dpm_solver.cpp:19-53): cumulative product of (1 - beta) in double over the
+// training schedule, beta linear in t, or linear in sqrt(beta) for "scaled_linear".
+void sampler_init(Sampler& s, const bh_sched_config& c) {
+    if (!same(c.algorithm_type, "dpmsolver++"))
+        throw std::runtime_error("scheduler: only dpmsolver++ is implemented");
+    if (!same(c.solver_type, "midpoint"))
+        throw std::runtime_error("scheduler: only the midpoint solver type is implemented");
+    if (!same(c.prediction_type, "epsilon"))
+        throw std::runtime_error("scheduler: only epsilon prediction is implemented");
+    if (c.num_train_timesteps < 2) throw std::runtime_error("scheduler: num_train_timesteps < 2");
+    if (c.solver_order < 1) throw std::runtime_error("scheduler: solver_order < 1");
+    const bool scaled = same(c.beta_schedule, "scaled_linear");
+    if (!scaled && !same(c.beta_schedule, "linear"))
+        throw std::runtime_error("scheduler: unsupported beta_schedule");
+    s.train_steps = c.num_train_timesteps;
+    s.order_cap = c.solver_order;
+    s.lower_final = c.lower_order_final != 0;
+    s.spacing_ok = same(c.timestep_spacing, "linspace");
+    s.karras.assign(static_cast<size_t>(s.train_steps), 0.0);
+    double acp = 1.0;
+    const double lo = scaled ? std::sqrt(c.beta_start) : c.beta_start;
+    const double hi = scaled ? std::sqrt(c.beta_end) : c.beta_end;
+    for (int t = 0; t < s.train_steps; ++t) {
+        const double f = lo + (hi - lo) * (static_cast<double>(t) / (s.train_steps - 1));
+        acp *= 1.0 - (scaled ? f * f : f);
+        s.karras[static_cast<size_t>(t)] = std::sqrt((1.0 - acp) / acp);
+    }
+}
+
+// set_timesteps (dpm_solver.cpp:55-75): step j of `steps` sits at round(j * (N-1) / steps) for
+// j = steps..1 (linspace over [0, N-1] with steps+1 points, reversed, the 0 dropped).
+void sampler_set_timesteps(Sampler& s, int steps) {
+    if (steps < 1) throw std::runtime_error("scheduler: at least one step");
+    if (!s.spacing_ok) throw std::runtime_error("scheduler: only linspace spacing is implemented");
+    s.ts.clear();
+    s.sig.clear();
+    for (int j = steps; j >= 1; --j) {
+        const double at = static_cast<double>(j) * (s.train_steps - 1) / static_cast<double>(steps);
+        s.ts.push_back(static_cast<int64_t>(std::llround(at)));
+        s.sig.push_back(s.karras[static_cast<size_t>(s.ts.back())]);
+    }
+    s.sig.push_back(0.0);
+    s.x0s.clear();
+    s.warm = 0;
+}
+
+// Karras sigma -> (alpha, sigma) of the variance-preserving form (dpm_solver.cpp:10-16).
+void vp_of(double k, double* alpha, double* sigma) {
+    const double r = std::sqrt(k * k + 1.0);
+    *alpha = 1.0 / r;
+    *sigma = k / r;
+}
+
+// coefficients(i) (dpm_solver.cpp:100-123).
+bh_sched_coefficients sampler_coefficients(const Sampler& s, int i) {
+    if (i < 0 || static_cast<size_t>(i) + 1 >= s.sig.size())
+        throw std::runtime_error("scheduler: step index out of range");
+    const size_t at = static_cast<size_t>(i);
+    bh_sched_coefficients c{};
+    c.sigma_s0 = s.sig[at];
+    c.sigma_t = s.sig[at + 1];
+    vp_of(c.sigma_t, &c.alpha_t, &c.sigma_vp_t);
+    vp_of(c.sigma_s0, &c.alpha_s0, &c.sigma_vp_s0);
+    c.exp_neg_h = c.sigma_s0 > 0.0 ? c.sigma_t / c.sigma_s0 : 0.0;
+    const bool final_step = at + 2 == s.sig.size();
+    const bool second = s.warm >= 1 && !(s.lower_final && final_step) && s.order_cap >= 2;
+    c.order = second ? 2 : 1;
+    if (second) {
+        if (at == 0) throw std::runtime_error("scheduler: a second-order step needs step i-1");
+        const double h = std::log(c.sigma_s0 / c.sigma_t);
+        const double h0 = std::log(s.sig[at - 1] / c.sigma_s0);
+        c.r0 = h0 / h;
+    }
+    return c;
+}
+
+// step (dpm_solver.cpp:89-98, 125-162) on a host sample of n elements. x0 is stored through the
+// sample's dtype before it is used, as the reference keeps it in a tensor of that dtype.
+void sampler_step(Sampler& s, const void* eps, int i, void* sample, int64_t n, int dt) {
+    if (i < 0 || static_cast<size_t>(i) >= s.ts.size())
+        throw std::runtime_error("scheduler: step index out of range");
+    double alpha_s, sigma_s;
+    vp_of(s.sig[static_cast<size_t>(i)], &alpha_s, &sigma_s);
+    View e{eps, dt}, x{sample, dt};
+    std::vector<float> x0(static_cast<size_t>(n));
+    for (int64_t k = 0; k < n; ++k)
+        x0[k] = stored(static_cast<float>((x.get(k) - sigma_s * e.get(k)) / alpha_s), dt);
+    s.x0s.push_back(std::move(x0));
+    if (static_cast<int>(s.x0s.size()) > s.order_cap) s.x0s.erase(s.x0s.begin());
+    const bh_sched_coefficients c = sampler_coefficients(s, i);
+    const std::vector<float>& m0 = s.x0s.back();
+    const double ratio = c.sigma_vp_s0 > 0.0 ? c.sigma_vp_t / c.sigma_vp_s0 : 0.0;
+    const double coef = c.alpha_t * (c.exp_neg_h - 1.0);
+    Out y{sample, dt};
+    if (c.order == 1) {
+        for (int64_t k = 0; k < n; ++k)
+            y.set(k, static_cast<float>(ratio * static_cast<double>(x.get(k)) - coef * m0[k]));
+    } else {
+        const std::vector<float>& m1 = s.x0s[s.x0s.size() - 2];
+        for (int64_t k = 0; k < n; ++k) {
+            const double d0 = m0[k];
+            const double d1 = (1.0 / c.r0) * (d0 - m1[k]);
+            y.set(k, static_cast<float>(ratio * static_cast<double>(x.get(k)) - coef * d0 -
+                                        0.5 * coef * d1));
+        }
+    }
+    if (s.warm < s.order_cap) ++s.warm;
+}
+
 thread_local std::string g_err;
 
 template <typename Fn>
@@ -598,6 +745,66 @@ int stock_dit_forward(const bh_dit_config* cfg, const bh_dit_weights* w, int64_t
         if (!cfg || !w) throw std::runtime_error("stock_dit_forward: null argument");
         dit_forward(*cfg, *w, batch, latent_hw, caption_len, latent, timestep, caption, mask,
                     mask_dtype, image, resolve_threads(threads), layers);
+    });
+}
+
+
+int stock_repeat(const void* in, void* out, int64_t outer, int64_t inner, int dtype) {
+    return guard([&] { repeat_impl(in, out, outer, inner, dtype); });
+}
+
+int stock_guidance(const void* pred, void* out, int64_t out_channels, int64_t channels,
+                   int64_t spatial, float scale, int dtype) {
+    return guard([&] {
+        if (channels > out_channels) throw std::runtime_error("guidance: channels > out_channels");
+        guidance_impl(pred, out, out_channels, channels, spatial, scale, dtype);
+    });
+}
+
+// The sampler behind an opaque handle (host buffers only).
+int stock_sched_create(const bh_sched_config* cfg, void** out) {
+    return guard([&] {
+        if (!cfg || !out) throw std::runtime_error("stock_sched_create: null argument");
+        auto* s = new Sampler();
+        try {
+            sampler_init(*s, *cfg);
+        } catch (...) {
+            delete s;
+            throw;
+        }
+        *out = s;
+    });
+}
+
+void stock_sched_destroy(void* h) { delete static_cast<Sampler*>(h); }
+
+int stock_sched_set_timesteps(void* h, int steps) {
+    return guard([&] { sampler_set_timesteps(*static_cast<Sampler*>(h), steps); });
+}
+
+int stock_sched_steps(const void* h) { return static_cast<int>(static_cast<const Sampler*>(h)->ts.size()); }
+
+int stock_sched_timestep(const void* h, int i, int64_t* out) {
+    return guard([&] { *out = static_cast<const Sampler*>(h)->ts.at(static_cast<size_t>(i)); });
+}
+
+int stock_sched_sigma(const void* h, int i, double* out) {
+    return guard([&] { *out = static_cast<const Sampler*>(h)->sig.at(static_cast<size_t>(i)); });
+}
+
+int stock_sched_coefficients(const void* h, int i, bh_sched_coefficients* out) {
+    return guard([&] { *out = sampler_coefficients(*static_cast<const Sampler*>(h), i); });
+}
+
+int stock_sched_step(void* h, const void* eps, int i, void* sample, int64_t n, int dtype) {
+    return guard([&] { sampler_step(*static_cast<Sampler*>(h), eps, i, sample, n, dtype); });
+}
+
+int stock_sched_reset(void* h) {
+    return guard([&] {
+        auto* s = static_cast<Sampler*>(h);
+        s->x0s.clear();
+        s->warm = 0;
     });
 }
 

@@ -81,3 +81,72 @@ def assert_within(got, want, op: str, where: str = "") -> dict:
     assert s["rel_l2"] <= tol["rel_l2"], msg
     assert s["cosine"] >= tol["cosine"], msg
     return s
+
+
+# ---- the sampler through the oracle's (or the reference's) C entry points -------------------
+
+# The pinned schedule's timesteps at 20 steps (/root/reference/tests/test_scheduler.cpp:21-22).
+TIMESTEPS_20 = [999, 949, 899, 849, 799, 749, 699, 649, 599, 549,
+                500, 450, 400, 350, 300, 250, 200, 150, 100, 50]
+
+
+class HostSampler:
+    """DPM-Solver++ 2M on host buffers: `prefix` "stock" (oracle/stock.cpp) or "ref" (the
+    reference's own DPMSolverMultistep through oracle/ref_shim.cpp)."""
+
+    def __init__(self, lib, prefix: str, steps: int | None = 20, **overrides):
+        import burnisher_amd as bh
+        import oracle
+        self.lib, self.prefix = lib, prefix
+        self.h = ctypes.c_void_p()
+        self.cfg = bh.SchedConfig.pinned(**overrides)
+        oracle.call(lib, f"{prefix}_sched_create", ctypes.byref(self.cfg), ctypes.byref(self.h))
+        if steps is not None:
+            self.set_timesteps(steps)
+
+    def _call(self, name, *args):
+        import oracle
+        oracle.call(self.lib, f"{self.prefix}_{name}", self.h, *args)
+
+    def set_timesteps(self, steps: int):
+        self._call("sched_set_timesteps", steps)
+
+    def steps(self) -> int:
+        return getattr(self.lib, f"{self.prefix}_sched_steps")(self.h)
+
+    def timestep(self, i: int) -> int:
+        v = ctypes.c_int64()
+        self._call("sched_timestep", i, ctypes.byref(v))
+        return v.value
+
+    def sigma(self, i: int) -> float:
+        v = ctypes.c_double()
+        self._call("sched_sigma", i, ctypes.byref(v))
+        return v.value
+
+    def coefficients(self, i: int):
+        import burnisher_amd as bh
+        c = bh.SchedCoefficients()
+        self._call("sched_coefficients", i, ctypes.byref(c))
+        return c
+
+    def step(self, eps: np.ndarray, i: int, sample: np.ndarray, dtype: int):
+        """In place on `sample` (float32 for F32, uint16 bf16 bits for BF16)."""
+        assert eps.dtype == sample.dtype and eps.size == sample.size
+        self._call("sched_step", addr(eps), i, addr(sample), sample.size, dtype)
+
+    def reset(self):
+        self._call("sched_reset")
+
+    def close(self):
+        if self.h:
+            getattr(self.lib, f"{self.prefix}_sched_destroy")(self.h)
+            self.h = ctypes.c_void_p()
+
+
+COEFF_FIELDS = ("order", "sigma_s0", "sigma_t", "sigma_vp_s0", "sigma_vp_t", "alpha_t",
+                "alpha_s0", "exp_neg_h", "r0")
+
+
+def coeff_tuple(c) -> tuple:
+    return tuple(getattr(c, f) for f in COEFF_FIELDS)
