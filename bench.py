@@ -3,6 +3,7 @@
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--resolution 1024] [--no-cpu]
     python bench.py --kernels          # the isolated kernels at 1024px shapes, one line each
     python bench.py --probe NAME       # one kernel three times after a copy, for rocprofv3 --pmc
+    python bench.py --denoise 20       # the 20-step on-device denoise loop, eager vs HIP graph
 
 One step is one PixArt-Sigma dit-step forward (28 blocks, hidden 1152, 16 heads x 72, MLP 4608)
 at batch 2 (classifier-free guidance) over a 128x128x4 latent (4096 image tokens) and a
@@ -75,6 +76,9 @@ def parse() -> argparse.Namespace:
     p.add_argument("--probe", choices=sorted(KERNEL_SHAPES),
                    help="for counter collection: run a 256 MiB device copy (calibration) and the "
                         "named kernel at the dit-step shape three times each, then exit")
+    p.add_argument("--denoise", type=int, default=0, metavar="STEPS",
+                   help="time the whole on-device denoise loop (STEPS sampler steps, CFG 4.5) "
+                        "eagerly and as one HIP graph, one JSON line")
     p.add_argument("--kernels", action="store_true",
                    help="time the isolated kernels at 1024px shapes (GEMMs, self- and "
                         "cross-attention, LayerNorm+modulate); one JSON line per kernel")
@@ -188,6 +192,86 @@ def kernels(iters: int) -> int:
     return 0
 
 
+def denoise(args) -> int:
+    """The generate loop's denoise stage (pipeline.cpp:110-131) on the device: STEPS x (repeat,
+    dit-step, guidance, DPM-Solver++ step), from one seeded N(0,1) latent, timed per image with
+    HIP events on the loop's stream, eagerly (every launch from the host) and as one replayed
+    HIP graph. Each image restarts from the same noise; the restoring copy is outside the events."""
+    import numpy as np
+    import torch
+
+    import burnisher_amd as bh
+    from burnisher_amd.workload import PIXART_SIGMA, config_struct, dit_step_flops, make_workload
+
+    bh.check(bh.lib().bh_init(0), "bh_init")
+    hw = HW[args.resolution]
+    steps = args.denoise
+    wl = make_workload(PIXART_SIGMA, batch=2, latent_hw=hw, caption_len=args.caption_len)
+    top, blocks, _, caption, mask = wl.to_device()
+    cfg = config_struct(wl.cfg)
+    w, keep = wl.weight_struct(top, blocks)
+    engine, sched, den = ctypes.c_void_p(), ctypes.c_void_p(), ctypes.c_void_p()
+    bh.call("bh_dit_create", ctypes.byref(cfg), ctypes.byref(w), 2, hw, wl.caption_len,
+            bh.DIT_FUSED, ctypes.byref(engine))
+    scfg = bh.SchedConfig.pinned()
+    bh.call("bh_sched_create", ctypes.byref(scfg), ctypes.byref(sched))
+    bh.call("bh_sched_set_timesteps", sched, steps)
+    bh.call("bh_denoiser_create", engine, sched, 1, 4.5, ctypes.byref(den))
+    noise = bh.fill_normal_bf16(4 * hw * hw, "initial_latent", 0, 1.0)
+    init = torch.from_numpy(noise.view(np.int16)).cuda()
+    latent = torch.empty_like(init)
+    stream = torch.cuda.Stream()
+    sp = stream.cuda_stream
+
+    def run(graph: bool, reps: int) -> float:
+        total = 0.0
+        for _ in range(reps):
+            with torch.cuda.stream(stream):
+                latent.copy_(init)
+                a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                a.record(stream)
+                bh.call("bh_denoiser_run", den, latent.data_ptr(), caption.data_ptr(),
+                        mask.data_ptr(), bh.F32, int(graph), sp)
+                b.record(stream)
+            torch.cuda.synchronize()
+            total += a.elapsed_time(b)
+        return total / reps
+
+    reps = max(1, min(args.steps, 5))
+    log(f"denoise {steps} steps at {args.resolution}px: warmup (eager, then graph capture)")
+    run(False, 1)
+    eager_first = latent.clone()
+    t0 = time.perf_counter()
+    run(True, 1)
+    capture_s = time.perf_counter() - t0
+    assert torch.equal(latent, eager_first), "graph loop differs from the eager loop"
+    eager_ms = run(False, reps)
+    graph_ms = run(True, reps)
+    assert torch.equal(latent, eager_first), "graph replay differs from the eager loop"
+    res = latent.view(torch.bfloat16).float()
+    assert torch.isfinite(res).all() and res.std() > 1e-3, "degenerate denoised latent"
+    flops = dit_step_flops(wl.cfg, batch=2, latent_hw=hw, caption_len=wl.caption_len)["total"]
+    line = {
+        "metric": f"denoise loop ms/image @{args.resolution}px bf16, {steps} steps (1 GPU)",
+        "value": round(graph_ms, 3), "unit": "ms", "n_gpus": 1, "steps": reps, "warmup": 1,
+        "higher_is_better": False, "dtype": "bf16",
+        "data": "synthetic: seeded N(0,0.02) bf16 weights, N(0,1) caption and initial latent",
+        "config": {"workload": f"PixArt-Sigma denoise loop {args.resolution}px, CFG 4.5, "
+                               f"{steps} DPM-Solver++ 2M steps, caption {wl.caption_len}",
+                   "resolution": args.resolution, "sampler_steps": steps},
+        "graph_ms_per_image": round(graph_ms, 3), "eager_ms_per_image": round(eager_ms, 3),
+        "graph_ms_per_step": round(graph_ms / steps, 4),
+        "eager_ms_per_step": round(eager_ms / steps, 4),
+        "graph_capture_s": round(capture_s, 3),
+        "step_tflops_graph": round(flops / (graph_ms / steps * 1e-3) / 1e12, 2),
+    }
+    bh.lib().bh_denoiser_destroy(den)
+    bh.lib().bh_sched_destroy(sched)
+    bh.lib().bh_dit_destroy(engine)
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 def cpu_baseline(wl, threads: int) -> dict:
     """The stock oracle's whole dit-step (all 28 blocks) on this host, timed once."""
     import numpy as np
@@ -215,6 +299,8 @@ def main() -> int:
         return probe(args.probe)
     if args.kernels:
         return kernels(max(args.steps, 10))
+    if args.denoise:
+        return denoise(args)
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
               "(the dit-step would shard on the CFG batch, see DESIGN.md)", file=sys.stderr)
