@@ -152,6 +152,12 @@ struct DitGeometry {
     int mode;
 };
 DitGeometry dit_geometry(const bh_dit* e);
+// bh_dit_forward without the C error boundary (throws Error). With caption_ready, a fused engine
+// reuses the caption projection and cross-attention K/V of its previous forward, which must have
+// had the same caption; the op-by-op plan always recomputes them.
+void dit_forward_step(bh_dit* e, const void* latent, double timestep, const void* caption,
+                      const void* caption_mask, int mask_dtype, void* out, hipStream_t s,
+                      bool caption_ready);
 
 // Engine hint: which engine GEMM is running, so its launch is also credited to a sub-class.
 void set_gemm_subclass(int cls);

@@ -323,11 +323,10 @@ struct bh_denoiser {
         const int steps = static_cast<int>(sched->ts.size());
         for (int i = 0; i < steps; ++i) {
             bh::launch_repeat(latent, batched.p, g.batch, per, 2, s);
-            if (bh_dit_forward(dit, batched.p, static_cast<double>(sched->ts[i]), caption, mask,
-                               mask_dtype, pred.p, s) != 0) {
-                throw bh::Error(std::string("denoise step ") + std::to_string(i) + ": " +
-                                bh_last_error());
-            }
+            // The caption branch depends on nothing that changes between steps: computed at
+            // step 0, reused by the rest.
+            bh::dit_forward_step(dit, batched.p, static_cast<double>(sched->ts[i]), caption,
+                                 mask, mask_dtype, pred.p, s, i > 0);
             bh::launch_guidance(pred.p, guided, eps.p, g.out_channels, g.in_channels, spatial,
                                 guided ? scale : 0.0f, false, s);
             sched->step(eps.p, i, latent, per, BH_BF16, s);

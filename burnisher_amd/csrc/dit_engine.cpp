@@ -249,8 +249,11 @@ void gemm(const bf16_t* a, const void* w, const void* b, bf16_t* out, int64_t m,
 }
 
 // The MI355X plan.
+// `caption_ready`: the caption projection and every layer's cross-attention K/V (which depend
+// only on the caption) are already in e.cap / e.kv_all / e.vt_cross from an earlier forward
+// with the same caption, so that branch is skipped.
 void forward_fused(bh_dit& e, const void* latent, double t, const void* caption, const void* mask,
-                   int mask_dtype, void* out, hipStream_t s) {
+                   int mask_dtype, void* out, hipStream_t s, bool caption_ready = false) {
     const auto& c = e.cfg;
     const int64_t B = e.B, N = e.N, M = e.M, d = e.d, P = c.patch_size, L = c.num_layers;
     const int64_t H = c.num_heads, Dh = c.head_dim;
@@ -283,7 +286,7 @@ void forward_fused(bh_dit& e, const void* latent, double t, const void* caption,
         }
         gemm(e.silu_t.bf(), e.w.adaln_w, e.w.adaln_b, e.modulation.bf(), B, 6 * d, d, plain, s);
     }
-    {   // caption projection, then every layer's cross-attention K and V in one GEMM
+    if (!caption_ready) {   // caption projection, then every layer's cross-attention K and V
         GemmEpilogue gelu;
         gelu.act = 1;
         gemm(static_cast<const bf16_t*>(caption), e.w.cap1_w, e.w.cap1_b, e.cap_h.bf(), e.Mcap, d,
@@ -546,17 +549,28 @@ int bh_dit_create(const bh_dit_config* cfg, const bh_dit_weights* w, int64_t bat
 int bh_dit_forward(bh_dit* e, const void* latent, double timestep, const void* caption,
                    const void* caption_mask, int mask_dtype, void* out, void* stream) {
     return guarded([&] {
-        require(e != nullptr, "dit_forward: null engine");
-        require(latent && caption && caption_mask && out, "dit_forward: null tensor pointer");
-        require(mask_dtype == BH_F32 || mask_dtype == BH_BF16, "dit_forward: mask dtype");
-        hipStream_t s = static_cast<hipStream_t>(stream);
-        if (e->mode == BH_DIT_OPWISE) {
-            forward_opwise(*e, latent, timestep, caption, caption_mask, mask_dtype, out, s);
-        } else {
-            forward_fused(*e, latent, timestep, caption, caption_mask, mask_dtype, out, s);
-        }
+        dit_forward_step(e, latent, timestep, caption, caption_mask, mask_dtype, out,
+                         static_cast<hipStream_t>(stream), false);
     });
 }
+
+}  // extern "C"
+
+void bh::dit_forward_step(bh_dit* e, const void* latent, double timestep, const void* caption,
+                          const void* caption_mask, int mask_dtype, void* out, hipStream_t s,
+                          bool caption_ready) {
+    require(e != nullptr, "dit_forward: null engine");
+    require(latent && caption && caption_mask && out, "dit_forward: null tensor pointer");
+    require(mask_dtype == BH_F32 || mask_dtype == BH_BF16, "dit_forward: mask dtype");
+    if (e->mode == BH_DIT_OPWISE) {
+        forward_opwise(*e, latent, timestep, caption, caption_mask, mask_dtype, out, s);
+    } else {
+        forward_fused(*e, latent, timestep, caption, caption_mask, mask_dtype, out, s,
+                      caption_ready);
+    }
+}
+
+extern "C" {
 
 int64_t bh_dit_workspace_bytes(const bh_dit* e) { return e ? e->workspace : 0; }
 

@@ -174,7 +174,7 @@ def test_sched_reset_and_reuse(hip):
 # ---- the whole loop -------------------------------------------------------------------------
 
 
-def reference_loop(engine, latent0, steps, scale):
+def reference_loop(engine, latent0, steps, scale, caption=None):
     """pipeline.cpp:110-131 as the reference runs it: repeat -> DiT forward -> guidance on the
     device engine's output, then the sampler on host copies (here the oracle's guidance and
     sampler, which the tests above pin to the device ops bit for bit)."""
@@ -189,7 +189,7 @@ def reference_loop(engine, latent0, steps, scale):
         for i in range(steps):
             batched = np.tile(lat, (2, 1, 1, 1))
             engine.latent.view(torch.int16).copy_(torch.from_numpy(batched.view(np.int16)).cuda())
-            pred = engine.forward(timestep=float(sampler.timestep(i)))
+            pred = engine.forward(timestep=float(sampler.timestep(i)), caption=caption)
             eps = np.zeros((C, hw * hw), np.uint16)
             o.call(o.stock(), "stock_guidance", addr(pred), addr(eps), oc, C, hw * hw, scale, BF16)
             flat = lat.reshape(-1)
@@ -237,6 +237,36 @@ def test_denoiser_matches_reference_loop(hip):
         lat = dev(latent0)
         d.run(lat, graph=False)
         assert np.array_equal(host(lat, latent0), want)
+    finally:
+        d.close()
+        e.close()
+
+
+def test_denoiser_recomputes_a_new_caption(hip):
+    """Steps after the first reuse the caption branch of step 0; a new caption (or new caption
+    contents) in the next run is projected afresh."""
+    import torch
+    print("denoiser with two captions, small config", flush=True)
+    e = small_engine()
+    d = Denoiser(e, 4, 3.0)
+    try:
+        C, hw = SMALL["in_channels"], e.wl.latent_hw
+        latent0 = to_bf16(np.random.default_rng(4).standard_normal((1, C, hw, hw)))
+        other = to_bf16(np.random.default_rng(5).standard_normal(tuple(e.caption.shape)))
+        cap2 = torch.from_numpy(other.view(np.int16)).cuda()
+        lat = dev(latent0)
+        d.run(lat, graph=False)
+        lat2 = dev(latent0)
+        d.run(lat2, graph=False, caption=cap2)
+        assert np.array_equal(host(lat2, latent0), reference_loop(e, latent0, 4, 3.0, caption=cap2))
+        # Same pointer, new contents, through the graph.
+        g = dev(latent0)
+        d.run(g, graph=True)
+        assert np.array_equal(host(g, latent0), host(lat, latent0))
+        e.caption.view(torch.int16).copy_(cap2)
+        g.copy_(torch.from_numpy(latent0.view(np.int16)).cuda())
+        d.run(g, graph=True)
+        assert np.array_equal(host(g, latent0), host(lat2, latent0))
     finally:
         d.close()
         e.close()
