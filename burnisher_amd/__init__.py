@@ -17,6 +17,8 @@ PKG = Path(__file__).resolve().parent
 LIB_PATH = PKG / "lib" / "libburnisher_hip.so"
 
 F32, BF16 = 0, 1
+ST_F32, ST_BF16, ST_F16, ST_F8_E4M3 = 0, 1, 2, 3
+ST_DTYPES = {ST_F32: "F32", ST_BF16: "BF16", ST_F16: "F16", ST_F8_E4M3: "F8_E4M3"}
 EPI_NONE, EPI_GELU, EPI_SILU, EPI_GELU_GATED = 0, 1, 2, 3
 DIT_FUSED, DIT_OPWISE = 0, 1
 (K_GEMM, K_GEMV, K_ATTN_SELF, K_ATTN_CROSS, K_NORM, K_ELEMENTWISE, K_GEMM_FF0, K_GEMM_FF2,
@@ -139,6 +141,19 @@ SIGNATURES = {
     "bh_denoiser_create": ([_V, _V, _I, _F, ctypes.POINTER(_V)], _I),
     "bh_denoiser_run": ([_V, _V, _V, _V, _I, _I, _V], _I),
     "bh_denoiser_destroy": ([_V], None),
+    "bh_checkpoint_open": ([ctypes.POINTER(ctypes.c_char_p), _I, ctypes.POINTER(_V)], _I),
+    "bh_checkpoint_open_component": ([ctypes.c_char_p, ctypes.c_char_p, ctypes.POINTER(_V)], _I),
+    "bh_checkpoint_close": ([_V], None),
+    "bh_checkpoint_count": ([_V], _I64),
+    "bh_checkpoint_entry": ([_V, _I64, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(_I),
+                             ctypes.POINTER(_I), ctypes.POINTER(_I64), _I], _I),
+    "bh_checkpoint_find": ([_V, ctypes.c_char_p, ctypes.POINTER(_I), ctypes.POINTER(_I),
+                            ctypes.POINTER(_I64), _I], _I),
+    "bh_checkpoint_read": ([_V, ctypes.c_char_p, _I, _V, _I64], _I),
+    "bh_dit_weights_load": ([_V, ctypes.POINTER(DitConfig), _V, ctypes.POINTER(_V)], _I),
+    "bh_dit_weights_view": ([_V], ctypes.POINTER(DitWeights)),
+    "bh_dit_weights_bytes": ([_V], _I64),
+    "bh_dit_weights_free": ([_V], None),
 }
 
 
@@ -188,3 +203,110 @@ def fill_normal_bf16(n: int, name: str, seed: int, std: float):
     out = np.empty(n, dtype=np.uint16)
     call("bh_fill_normal_bf16", out.ctypes.data, n, seed, name.encode(), std)
     return out
+
+
+# ---- checkpoints ---------------------------------------------------------------------------
+
+class Checkpoint:
+    """A safetensors checkpoint component, memory-mapped by the library (bh_checkpoint_*).
+
+    Mirrors the reference's CheckpointWeights (src/models/weights.cpp:26-69): `has`, `shape`,
+    `read` (host conversion to bf16 bits or fp32) and `require`, whose miss names near misses.
+    """
+
+    MAX_RANK = 8
+
+    def __init__(self, handle: int):
+        self._h = ctypes.c_void_p(handle)
+
+    @classmethod
+    def open(cls, *shards) -> "Checkpoint":
+        paths = (ctypes.c_char_p * len(shards))(*[os.fsencode(str(p)) for p in shards])
+        h = ctypes.c_void_p()
+        call("bh_checkpoint_open", paths, len(shards), ctypes.byref(h))
+        return cls(h.value)
+
+    @classmethod
+    def component(cls, directory, name: str) -> "Checkpoint":
+        h = ctypes.c_void_p()
+        call("bh_checkpoint_open_component", os.fsencode(str(directory)), name.encode(),
+             ctypes.byref(h))
+        return cls(h.value)
+
+    @property
+    def handle(self) -> ctypes.c_void_p:
+        if self._h is None:
+            raise BurnisherError("checkpoint is closed")
+        return self._h
+
+    def close(self) -> None:
+        if self._h is not None:
+            lib().bh_checkpoint_close(self._h)
+            self._h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def entries(self) -> list[tuple[str, str, tuple]]:
+        """(name, dtype name, shape) of every tensor, shard by shard, in name order."""
+        out = []
+        shape = (ctypes.c_int64 * self.MAX_RANK)()
+        name, dt, rank = ctypes.c_char_p(), ctypes.c_int(), ctypes.c_int()
+        for i in range(lib().bh_checkpoint_count(self.handle)):
+            call("bh_checkpoint_entry", self.handle, i, ctypes.byref(name), ctypes.byref(dt),
+                 ctypes.byref(rank), shape, self.MAX_RANK)
+            out.append((name.value.decode(), ST_DTYPES[dt.value], tuple(shape[:rank.value])))
+        return out
+
+    def require(self, name: str) -> tuple[str, tuple]:
+        """(dtype name, shape) of `name`; raises naming near misses when it is absent."""
+        shape = (ctypes.c_int64 * self.MAX_RANK)()
+        dt, rank = ctypes.c_int(), ctypes.c_int()
+        call("bh_checkpoint_find", self.handle, name.encode(), ctypes.byref(dt),
+             ctypes.byref(rank), shape, self.MAX_RANK)
+        return ST_DTYPES[dt.value], tuple(shape[:rank.value])
+
+    def has(self, name: str) -> bool:
+        return lib().bh_checkpoint_find(self.handle, name.encode(), None, None, None, 0) == 0
+
+    def read(self, name: str, dtype: int = BF16):
+        """The tensor converted on the host: bf16 bits (uint16) or float32, in its shape."""
+        import numpy as np
+        _, shape = self.require(name)
+        out = np.empty(shape, dtype=np.uint16 if dtype == BF16 else np.float32)
+        call("bh_checkpoint_read", self.handle, name.encode(), dtype, out.ctypes.data, out.size)
+        return out
+
+
+class DitDeviceWeights:
+    """The DiT's weights from a checkpoint, bf16 in one device arena (bh_dit_weights_load).
+
+    `weights` is the DitWeights struct bh_dit_create takes; it stays valid until `free`."""
+
+    def __init__(self, checkpoint: Checkpoint, cfg: DitConfig, stream=None):
+        h = ctypes.c_void_p()
+        call("bh_dit_weights_load", checkpoint.handle, ctypes.byref(cfg), stream, ctypes.byref(h))
+        self._h = h
+        self.weights = lib().bh_dit_weights_view(h).contents
+        self.bytes = lib().bh_dit_weights_bytes(h)
+
+    def free(self) -> None:
+        if self._h is not None:
+            lib().bh_dit_weights_free(self._h)
+            self._h = None
+            self.weights = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass

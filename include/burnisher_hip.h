@@ -343,6 +343,51 @@ int bh_profile_read(int kernel_class, double* total_ms, int64_t* launches, doubl
  * 2*(i/2) and 2*(i/2)+1, so the result does not depend on how the work is split. Host only. */
 int bh_fill_normal_bf16(uint16_t* dst, int64_t n, uint64_t seed, const char* name, float std_dev);
 
+/* ---- checkpoints: safetensors shards and the DiT's device weights -------------------------- */
+
+/* Element types a safetensors header may name (safetensors.cpp:186-195). */
+typedef enum bh_st_dtype { BH_ST_F32 = 0, BH_ST_BF16 = 1, BH_ST_F16 = 2, BH_ST_F8_E4M3 = 3 } bh_st_dtype;
+
+typedef struct bh_checkpoint bh_checkpoint;
+
+/* CheckpointWeights(paths) (weights.cpp:51-54) over SafeTensors::open (safetensors.cpp:207-250):
+ * every shard memory-mapped read-only and its header parsed and checked (dtype known, byte range
+ * equal to shape x dtype size, inside the file). Host only. */
+int bh_checkpoint_open(const char* const* shard_paths, int n_shards, bh_checkpoint** out);
+/* CheckpointWeights::component (weights.cpp:26-49): the sorted *.safetensors of <dir>/<component>. */
+int bh_checkpoint_open_component(const char* dir, const char* component, bh_checkpoint** out);
+void bh_checkpoint_close(bh_checkpoint* ck);
+/* Number of tensors over all shards (-1 for a null handle); entries are in shard order, then
+ * name order within a shard. */
+int64_t bh_checkpoint_count(const bh_checkpoint* ck);
+/* Entry `index`: its name (valid while the checkpoint is open), bh_st_dtype and shape. */
+int bh_checkpoint_entry(const bh_checkpoint* ck, int64_t index, const char** name, int* dtype,
+                        int* rank, int64_t* shape, int max_rank);
+/* WeightSource::require (weights.cpp:14-24, 56-65): the entry named `name` in the first shard
+ * holding it; a miss is an error naming up to five near misses (safetensors.cpp:256-280). */
+int bh_checkpoint_find(const bh_checkpoint* ck, const char* name, int* dtype, int* rank,
+                       int64_t* shape, int max_rank);
+/* Tensor::convert_into (tensor.cpp:130-160): `numel` elements of `name` into host memory as
+ * `dtype` (BH_BF16: fp32 rounded to nearest even; BH_F32). F16 and F8_E4M3 have no per-element
+ * conversion in the reference (tensor.cpp:68-82) and are refused. */
+int bh_checkpoint_read(const bh_checkpoint* ck, const char* name, int dtype, void* dst,
+                       int64_t numel);
+
+typedef struct bh_dit_device_weights bh_dit_device_weights;
+
+/* DeviceWeights over the DiT's tensors (weights.cpp:198-217, names and shapes of
+ * declare_pixart_shapes, weights.cpp:246-282): every tensor the configuration needs is checked
+ * (present, shape, F32 or BF16) before anything is allocated, then converted to bf16 on the host
+ * into page-locked staging and copied into one device arena on `stream`. Returns after the
+ * copies have completed. Allocates (the arena, 32 MiB of staging while it runs). */
+int bh_dit_weights_load(const bh_checkpoint* ck, const bh_dit_config* cfg, void* stream,
+                        bh_dit_device_weights** out);
+/* The loaded weights as the struct bh_dit_create takes; valid until bh_dit_weights_free. */
+const bh_dit_weights* bh_dit_weights_view(const bh_dit_device_weights* w);
+/* Device bytes of the arena (-1 for a null handle). */
+int64_t bh_dit_weights_bytes(const bh_dit_device_weights* w);
+void bh_dit_weights_free(bh_dit_device_weights* w);
+
 #ifdef __cplusplus
 }
 #endif
