@@ -343,6 +343,27 @@ int bh_profile_read(int kernel_class, double* total_ms, int64_t* launches, doubl
  * 2*(i/2) and 2*(i/2)+1, so the result does not depend on how the work is split. Host only. */
 int bh_fill_normal_bf16(uint16_t* dst, int64_t n, uint64_t seed, const char* name, float std_dev);
 
+/* ---- the VAE decoder (the vae-decode stage, vae_decoder.cpp) ------------------------------ */
+
+/* VaeConfig (models.h:120-130). */
+typedef struct bh_vae_config {
+    int block_out_channels[8]; /* {128, 256, 512, 512}: decoder up-blocks use them reversed */
+    int num_blocks;            /* 4 */
+    int layers_per_block;      /* 2: each up-block has layers_per_block + 1 resnets */
+    int latent_channels;       /* 4 */
+    int norm_num_groups;       /* 32 */
+    double eps;                /* 1e-6 */
+} bh_vae_config;
+
+/* The decoder's weights by checkpoint name (the VAE part of declare_pixart_shapes,
+ * weights.cpp:284-320): `count` names, each with a bf16 tensor in the checkpoint layout
+ * (convolutions [out, in, k, k]; linear [out, in]; norms [channels]). */
+typedef struct bh_vae_weights {
+    int count;
+    const char* const* names;
+    const void* const* tensors;
+} bh_vae_weights;
+
 /* ---- checkpoints: safetensors shards and the DiT's device weights -------------------------- */
 
 /* Element types a safetensors header may name (safetensors.cpp:186-195). */

@@ -46,6 +46,11 @@ _STOCK_SIGS = {
     "stock_sched_coefficients": ([_V, _I, _V], _I),
     "stock_sched_step": ([_V, _V, _I, _V, _I64, _I], _I),
     "stock_sched_reset": ([_V], _I),
+    "stock_conv2d": ([_V, _V, _V, _V, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I, _I], _I),
+    "stock_group_norm": ([_V, _V, _V, _V, _I64, _I64, _F, _I64, _I64, _I, _I], _I),
+    "stock_upsample": ([_V, _V, _I64, _I64, _I64, _I64, _I64, _I], _I),
+    "stock_transpose": ([_V, _V, _I64, _I64, _I64, _I, _I], _I),
+    "stock_vae_forward": ([_V, _V, _V, _I64, _V, _I, _I], _I),
 }
 _REF_SIGS = {
     "ref_last_error": ([], ctypes.c_char_p),
@@ -71,6 +76,11 @@ _REF_SIGS = {
     "ref_sched_coefficients": ([_V, _I, _V], _I),
     "ref_sched_step": ([_V, _V, _I, _V, _I64, _I], _I),
     "ref_sched_reset": ([_V], _I),
+    "ref_conv2d": ([_V, _V, _V, _V, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I], _I),
+    "ref_group_norm": ([_V, _V, _V, _V, _I64, _I64, _F, _I64, _I64, _I], _I),
+    "ref_upsample": ([_V, _V, _I64, _I64, _I64, _I64, _I64, _I], _I),
+    "ref_transpose": ([_V, _V, _I64, _I64, _I64, _I, _I], _I),
+    "ref_vae_forward": ([_V, _V, _V, _I64, _V], _I),
 }
 
 _stock = None

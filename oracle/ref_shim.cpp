@@ -108,6 +108,26 @@ class TableWeights : public WeightSource {
     std::map<std::string, Tensor> m_;
 };
 
+// Serves a name-keyed table of bf16 tensors (the VAE's weights) with the shapes the reference
+// itself declares for those names.
+class NamedWeights : public WeightSource {
+  public:
+    explicit NamedWeights(const bh_vae_weights& w) {
+        for (int i = 0; i < w.count; ++i) ptr_[w.names[i]] = w.tensors[i];
+    }
+    bool has(const std::string& name) const override { return ptr_.count(name) != 0; }
+    Tensor get(const std::string& name) const override {
+        auto it = ptr_.find(name);
+        if (it == ptr_.end()) throw std::runtime_error("ref vae weights: no '" + name + "'");
+        return view(it->second, shape_.at(name), BH_BF16);
+    }
+    void set_shape(const std::string& name, std::vector<int64_t> shape) { shape_[name] = std::move(shape); }
+
+  private:
+    std::map<std::string, const void*> ptr_;
+    std::map<std::string, std::vector<int64_t>> shape_;
+};
+
 }  // namespace
 
 extern "C" {
@@ -324,6 +344,78 @@ int ref_sched_step(void* h, const void* eps, int i, void* sample, int64_t n, int
 
 int ref_sched_reset(void* h) {
     return guard([&] { static_cast<DPMSolverMultistep*>(h)->reset(); });
+}
+
+int ref_conv2d(const void* x, const void* w, const void* bias, void* out, int64_t batch, int64_t c_in,
+               int64_t h, int64_t wd, int64_t c_out, int64_t k, int64_t pad, int dtype) {
+    return guard([&] {
+        const int64_t ho = h + 2 * pad - k + 1, wo = wd + 2 * pad - k + 1;
+        Tensor tx = view(x, {batch, c_in, h, wd}, dtype), tw = view(w, {c_out, c_in, k, k}, dtype);
+        Tensor tb = bias ? view(bias, {c_out}, dtype) : Tensor();
+        Tensor to = view(out, {batch, c_out, ho, wo}, dtype);
+        Conv2dArgs a{&tx, &tw, bias ? &tb : nullptr, &to, batch, c_in, h, wd, c_out, k, pad};
+        Conv2dRegistry::instance().get("stock")(a);
+    });
+}
+
+int ref_group_norm(const void* x, const void* weight, const void* bias, void* out, int64_t rows,
+                   int64_t cols, float eps, int64_t groups, int64_t channels, int dtype) {
+    return guard([&] {
+        Tensor tx = view(x, {rows, cols}, dtype), to = view(out, {rows, cols}, dtype);
+        Tensor tw = weight ? view(weight, {channels}, dtype) : Tensor();
+        Tensor tb = bias ? view(bias, {channels}, dtype) : Tensor();
+        NormArgs a{&tx, weight ? &tw : nullptr, bias ? &tb : nullptr, &to, rows, cols, eps, false,
+                   groups, channels};
+        NormRegistry::instance().get("stock")(a);
+    });
+}
+
+int ref_upsample(const void* in, void* out, int64_t batch, int64_t channels, int64_t h, int64_t w,
+                 int64_t factor, int dtype) {
+    return guard([&] {
+        Tensor ti = view(in, {batch, channels, h, w}, dtype);
+        Tensor to = view(out, {batch, channels, h * factor, w * factor}, dtype);
+        UpsampleArgs a{&ti, &to, batch, channels, h, w, factor};
+        UpsampleRegistry::instance().get("stock")(a);
+    });
+}
+
+int ref_transpose(const void* in, void* out, int64_t batch, int64_t channels, int64_t spatial,
+                  int to_channels_first, int dtype) {
+    return guard([&] {
+        std::vector<int64_t> cf{batch, channels, spatial}, sf{batch, spatial, channels};
+        Tensor ti = view(in, to_channels_first ? sf : cf, dtype);
+        Tensor to = view(out, to_channels_first ? cf : sf, dtype);
+        TransposeArgs a{&ti, &to, batch, channels, spatial, to_channels_first != 0};
+        TransposeRegistry::instance().get("stock")(a);
+    });
+}
+
+// VaeDecoder::forward (vae_decoder.cpp:127-180) on the reference's own model code; the weight
+// shapes come from its own declaration (declare_pixart_shapes, weights.cpp:284-320).
+int ref_vae_forward(const bh_vae_config* cfg, const bh_vae_weights* w, const uint16_t* latent,
+                    int64_t latent_hw, uint16_t* image) {
+    return guard([&] {
+        VaeConfig vc;
+        vc.block_out_channels.assign(cfg->block_out_channels, cfg->block_out_channels + cfg->num_blocks);
+        vc.layers_per_block = cfg->layers_per_block;
+        vc.latent_channels = cfg->latent_channels;
+        vc.norm_num_groups = cfg->norm_num_groups;
+        vc.eps = cfg->eps;
+        NamedWeights nw(*w);
+        T5Config t5;
+        t5.num_layers = 0;
+        DiTConfig dit;
+        dit.num_layers = 0;
+        SyntheticWeights decl(DType::BF16, 0);
+        declare_pixart_shapes(decl, t5, dit, vc);
+        for (int i = 0; i < w->count; ++i) nw.set_shape(w->names[i], decl.get(w->names[i]).shape());
+        VaeDecoder dec(vc, nw, DType::BF16);
+        const ImplSelection impls = ImplSelection::from_request("stock", Device::CPU);
+        Tensor x = view(latent, {1, vc.latent_channels, latent_hw, latent_hw}, BH_BF16);
+        Tensor out = dec.forward(x, impls);
+        std::memcpy(image, out.data(), static_cast<size_t>(out.numel()) * 2);
+    });
 }
 
 }  // extern "C"

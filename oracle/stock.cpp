@@ -648,6 +648,215 @@ void sampler_step(Sampler& s, const void* eps, int i, void* sample, int64_t n, i
     if (s.warm < s.order_cap) ++s.warm;
 }
 
+// ---- the VAE decoder's ops (ops_cpu.cpp:186-224, 276-300, 384-412) -----------------------------
+
+// GroupNorm (ops_cpu.cpp:186-224): rows = batch, cols = channels * spatial (NCHW), the group split
+// over channels: per (row, group) an fp64 mean, then an fp64 sum of squared deviations, inv =
+// 1/sqrt(float(var) + eps), (x - float(mean)) * inv, then * weight[channel], + bias[channel].
+void group_norm_impl(const void* x, const void* w, const void* bias, void* out, int64_t rows,
+                     int64_t cols, float eps, int64_t groups, int64_t channels, int dt,
+                     int threads) {
+    const int64_t per_group = cols / groups;
+    if (channels && (channels % groups)) throw std::runtime_error("groupnorm: channels not divisible by groups");
+    if (per_group * groups != cols) throw std::runtime_error("groupnorm: channels*spatial not divisible by groups");
+    const View xv{x, dt}, wv{w, dt}, bv{bias, dt};
+    const Out o{out, dt};
+    const int64_t spatial = channels ? cols / channels : 1;
+    parallel_for(rows * groups, threads, [&](int64_t rg) {
+        const int64_t r = rg / groups, g = rg - r * groups;
+        const int64_t base = r * cols + g * per_group;
+        double mean = 0.0;
+        for (int64_t i = 0; i < per_group; ++i) mean += xv.get(base + i);
+        mean /= per_group;
+        double var = 0.0;
+        for (int64_t i = 0; i < per_group; ++i) {
+            double d = xv.get(base + i) - mean;
+            var += d * d;
+        }
+        var /= per_group;
+        const float inv = 1.0f / std::sqrt(static_cast<float>(var) + eps);
+        for (int64_t i = 0; i < per_group; ++i) {
+            float v = (xv.get(base + i) - static_cast<float>(mean)) * inv;
+            if (w || bias) {
+                const int64_t ch = (g * per_group + i) / spatial;
+                if (w) v *= wv.get(ch);
+                if (bias) v += bv.get(ch);
+            }
+            o.set(base + i, v);
+        }
+    });
+}
+
+// conv2d (ops_cpu.cpp:276-300), NCHW, stride 1: acc starts at the bias, then ic, ky, kx in that
+// order, taps outside the input skipped, one fp32 product and add each. Vectorised across ox
+// (independent outputs); every output sees the same sequence of operations.
+void conv2d_impl(const void* x, const void* w, const void* bias, void* out, int64_t B,
+                 int64_t ci, int64_t H, int64_t W, int64_t co, int64_t k, int64_t pad, int dt,
+                 int threads) {
+    const int64_t Ho = H + 2 * pad - k + 1, Wo = W + 2 * pad - k + 1;
+    const std::vector<float> xf = widen(x, dt, B * ci * H * W);
+    const std::vector<float> wf = widen(w, dt, co * ci * k * k);
+    const View bv{bias, dt};
+    const Out o{out, dt};
+    parallel_for(B * co * Ho, threads, [&](int64_t row) {
+        const int64_t oy = row % Ho, oc = (row / Ho) % co, b = row / (Ho * co);
+        std::vector<float> acc(static_cast<size_t>(Wo), bias ? bv.get(oc) : 0.0f);
+        for (int64_t ic = 0; ic < ci; ++ic)
+            for (int64_t ky = 0; ky < k; ++ky) {
+                const int64_t iy = oy + ky - pad;
+                if (iy < 0 || iy >= H) continue;
+                const float* xr = &xf[static_cast<size_t>(((b * ci + ic) * H + iy) * W)];
+                for (int64_t kx = 0; kx < k; ++kx) {
+                    const float wt = wf[static_cast<size_t>(((oc * ci + ic) * k + ky) * k + kx)];
+                    const int64_t lo = std::max<int64_t>(0, pad - kx), hi = std::min<int64_t>(Wo, W + pad - kx);
+                    for (int64_t ox = lo; ox < hi; ++ox) acc[ox] += xr[ox + kx - pad] * wt;
+                }
+            }
+        for (int64_t ox = 0; ox < Wo; ++ox) o.set(((b * co + oc) * Ho + oy) * Wo + ox, acc[ox]);
+    });
+}
+
+// Nearest upsample (ops_cpu.cpp:384-397) and the [C, S] <-> [S, C] transpose (:399-412): copies.
+void upsample_impl(const void* in, void* out, int64_t B, int64_t C, int64_t H, int64_t W,
+                   int64_t f, int dt) {
+    const int64_t es = dt == BH_F32 ? 4 : 2, H2 = H * f, W2 = W * f;
+    const char* src = static_cast<const char*>(in);
+    char* dst = static_cast<char*>(out);
+    for (int64_t bc = 0; bc < B * C; ++bc)
+        for (int64_t y = 0; y < H2; ++y)
+            for (int64_t x = 0; x < W2; ++x)
+                std::memcpy(dst + ((bc * H2 + y) * W2 + x) * es, src + ((bc * H + y / f) * W + x / f) * es, es);
+}
+
+void transpose_impl(const void* in, void* out, int64_t B, int64_t C, int64_t S, bool to_cf, int dt) {
+    const int64_t es = dt == BH_F32 ? 4 : 2;
+    const char* src = static_cast<const char*>(in);
+    char* dst = static_cast<char*>(out);
+    for (int64_t b = 0; b < B; ++b)
+        for (int64_t c = 0; c < C; ++c)
+            for (int64_t s = 0; s < S; ++s) {
+                const int64_t cf = (b * C + c) * S + s, sf = (b * S + s) * C + c;
+                if (to_cf) std::memcpy(dst + cf * es, src + sf * es, es);
+                else std::memcpy(dst + sf * es, src + cf * es, es);
+            }
+}
+
+// ---- the VAE decoder graph (vae_decoder.cpp:127-180), NCHW, batch 1 ----------------------------
+
+struct VaeTable {
+    std::vector<std::pair<std::string, const void*>> t;
+    const void* at(const std::string& n) const {
+        for (const auto& kv : t)
+            if (kv.first == n) return kv.second;
+        throw std::runtime_error("vae weights: '" + n + "' is missing");
+    }
+};
+
+struct VaeRun {
+    const VaeTable& w;
+    double eps;
+    int64_t groups;
+    int threads;
+    using Buf = std::vector<uint16_t>;
+
+    Buf conv(const Buf& x, const std::string& n, int64_t ci, int64_t co, int64_t h, int64_t k,
+             int64_t pad) const {
+        const int64_t ho = h + 2 * pad - k + 1;
+        Buf out(static_cast<size_t>(co * ho * ho));
+        conv2d_impl(x.data(), w.at(n + ".weight"), w.at(n + ".bias"), out.data(), 1, ci, h, h, co,
+                    k, pad, BH_BF16, threads);
+        return out;
+    }
+    Buf gn(const Buf& x, const std::string& n, int64_t ch, int64_t h) const {
+        Buf out(x.size());
+        group_norm_impl(x.data(), w.at(n + ".weight"), w.at(n + ".bias"), out.data(), 1, ch * h * h,
+                        static_cast<float>(eps), groups, ch, BH_BF16, threads);
+        return out;
+    }
+    Buf silu(const Buf& x) const {
+        Buf out(x.size());
+        activation_impl(x.data(), out.data(), static_cast<int64_t>(x.size()), BH_EPI_SILU, nullptr, BH_BF16);
+        return out;
+    }
+    Buf add(const Buf& a, const Buf& b) const {
+        Buf out(a.size());
+        add_impl(a.data(), b.data(), out.data(), 1, static_cast<int64_t>(a.size()), 1.0f, false, BH_BF16);
+        return out;
+    }
+    Buf resnet(const Buf& x, const std::string& n, int64_t ci, int64_t co, int64_t h) const {
+        Buf t = silu(gn(x, n + ".norm1", ci, h));
+        t = conv(t, n + ".conv1", ci, co, h, 3, 1);
+        t = silu(gn(t, n + ".norm2", co, h));
+        t = conv(t, n + ".conv2", co, co, h, 3, 1);
+        const Buf skip = ci != co ? conv(x, n + ".conv_shortcut", ci, co, h, 1, 0) : x;
+        return add(skip, t);
+    }
+    Buf attention(const Buf& x, const std::string& n, int64_t ch, int64_t h) const {
+        const int64_t s = h * h;
+        const Buf normed = gn(x, n + ".group_norm", ch, h);
+        Buf seq(static_cast<size_t>(s * ch));
+        transpose_impl(normed.data(), seq.data(), 1, ch, s, false, BH_BF16);
+        Buf q(seq.size()), k(seq.size()), v(seq.size()), o(seq.size()), proj(seq.size());
+        const std::pair<const char*, Buf*> qkv[3] = {{"to_q", &q}, {"to_k", &k}, {"to_v", &v}};
+        for (const auto& pr : qkv)
+            gemm_impl(seq.data(), w.at(n + "." + pr.first + ".weight"), w.at(n + "." + pr.first + ".bias"),
+                      pr.second->data(), s, ch, ch, true, BH_EPI_NONE, BH_BF16, threads);
+        attention_impl(q.data(), k.data(), v.data(), o.data(), AttnGeom{1, 1, s, s, ch, ch, ch, ch}, 0.0f,
+                       nullptr, nullptr, BH_F32, BH_BF16, threads, false);
+        gemm_impl(o.data(), w.at(n + ".to_out.0.weight"), w.at(n + ".to_out.0.bias"), proj.data(), s,
+                  ch, ch, true, BH_EPI_NONE, BH_BF16, threads);
+        Buf back(seq.size());
+        transpose_impl(proj.data(), back.data(), 1, ch, s, true, BH_BF16);
+        return add(x, back);
+    }
+    Buf upsample(const Buf& x, int64_t ch, int64_t h) const {
+        Buf out(x.size() * 4);
+        upsample_impl(x.data(), out.data(), 1, ch, h, h, 2, BH_BF16);
+        return out;
+    }
+};
+
+void vae_forward(const bh_vae_config& c, const VaeTable& w, const uint16_t* latent, int64_t h,
+                 uint16_t* image, int threads, int stop_after) {
+    VaeRun r{w, c.eps, c.norm_num_groups, threads};
+    std::vector<int64_t> rev;
+    for (int i = c.num_blocks - 1; i >= 0; --i) rev.push_back(c.block_out_channels[i]);
+    const int64_t zc = c.latent_channels;
+    VaeRun::Buf x(latent, latent + zc * h * h);
+    x = r.conv(x, "post_quant_conv", zc, zc, h, 1, 0);
+    x = r.conv(x, "decoder.conv_in", zc, rev[0], h, 3, 1);
+    x = r.resnet(x, "decoder.mid_block.resnets.0", rev[0], rev[0], h);
+    x = r.attention(x, "decoder.mid_block.attentions.0", rev[0], h);
+    x = r.resnet(x, "decoder.mid_block.resnets.1", rev[0], rev[0], h);
+    int64_t prev = rev[0];
+    for (size_t i = 0; i < rev.size(); ++i) {
+        if (stop_after >= 0 && static_cast<int>(i) >= stop_after) break;
+        const int64_t co = rev[i];
+        for (int j = 0; j <= c.layers_per_block; ++j)
+            x = r.resnet(x, "decoder.up_blocks." + std::to_string(i) + ".resnets." + std::to_string(j),
+                         j == 0 ? prev : co, co, h);
+        prev = co;
+        if (i + 1 != rev.size()) {
+            x = r.upsample(x, co, h);
+            h *= 2;
+            x = r.conv(x, "decoder.up_blocks." + std::to_string(i) + ".upsamplers.0.conv", co, co, h, 3, 1);
+        }
+    }
+    if (stop_after >= 0) {   // a truncated decoder returns the activation where it stopped
+        std::memcpy(image, x.data(), x.size() * 2);
+        return;
+    }
+    x = r.silu(r.gn(x, "decoder.conv_norm_out", prev, h));
+    x = r.conv(x, "decoder.conv_out", prev, 3, h, 3, 1);
+    std::memcpy(image, x.data(), x.size() * 2);
+}
+
+VaeTable vae_table(const bh_vae_weights& w) {
+    VaeTable t;
+    for (int i = 0; i < w.count; ++i) t.t.emplace_back(w.names[i], w.tensors[i]);
+    return t;
+}
+
 thread_local std::string g_err;
 
 template <typename Fn>
@@ -805,6 +1014,40 @@ int stock_sched_reset(void* h) {
         auto* s = static_cast<Sampler*>(h);
         s->x0s.clear();
         s->warm = 0;
+    });
+}
+
+int stock_conv2d(const void* x, const void* w, const void* bias, void* out, int64_t batch,
+                 int64_t c_in, int64_t h, int64_t wd, int64_t c_out, int64_t k, int64_t pad,
+                 int dtype, int threads) {
+    return guard([&] {
+        conv2d_impl(x, w, bias, out, batch, c_in, h, wd, c_out, k, pad, dtype, resolve_threads(threads));
+    });
+}
+
+int stock_group_norm(const void* x, const void* weight, const void* bias, void* out, int64_t rows,
+                     int64_t cols, float eps, int64_t groups, int64_t channels, int dtype,
+                     int threads) {
+    return guard([&] {
+        group_norm_impl(x, weight, bias, out, rows, cols, eps, groups, channels, dtype,
+                        resolve_threads(threads));
+    });
+}
+
+int stock_upsample(const void* in, void* out, int64_t batch, int64_t channels, int64_t h,
+                   int64_t w, int64_t factor, int dtype) {
+    return guard([&] { upsample_impl(in, out, batch, channels, h, w, factor, dtype); });
+}
+
+int stock_transpose(const void* in, void* out, int64_t batch, int64_t channels, int64_t spatial,
+                    int to_channels_first, int dtype) {
+    return guard([&] { transpose_impl(in, out, batch, channels, spatial, to_channels_first != 0, dtype); });
+}
+
+int stock_vae_forward(const bh_vae_config* cfg, const bh_vae_weights* w, const uint16_t* latent,
+                      int64_t latent_hw, uint16_t* image, int threads, int stop_after) {
+    return guard([&] {
+        vae_forward(*cfg, vae_table(*w), latent, latent_hw, image, resolve_threads(threads), stop_after);
     });
 }
 
