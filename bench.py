@@ -79,6 +79,9 @@ def parse() -> argparse.Namespace:
     p.add_argument("--denoise", type=int, default=0, metavar="STEPS",
                    help="time the whole on-device denoise loop (STEPS sampler steps, CFG 4.5) "
                         "eagerly and as one HIP graph, one JSON line")
+    p.add_argument("--vae", action="store_true",
+                   help="time the vae-decode stage (SDXL VAE widths, batch 1) at --resolution; "
+                        "one JSON line")
     p.add_argument("--kernels", action="store_true",
                    help="time the isolated kernels at 1024px shapes (GEMMs, self- and "
                         "cross-attention, LayerNorm+modulate); one JSON line per kernel")
@@ -272,6 +275,100 @@ def denoise(args) -> int:
     return 0
 
 
+def vae(args) -> int:
+    """The vae-decode stage (VaeDecoder::forward, vae_decoder.cpp:127-180) at the resolution's
+    latent (resolution / 8), batch 1, SDXL VAE widths, seeded synthetic weights, through the
+    library's decoder engine. K decodes timed between HIP events on one stream after W warm-up
+    decodes; one more decode runs with the launch profiler for the per-class breakdown. The
+    roofline is the implicit-GEMM convolution and projection class (MFMA), as that class's
+    algorithmic FLOP over its summed launch time. The CPU baseline is the stock oracle's decoder
+    on a 128px sample (latent 16) on this host, scaled to the resolution by the FLOP ratio."""
+    import numpy as np
+    import torch
+
+    import burnisher_amd as bh
+    from burnisher_amd.vae import SDXL_VAE, config_struct, make_vae_workload, vae_decode_flops
+
+    bh.check(bh.lib().bh_init(0), "bh_init")
+    hw = args.resolution // 8
+    wl = make_vae_workload(SDXL_VAE, latent_hw=hw)
+    tensors, latent = wl.to_device()
+    cfg = config_struct(wl.cfg)
+    w, keep = wl.table(tensors)
+    h = ctypes.c_void_p()
+    bh.call("bh_vae_create", ctypes.byref(cfg), ctypes.byref(w), hw, ctypes.byref(h))
+    image = torch.zeros((1, 3, wl.image_hw, wl.image_hw), dtype=torch.bfloat16, device="cuda")
+    stream = torch.cuda.Stream()
+    sp = stream.cuda_stream
+    steps = max(1, min(args.steps, 10))
+    for _ in range(max(1, args.warmup)):
+        bh.call("bh_vae_decode", h, latent.data_ptr(), image.data_ptr(), sp)
+    torch.cuda.synchronize()
+    with torch.cuda.stream(stream):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        for _ in range(steps):
+            bh.call("bh_vae_decode", h, latent.data_ptr(), image.data_ptr(), sp)
+        b.record(stream)
+    torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / steps
+    img = image.float()
+    assert torch.isfinite(img).all() and img.std() > 1e-3, "degenerate decoded image"
+    # one profiled decode for the breakdown
+    bh.check(bh.lib().bh_profile_enable((1 << bh.K_GEMM_QKV + 1) - 1), "bh_profile_enable")
+    bh.call("bh_vae_decode", h, latent.data_ptr(), image.data_ptr(), sp)
+    torch.cuda.synchronize()
+    breakdown = {}
+    for cls, name in enumerate(bh.KERNEL_CLASSES[:6]):
+        tot, n, work = ctypes.c_double(), ctypes.c_int64(), ctypes.c_double()
+        bh.check(bh.lib().bh_profile_read(cls, ctypes.byref(tot), ctypes.byref(n), ctypes.byref(work)))
+        if n.value:
+            breakdown[name] = {"ms": round(tot.value, 4), "launches": n.value, "work": work.value}
+    bh.lib().bh_profile_enable(0)
+    bh.lib().bh_vae_destroy(h)
+    flops = vae_decode_flops(wl.cfg, hw)
+    g = breakdown.get("gemm", {"ms": 0.0, "work": 0.0})
+    conv_tflops = g["work"] / (g["ms"] * 1e-3) / 1e12 if g["ms"] else 0.0
+    tflops = flops["total"] / (ms * 1e-3) / 1e12
+    line = {
+        "metric": f"vae-decode ms @{args.resolution}px bf16 (1 GPU)",
+        "value": round(ms, 4), "unit": "ms", "n_gpus": 1, "steps": steps, "warmup": args.warmup,
+        "ms_per_step": round(ms, 4), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: seeded weights (convs N(0, 1/fan_in), GroupNorm affine near identity), "
+                "N(0,1) latent",
+        "config": {"workload": f"SDXL VAE decoder {args.resolution}px, batch 1",
+                   "latent": [1, 4, hw, hw], "image": [1, 3, wl.image_hw, wl.image_hw],
+                   "block_out_channels": list(wl.cfg["block_out_channels"])},
+        "roofline": {"bound": "mfma", "kernel": "conv3x3 implicit GEMM + projections (class)",
+                     "achieved": round(conv_tflops, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(conv_tflops / PEAK_BF16_TFLOPS, 4), "traffic": None},
+        "step": {"flop": flops["total"], "tflops": round(tflops, 2),
+                 "mfma_frac": round(tflops / PEAK_BF16_TFLOPS, 4),
+                 "ceiling_ms": round(flops["total"] / (PEAK_BF16_TFLOPS * 1e12) * 1e3, 3)},
+        "kernels": breakdown,
+    }
+    if not args.no_cpu:
+        import oracle
+        threads = args.cpu_threads or min(16, os.cpu_count() or 1)
+        sample = make_vae_workload(SDXL_VAE, latent_hw=16)
+        scfg = config_struct(sample.cfg)
+        sw, skeep = sample.table()
+        out = np.zeros((1, 3, sample.image_hw, sample.image_hw), np.uint16)
+        log(f"cpu baseline: stock decoder at 128px on {threads} threads")
+        t0 = time.perf_counter()
+        oracle.call(oracle.stock(), "stock_vae_forward", ctypes.byref(scfg), ctypes.byref(sw),
+                    sample.latent.ctypes.data, 16, out.ctypes.data, threads, -1)
+        secs = time.perf_counter() - t0
+        ratio = flops["total"] / vae_decode_flops(sample.cfg, 16)["total"]
+        line["cpu_baseline"] = {"value": round(secs * ratio * 1e3, 1), "unit": "ms", "cores": threads,
+                                "kind": "port",
+                                "sample": f"stock oracle decoder at 128px (latent 16), {secs:.2f} s, "
+                                          f"scaled x{ratio:.1f} by algorithmic FLOP to {args.resolution}px"}
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 def cpu_baseline(wl, threads: int) -> dict:
     """The stock oracle's whole dit-step (all 28 blocks) on this host, timed once."""
     import numpy as np
@@ -301,6 +398,8 @@ def main() -> int:
         return kernels(max(args.steps, 10))
     if args.denoise:
         return denoise(args)
+    if args.vae:
+        return vae(args)
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
               "(the dit-step would shard on the CFG batch, see DESIGN.md)", file=sys.stderr)

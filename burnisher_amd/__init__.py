@@ -154,6 +154,13 @@ SIGNATURES = {
     "bh_dit_weights_view": ([_V], ctypes.POINTER(DitWeights)),
     "bh_dit_weights_bytes": ([_V], _I64),
     "bh_dit_weights_free": ([_V], None),
+    "bh_vae_create": ([_V, _V, _I64, ctypes.POINTER(_V)], _I),
+    "bh_vae_decode": ([_V, _V, _V, _V], _I),
+    "bh_vae_workspace_bytes": ([_V], _I64),
+    "bh_vae_destroy": ([_V], None),
+    "bh_conv2d": ([_V, _V, _V, _V, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I, _V], _I),
+    "bh_upsample": ([_V, _V, _I64, _I64, _I64, _I64, _I64, _I, _V], _I),
+    "bh_transpose": ([_V, _V, _I64, _I64, _I64, _I, _I, _V], _I),
 }
 
 

@@ -426,6 +426,18 @@ void launch_attention_bf16(const bf16_t* q, const bf16_t* k, const bf16_t* v, bf
                            const AttnShape& sh, const void* key_mask, bool mask_f32,
                            hipStream_t s) {
     if (sh.batch * sh.heads * sh.q_len == 0) return;
+    // head_dim 512, one head, self-attention, unmasked (the VAE mid-block): its own kernel.
+    if (sh.head_dim == 512 && sh.heads == 1 && sh.q_len == sh.kv_len && !key_mask &&
+        sh.ld_q == 512 && sh.ld_kv == 512 && sh.ld_o == 512 && aligned16(q) && aligned16(k) &&
+        aligned16(v) && aligned16(out)) {
+        const int64_t ld = vt512_ld(sh.kv_len);
+        bf16_t* vt = vt_workspace(static_cast<size_t>(512 * ld));
+        for (int64_t b = 0; b < sh.batch; ++b) {
+            const int64_t off = b * sh.q_len * 512;
+            launch_attention512(q + off, k + off, v + off, vt, out + off, sh.q_len, sh.scale, s);
+        }
+        return;
+    }
     // head_dim 72 (the DiT): V transposed once, then the flash kernel built for that width.
     const bool fast72 = sh.head_dim == 72 && sh.kv_len <= 16384 && sh.ld_q % 8 == 0 &&
                         sh.ld_kv % 8 == 0 && sh.ld_o % 4 == 0 && aligned16(q) && aligned16(k) &&

@@ -269,7 +269,9 @@ int attention_impl(const void* q, int64_t ld_q, const void* k, const void* v, in
         AttnShape sh{batch, heads, q_len, kv_len, head_dim, ld_q, ld_kv, ld_o,
                      // 0 means 1/sqrt(head_dim), computed exactly as the oracle does.
                      scale > 0.0f ? scale : 1.0f / std::sqrt(static_cast<float>(head_dim))};
-        if (f32 || bias || head_dim > 128) {
+        const bool flash512 = head_dim == 512 && heads == 1 && q_len == kv_len && !key_mask &&
+                              ld_q == 512 && ld_kv == 512 && ld_o == 512;
+        if (f32 || bias || (head_dim > 128 && !flash512)) {
             ProfileScope ps(q_len == kv_len ? K_ATTN_SELF : K_ATTN_CROSS, as_stream(stream),
                             4.0 * batch * heads * static_cast<double>(q_len) * kv_len * head_dim);
             launch_attention_generic(q, k, v, out, sh, bias, key_mask, mask_f32, f32,
@@ -309,10 +311,21 @@ int bh_norm(const void* x, const void* weight, const void* bias, void* out, int6
             void* stream) {
     return guarded([&] {
         const char* op = "norm (hip-gfx950)";
-        (void)channels;
-        require(groups <= 0, "norm (hip-gfx950): GroupNorm is a VAE op and has no kernel here");
         require_nonneg(rows, op, "rows");
         require(cols > 0 || rows == 0, "norm: cols must be positive");
+        if (groups > 0) {   // GroupNorm (the VAE's), NCHW rows of channels * spatial
+            require(!rms, "norm: GroupNorm has no RMS form");
+            require(!is_f32(dtype), "norm (hip-gfx950): GroupNorm is bf16 only");
+            if (rows == 0) return;
+            require_device_ptr(x, op, "x");
+            require_device_ptr(out, op, "out");
+            optional_device_ptr(weight, op, "weight");
+            optional_device_ptr(bias, op, "bias");
+            launch_group_norm_nchw(static_cast<const bf16_t*>(x), static_cast<const bf16_t*>(weight),
+                                   static_cast<const bf16_t*>(bias), static_cast<bf16_t*>(out), rows,
+                                   cols, eps, groups, channels, as_stream(stream));
+            return;
+        }
         if (rows == 0) return;
         require_device_ptr(x, op, "x");
         require_device_ptr(out, op, "out");

@@ -184,6 +184,67 @@ struct GemmEpilogue {
     int vt_heads = 0, vt_dim = 72;
 };
 
+// A 3x3, stride-1, pad-1 convolution read as a GEMM (batch 1, NHWC): out[H*W, c_out] =
+// im2col(in)[H*W, 9*c_in] . W[c_out, 9*c_in]^T with W repacked [c_out][ky][kx][c_in]. With `up`
+// the input is in_h x in_w = H/2 x W/2 and upsampled 2x (nearest) on the fly. `zero` points at
+// 64 zero bf16, the source of the padding taps.
+struct ConvGeom {
+    const bf16_t* in = nullptr;
+    const bf16_t* zero = nullptr;
+    int H = 0, W = 0;
+    int in_h = 0, in_w = 0;
+    int c_in = 0;
+    int up = 0;
+};
+void launch_conv3x3_bf16(const ConvGeom& cv, const bf16_t* wr, const bf16_t* bias, bf16_t* out,
+                         int64_t c_out, const GemmEpilogue& ep, hipStream_t s);
+
+// ---- the VAE decoder's kernels (vae.hip) ----
+// [batch][R][C] -> [batch][C][R], bf16.
+void launch_transpose_bf16(const bf16_t* in, bf16_t* out, int64_t batch, int64_t R, int64_t C,
+                           hipStream_t s);
+// Device scratch of a channels-last GroupNorm: per-chunk fp64 partials and the group statistics.
+struct GroupNormScratch {
+    double* part = nullptr;   // max_chunks * 64
+    double* mean = nullptr;   // 64
+    float* inv = nullptr;     // 64
+    int64_t max_chunks = 0;
+};
+bool gn_nhwc_supported(int64_t C, int64_t G);
+// GroupNorm over x [S, C] (channels-last, batch 1), G groups of C/G channels, then optionally
+// SiLU; each rounded to bf16 as the reference stores them. out may alias x.
+void launch_group_norm_nhwc(const bf16_t* x, bf16_t* out, int64_t S, int64_t C, int64_t G,
+                            float eps, const bf16_t* w, const bf16_t* b, bool silu,
+                            GroupNormScratch& sc, hipStream_t s);
+// Stride-1 "same" convolution, channels-last, w in the checkpoint layout [co][ci][k][k], in the
+// reference's summation order (bit-identical with it).
+void launch_conv_direct_nhwc(const bf16_t* x, const bf16_t* w, const bf16_t* bias, bf16_t* out,
+                             int64_t H, int64_t W, int64_t ci, int64_t co, int64_t k, int64_t pad,
+                             hipStream_t s);
+void launch_upsample_nchw(const bf16_t* in, bf16_t* out, int64_t planes, int64_t H, int64_t W,
+                          int64_t f, hipStream_t s);
+void launch_repack3x3(const bf16_t* w, bf16_t* out, int64_t co, int64_t ci, hipStream_t s);
+// The same, zero-padded to cop output and cip input channels.
+void launch_repack3x3_pad(const bf16_t* w, bf16_t* out, int64_t co, int64_t ci, int64_t cop,
+                          int64_t cip, hipStream_t s);
+// [R][C] -> [keep][R] (the first `keep` columns only), batch 1.
+void launch_transpose_keep_bf16(const bf16_t* in, bf16_t* out, int64_t R, int64_t C, int64_t keep,
+                                hipStream_t s);
+// Rows [S][C] -> [S][Cp], columns C..Cp-1 zero.
+void launch_pad_rows(const bf16_t* in, bf16_t* out, int64_t S, int64_t C, int64_t Cp, hipStream_t s);
+// The op-level (NCHW) convolution and GroupNorm; they use per-device scratch grown on demand.
+void launch_conv2d_nchw(const bf16_t* x, const bf16_t* w, const bf16_t* bias, bf16_t* out,
+                        int64_t batch, int64_t ci, int64_t h, int64_t wd, int64_t co, int64_t k,
+                        int64_t pad, hipStream_t s);
+void launch_group_norm_nchw(const bf16_t* x, const bf16_t* w, const bf16_t* b, bf16_t* out,
+                            int64_t rows, int64_t cols, float eps, int64_t groups, int64_t channels,
+                            hipStream_t s);
+// Keys per V^T row for the head_dim-512 attention (S rounded up to 32).
+int64_t vt512_ld(int64_t S);
+// Single-head attention at head_dim 512: q, k, v, out [S, 512]; vt is scratch of 512 x vt512_ld(S).
+void launch_attention512(const bf16_t* q, const bf16_t* k, const bf16_t* v, bf16_t* vt, bf16_t* out,
+                         int64_t S, float scale, hipStream_t s);
+
 // bf16 out[m, n] = A[m, k] . B[n, k]^T (+bias) with `ep`. Picks the MFMA tile kernel, the
 // small-M kernel or the reference-order kernel by shape.
 void launch_gemm_bf16(const bf16_t* a, const bf16_t* b, const bf16_t* bias, bf16_t* out,

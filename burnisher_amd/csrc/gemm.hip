@@ -205,6 +205,7 @@ struct Operands {
     const bf16_t* A;
     const bf16_t* B;
     int64_t M, N, K;
+    ConvGeom cv;   // cv.in != null: A is the implicit im2col of a 3x3 convolution (see below)
 };
 
 // This lane's source address (at k = 0) for each of the wave's 13 DMA items of a tile: items
@@ -238,6 +239,42 @@ __device__ __forceinline__ void dma_tile(char* stage, const bf16_t* const (&src)
     for (int r = 0; r < kDmaItems; ++r) {
         const int rb = r < BM / 32 ? r * 4 + wave : min((r - BM / 32) * 4 + wave, BN / 8);
         dma16(src[r] + k0, stage + (r < BM / 32 ? 0 : kABytes) + rb * 1024);
+    }
+}
+
+// The implicit-convolution k-tile `kt` into one stage. k-tile kt covers tap t = kt / (c_in/64)
+// (ky = t / 3, kx = t % 3) and input channels 64 (kt % (c_in/64)) .. +63, so an A row of the tile
+// is 128 contiguous bytes of one input pixel: the output pixel's neighbour (y + ky - 1,
+// x + kx - 1), halved when the input is upsampled 2x on the fly, or the zero row for a tap in the
+// padding. B rows (the weights, repacked [c_out][ky][kx][c_in]) stream as in the plain GEMM.
+__device__ __forceinline__ void dma_tile_conv(char* stage, const bf16_t* const (&src)[kDmaItems],
+                                              const Operands& o, const int (&py)[BM / 32],
+                                              const int (&px)[BM / 32], int kt, int wave, int lane) {
+    const ConvGeom& c = o.cv;
+    const int cb_count = c.c_in >> 6;
+    const int tap = kt / cb_count, cb = kt - tap * cb_count;
+    const int ky = tap / 3, kx = tap - 3 * ky;
+    const int slot = lane & 7;
+#pragma unroll
+    for (int r = 0; r < BM / 32; ++r) {
+        const int row_in = (r * 4 + wave) * 8 + (lane >> 3);
+        const int ch = (slot ^ ((row_in >> 1) & 7)) * 8;
+        int sy = py[r] + ky - 1, sx = px[r] + kx - 1;
+        const bool inside = static_cast<unsigned>(sy) < static_cast<unsigned>(c.H) &&
+                            static_cast<unsigned>(sx) < static_cast<unsigned>(c.W);
+        if (c.up) {
+            sy >>= 1;
+            sx >>= 1;
+        }
+        const bf16_t* a = inside ? c.in + (static_cast<int64_t>(sy) * c.in_w + sx) * c.c_in + cb * 64 + ch
+                                 : c.zero + ch;
+        dma16(a, stage + (r * 4 + wave) * 1024);
+    }
+    const int64_t k0 = static_cast<int64_t>(kt) * BK;
+#pragma unroll
+    for (int r = BM / 32; r < kDmaItems; ++r) {
+        const int rb = min((r - BM / 32) * 4 + wave, BN / 8);
+        dma16(src[r] + k0, stage + kABytes + rb * 1024);
     }
 }
 
@@ -316,6 +353,7 @@ __device__ __forceinline__ void wait_and_join() {
 constexpr int kConsumers = 4;
 constexpr int kWgThreads = 2 * kConsumers * 64;   // 512
 
+template <bool CONV>
 __device__ __forceinline__ void produce(char* smem, const Operands& o, int KT, int my_tiles,
                                         int tiles_m, int tiles_n, int group_m, int wave, int lane) {
     const int total = my_tiles * KT;
@@ -332,15 +370,40 @@ __device__ __forceinline__ void produce(char* smem, const Operands& o, int KT, i
             dma_sources(src, o, m0, n0, wave, lane);
         }
     };
-    dma_tile(smem, src, 0, wave);
-    if (total > 1) advance();
-    dma_tile(smem + kStageBytes, src, static_cast<int64_t>(kt) * BK, wave);
+    // Implicit convolution: the output pixel of each A item of this lane, per tile.
+    constexpr bool conv = CONV;
+    int py[BM / 32], px[BM / 32];
+    auto conv_rows = [&]() {
+#pragma unroll
+        for (int r = 0; r < BM / 32; ++r) {
+            const int row_in = (r * 4 + wave) * 8 + (lane >> 3);
+            const int p = static_cast<int>(min(m0 + a_row(row_in), o.M - 1));
+            py[r] = p / o.cv.W;
+            px[r] = p - py[r] * o.cv.W;
+        }
+    };
+    auto issue = [&](char* stage_ptr) {
+        if (conv) dma_tile_conv(stage_ptr, src, o, py, px, kt, wave, lane);
+        else dma_tile(stage_ptr, src, static_cast<int64_t>(kt) * BK, wave);
+    };
+    if (conv) conv_rows();
+    issue(smem);
+    if (total > 1) {
+        const int it0 = it;
+        advance();
+        if (conv && it != it0) conv_rows();
+    }
+    issue(smem + kStageBytes);
     int stage = 0;
     for (int g = 0; g < total; ++g) {
         wait_and_join<kDmaItems>();
-        if (g + 2 < total) advance();
+        if (g + 2 < total) {
+            const int it0 = it;
+            advance();
+            if (conv && it != it0) conv_rows();
+        }
         const int s2 = stage == 0 ? 2 : stage - 1;   // (g + 2) % 3
-        dma_tile(smem + s2 * kStageBytes, src, static_cast<int64_t>(kt) * BK, wave);
+        issue(smem + s2 * kStageBytes);
         stage = stage == 2 ? 0 : stage + 1;
     }
     wait_and_join<0>();   // the trailing copies have landed before the LDS holds the output
@@ -719,10 +782,10 @@ __device__ __forceinline__ void consume(char* smem, const Epi& e, bf16_t* out, i
     }
 }
 
-template <int ACT, int MODE>
+template <int ACT, int MODE, bool CONV>
 __global__ void __launch_bounds__(kWgThreads, 1)
 k_gemm_tn(const bf16_t* __restrict__ A, const bf16_t* __restrict__ B, bf16_t* out, int64_t M,
-          int64_t N, int64_t K, Epi e, int tiles_m, int tiles_n, int group_m) {
+          int64_t N, int64_t K, Epi e, int tiles_m, int tiles_n, int group_m, ConvGeom cv) {
     __shared__ __attribute__((aligned(1024))) char smem[3 * kStageBytes];
     const int T = tiles_m * tiles_n;
     const int my_tiles = (T - static_cast<int>(blockIdx.x) + static_cast<int>(gridDim.x) - 1) /
@@ -733,8 +796,8 @@ k_gemm_tn(const bf16_t* __restrict__ A, const bf16_t* __restrict__ B, bf16_t* ou
     const int lane = threadIdx.x & 63;
     const int KT = static_cast<int>(K / BK);
     if (wave >= kConsumers) {
-        produce(smem, Operands{A, B, M, N, K}, KT, my_tiles, tiles_m, tiles_n, group_m,
-                wave - kConsumers, lane);
+        produce<CONV>(smem, Operands{A, B, M, N, K, cv}, KT, my_tiles, tiles_m, tiles_n, group_m,
+                      wave - kConsumers, lane);
     } else {
         consume<ACT, MODE>(smem, e, out, M, N, KT, my_tiles, tiles_m, tiles_n, group_m, wave, lane);
     }
@@ -923,9 +986,9 @@ bool aligned(const void* p, int bytes) {
     return (reinterpret_cast<uintptr_t>(p) % bytes) == 0;
 }
 
-template <int ACT, int MODE>
+template <int ACT, int MODE, bool CONV = false>
 void launch_tn(const bf16_t* a, const bf16_t* b, bf16_t* out, int64_t m, int64_t n, int64_t k,
-               const Epi& e, hipStream_t s) {
+               const Epi& e, hipStream_t s, const ConvGeom& cv = ConvGeom{}) {
     const int tiles_m = static_cast<int>((m + BM - 1) / BM);
     const int tiles_n = static_cast<int>((n + BN - 1) / BN);
     const int tiles = tiles_m * tiles_n;
@@ -933,7 +996,7 @@ void launch_tn(const bf16_t* a, const bf16_t* b, bf16_t* out, int64_t m, int64_t
     // a multiple of 8, so is the grid, which the XCD banding relies on.
     int grid = min(tiles, device_cus() & ~7);
     if (grid < 8) grid = min(tiles, device_cus());
-    k_gemm_tn<ACT, MODE><<<grid, kWgThreads, 0, s>>>(a, b, out, m, n, k, e, tiles_m, tiles_n, 4);
+    k_gemm_tn<ACT, MODE, CONV><<<grid, kWgThreads, 0, s>>>(a, b, out, m, n, k, e, tiles_m, tiles_n, 4, cv);
 }
 
 template <int ACT>
@@ -1026,6 +1089,30 @@ void launch_gemm_bf16(const bf16_t* a, const bf16_t* b, const bf16_t* bias, bf16
         default: launch_tn_mode<0>(mode, a, b, out, m, n, k, e, s); break;
     }
     launch_check("gemm (mfma)");
+}
+
+void launch_conv3x3_bf16(const ConvGeom& cv, const bf16_t* wr, const bf16_t* bias, bf16_t* out,
+                         int64_t c_out, const GemmEpilogue& ep, hipStream_t s) {
+    const int64_t m = static_cast<int64_t>(cv.H) * cv.W, k = 9 * static_cast<int64_t>(cv.c_in);
+    if (m == 0 || c_out == 0) return;
+    require(cv.in && cv.zero && wr && out, "conv3x3: null operand");
+    require(cv.c_in % 64 == 0 && cv.c_in > 0, "conv3x3 (mfma): c_in must be a positive multiple of 64");
+    require(c_out % 8 == 0, "conv3x3 (mfma): c_out must be a multiple of 8");
+    require(cv.up ? (cv.in_h * 2 == cv.H && cv.in_w * 2 == cv.W) : (cv.in_h == cv.H && cv.in_w == cv.W),
+            "conv3x3: input and output sizes disagree");
+    require(!ep.vt && !ep.row_add && !ep.gate, "conv3x3: epilogue must be a plain store or a residual add");
+    require(aligned(cv.in, 16) && aligned(cv.zero, 16) && aligned(wr, 16) && aligned(out, 16) &&
+                (!bias || aligned(bias, 16)) && (!ep.residual || aligned(ep.residual, 16)),
+            "conv3x3: operands must be 16-byte aligned");
+    require(static_cast<int64_t>(cv.in_h) * cv.in_w * cv.c_in < (int64_t{1} << 31),
+            "conv3x3: input too large for 32-bit pixel offsets");
+    Epi e{bias, ep.act, ep.round_mid, nullptr, 1, ep.residual, nullptr, 1,
+          ep.ld_out > 0 ? ep.ld_out : c_out, nullptr, 0, 0, 0, 0, 0, 72};
+    require(ep.act == 0, "conv3x3: no activation epilogue (the decoder's SiLU follows a GroupNorm)");
+    ProfileScope ps(K_GEMM, s, 2.0 * static_cast<double>(m) * c_out * k);
+    if (ep.residual) launch_tn<0, EPI_RESIDUAL, true>(cv.in, wr, out, m, c_out, k, e, s, cv);
+    else launch_tn<0, EPI_STORE, true>(cv.in, wr, out, m, c_out, k, e, s, cv);
+    launch_check("conv3x3 (mfma)");
 }
 
 }  // namespace bh

@@ -95,8 +95,10 @@ int bh_attention_strided(const void* q, int64_t ld_q, const void* k, const void*
                          int mask_dtype, int dtype, void* stream);
 
 /* NormArgs (ops.h:81-94): LayerNorm (rms=0) or RMSNorm (rms=1) over the last dimension with
- * optional weight/bias; fp64 statistics like the reference oracle. GroupNorm (groups>0) is a
- * VAE op and is rejected. Replaces `k_layernorm` (src/cuda/ops_cuda.cu:227-272). */
+ * optional weight/bias; fp64 statistics like the reference oracle. Replaces `k_layernorm`
+ * (src/cuda/ops_cuda.cu:227-272). groups > 0 is GroupNorm (ops_cpu.cpp:186-224) over NCHW rows
+ * of `channels` x spatial (channels 0: cols), bf16, channels % 8 == 0 with channels/8 dividing
+ * 256; it uses per-device scratch grown on demand. Replaces `groupnorm_chunked` (ops_cuda.cu:275-371). */
 int bh_norm(const void* x, const void* weight, const void* bias, void* out, int64_t rows,
             int64_t cols, float eps, int rms, int64_t groups, int64_t channels, int dtype,
             void* stream);
@@ -125,6 +127,22 @@ int bh_chunk(const void* modulation, const void* table, void* out, int64_t batch
  * [B,G*G,P*P*C] in (ky,kx,c) order -> [B,C,G*P,G*P]. */
 int bh_patch(const void* in, void* out, int64_t batch, int64_t channels, int64_t grid,
              int64_t patch, int inverse, int dtype, void* stream);
+
+/* Conv2dArgs (ops.h:120-126): NCHW bf16, stride 1, "same" padding (2*pad == k-1), weight
+ * [c_out, c_in, k, k]. 3x3 with c_in % 64 == 0 runs as an implicit GEMM on the MFMA tile kernel,
+ * 1x1 as a GEMM, other kernels in the reference's summation order. Uses per-device scratch grown
+ * on demand. Replaces `conv2d_cuda` (src/cuda/ops_cuda.cu:897-1015, cuDNN). */
+int bh_conv2d(const void* x, const void* weight, const void* bias, void* out, int64_t batch,
+              int64_t c_in, int64_t h, int64_t w, int64_t c_out, int64_t k, int64_t pad, int dtype,
+              void* stream);
+/* UpsampleArgs (ops.h:178-182): nearest, integer factor, NCHW bf16. Replaces `upsample_cuda`
+ * (ops_cuda.cu:1132-1157). */
+int bh_upsample(const void* in, void* out, int64_t batch, int64_t channels, int64_t h, int64_t w,
+                int64_t factor, int dtype, void* stream);
+/* TransposeArgs (ops.h:184-191): [batch, channels, spatial] <-> [batch, spatial, channels],
+ * bf16. Replaces `transpose_cuda` (ops_cuda.cu:1159-1170). */
+int bh_transpose(const void* in, void* out, int64_t batch, int64_t channels, int64_t spatial,
+                 int to_channels_first, int dtype, void* stream);
 
 /* ---- fused ops (no single reference op; each equals a fixed reference op sequence) -------- */
 
@@ -363,6 +381,21 @@ typedef struct bh_vae_weights {
     const char* const* names;
     const void* const* tensors;
 } bh_vae_weights;
+
+typedef struct bh_vae bh_vae;
+
+/* Prepares VaeDecoder::forward (vae_decoder.cpp:127-180) for one latent side (batch 1): checks the
+ * configuration, repacks the 3x3 convolution weights for the implicit-GEMM kernel and allocates
+ * every activation once (4 buffers of the largest layer, the attention's Q/K/V/O). The weight
+ * pointers must stay valid for the engine's lifetime. This call allocates; decode does not. */
+int bh_vae_create(const bh_vae_config* cfg, const bh_vae_weights* w, int64_t latent_hw, bh_vae** out);
+/* latent [1, latent_channels, h, h] -> image [1, 3, h*f, h*f] (f = 2^(num_blocks-1)), bf16 NCHW
+ * device pointers, on `stream`. No host synchronisation. The latent is NOT divided by the
+ * scaling factor here, as in the reference (the pipeline does that, burnisher_main.cpp:661-663). */
+int bh_vae_decode(bh_vae* e, const void* latent, void* image, void* stream);
+/* Device bytes the engine holds. */
+int64_t bh_vae_workspace_bytes(const bh_vae* e);
+void bh_vae_destroy(bh_vae* e);
 
 /* ---- checkpoints: safetensors shards and the DiT's device weights -------------------------- */
 

@@ -43,8 +43,12 @@ def test_arguments_refused_before_any_device_work():
     assert b"null" in lib.bh_last_error()
     assert lib.bh_gemm(None, None, None, None, -1, 4, 4, 1, 0, 1, None) != 0
     assert b"negative" in lib.bh_last_error()
-    assert lib.bh_norm(None, None, None, None, 4, 4, 1e-6, 0, 8, 4, 1, None) != 0
-    assert b"GroupNorm" in lib.bh_last_error()
+    assert lib.bh_norm(None, None, None, None, 4, 4, 1e-6, 1, 8, 4, 1, None) != 0
+    assert b"GroupNorm has no RMS form" in lib.bh_last_error()
+    assert lib.bh_conv2d(None, None, None, None, 1, 4, 8, 8, 4, 3, 0, 1, None) != 0
+    assert b"same" in lib.bh_last_error()
+    assert lib.bh_conv2d(None, None, None, None, 1, 4, 8, 8, 4, 3, 1, 0, None) != 0
+    assert b"bf16 only" in lib.bh_last_error()
     assert lib.bh_chunk(None, None, None, 2, 4, 6, 9, -1, 1, None) != 0
     assert b"chunk" in lib.bh_last_error()
     # an empty op is a no-op, not an error
