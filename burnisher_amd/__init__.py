@@ -159,6 +159,10 @@ SIGNATURES = {
     "bh_vae_workspace_bytes": ([_V], _I64),
     "bh_vae_destroy": ([_V], None),
     "bh_conv2d": ([_V, _V, _V, _V, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I, _V], _I),
+    "bh_vae_weights_load": ([_V, _V, _V, ctypes.POINTER(_V)], _I),
+    "bh_vae_weights_view": ([_V], _V),
+    "bh_vae_weights_bytes": ([_V], _I64),
+    "bh_vae_weights_free": ([_V], None),
     "bh_upsample": ([_V, _V, _I64, _I64, _I64, _I64, _I64, _I, _V], _I),
     "bh_transpose": ([_V, _V, _I64, _I64, _I64, _I, _I, _V], _I),
 }
@@ -311,6 +315,30 @@ class DitDeviceWeights:
             lib().bh_dit_weights_free(self._h)
             self._h = None
             self.weights = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class VaeDeviceWeights:
+    """The VAE decoder's weights from a checkpoint's `vae/` component, bf16 in one device arena
+    (bh_vae_weights_load). `table` is the address of the bh_vae_weights bh_vae_create takes."""
+
+    def __init__(self, checkpoint: Checkpoint, cfg, stream=None):
+        h = ctypes.c_void_p()
+        call("bh_vae_weights_load", checkpoint.handle, ctypes.byref(cfg), stream, ctypes.byref(h))
+        self._h = h
+        self.table = lib().bh_vae_weights_view(h)
+        self.bytes = lib().bh_vae_weights_bytes(h)
+
+    def free(self) -> None:
+        if self._h is not None:
+            lib().bh_vae_weights_free(self._h)
+            self._h = None
+            self.table = None
 
     def __del__(self):
         try:

@@ -484,6 +484,18 @@ struct bh_dit_device_weights {
     }
 };
 
+struct bh_vae_device_weights {
+    void* arena = nullptr;
+    int64_t bytes = 0;
+    std::vector<std::string> names;
+    std::vector<const char*> cnames;
+    std::vector<const void*> ptrs;
+    bh_vae_weights view{};
+    ~bh_vae_device_weights() {
+        if (arena) (void)hipFree(arena);
+    }
+};
+
 namespace bh {
 namespace {
 
@@ -575,6 +587,57 @@ struct PinnedStage {
 };
 
 }  // namespace
+
+// Checks every wanted tensor (present, shape, F32 or BF16) before allocating anything, then
+// converts each to bf16 on the host into page-locked staging and copies it into one device arena
+// on `st`, setting *want[i].slot to its address. Returns the arena's size; *arena owns it.
+int64_t upload_arena(const Checkpoint& ck, const std::vector<Want>& want, hipStream_t st, void** arena) {
+    struct Src { const Shard* shard; const Entry* entry; int64_t offset; };
+    std::vector<Src> src;
+    int64_t total = 0;
+    for (const Want& t : want) {
+        const Entry* e = nullptr;
+        const Shard* s = ck.require(t.name, &e);
+        if (!shape_ok(t.name, e->shape, t.shape)) {
+            throw Error("weights: '" + t.name + "' is " + shape_str(e->shape) +
+                        " in the checkpoint, but this configuration needs " + shape_str(t.shape));
+        }
+        if (e->dtype != ST_F32 && e->dtype != ST_BF16) {
+            throw Error(std::string("weights: '") + t.name + "' is " + st_dtype_name(e->dtype) +
+                        ", which has no per-element conversion to bf16 here (as in the reference "
+                        "runtime); convert the checkpoint to F32 or BF16 deliberately");
+        }
+        src.push_back({s, e, total});
+        total += (e->numel() * 2 + kAlign - 1) / kAlign * kAlign;
+    }
+    hip_check(hipMalloc(arena, static_cast<size_t>(std::max<int64_t>(total, kAlign))), "hipMalloc (weights)");
+    PinnedStage stage;
+    const int64_t half = kStageBytes / 2;
+    int buf = 0;
+    bool used[2] = {false, false};
+    for (size_t k = 0; k < want.size(); ++k) {
+        char* dev = static_cast<char*>(*arena) + src[k].offset;
+        *want[k].slot = dev;
+        const Entry& e = *src[k].entry;
+        const char* host = src[k].shard->data(e);
+        const int64_t n = e.numel();
+        const int64_t per = half / 2;   // bf16 elements per staging half
+        for (int64_t b = 0; b < n; b += per) {
+            const int64_t m = std::min(per, n - b);
+            if (used[buf]) hip_check(hipEventSynchronize(stage.done[buf]), "hipEventSynchronize");
+            char* h = stage.p + buf * half;
+            convert(host + b * st_dtype_bytes(e.dtype), e.dtype, h, BH_BF16, m, e.name);
+            hip_check(hipMemcpyAsync(dev + 2 * b, h, static_cast<size_t>(m) * 2, hipMemcpyHostToDevice, st),
+                      "hipMemcpyAsync (weights)");
+            hip_check(hipEventRecord(stage.done[buf], st), "hipEventRecord");
+            used[buf] = true;
+            buf ^= 1;
+        }
+    }
+    hip_check(hipStreamSynchronize(st), "hipStreamSynchronize (weights)");
+    return total;
+}
+
 }  // namespace bh
 
 extern "C" {
@@ -702,62 +765,44 @@ int bh_dit_weights_load(const bh_checkpoint* ck, const bh_dit_config* cfg, void*
         auto w = std::make_unique<bh_dit_device_weights>();
         w->blocks.resize(static_cast<size_t>(cfg->num_layers));
         const std::vector<bh::Want> want = bh::dit_tensors(*cfg, *w);
-
-        // Check every tensor (present, shape, dtype) before allocating anything.
-        struct Src { const bh::Shard* shard; const bh::Entry* entry; int64_t offset; };
-        std::vector<Src> src;
-        int64_t total = 0;
-        for (const bh::Want& t : want) {
-            const bh::Entry* e = nullptr;
-            const bh::Shard* s = ck->require(t.name, &e);
-            if (!bh::shape_ok(t.name, e->shape, t.shape)) {
-                throw bh::Error("weights: '" + t.name + "' is " + bh::shape_str(e->shape) +
-                                " in the checkpoint, but this configuration needs " +
-                                bh::shape_str(t.shape));
-            }
-            if (e->dtype != bh::ST_F32 && e->dtype != bh::ST_BF16) {
-                throw bh::Error(std::string("weights: '") + t.name + "' is " +
-                                bh::st_dtype_name(e->dtype) +
-                                ", which has no per-element conversion to bf16 here (as in the "
-                                "reference runtime); convert the checkpoint to F32 or BF16 "
-                                "deliberately");
-            }
-            src.push_back({s, e, total});
-            total += (e->numel() * 2 + bh::kAlign - 1) / bh::kAlign * bh::kAlign;
-        }
-
-        hipStream_t st = static_cast<hipStream_t>(stream);
-        bh::hip_check(hipMalloc(&w->arena, static_cast<size_t>(total)), "hipMalloc (DiT weights)");
-        w->bytes = total;
-        bh::PinnedStage stage;
-        const int64_t half = bh::kStageBytes / 2;
-        int buf = 0;
-        bool used[2] = {false, false};
-        for (size_t k = 0; k < want.size(); ++k) {
-            char* dev = static_cast<char*>(w->arena) + src[k].offset;
-            *want[k].slot = dev;
-            const bh::Entry& e = *src[k].entry;
-            const char* host = src[k].shard->data(e);
-            const int64_t n = e.numel();
-            const int64_t per = half / 2;   // bf16 elements per staging half
-            for (int64_t b = 0; b < n; b += per) {
-                const int64_t m = std::min(per, n - b);
-                if (used[buf]) bh::hip_check(hipEventSynchronize(stage.done[buf]), "hipEventSynchronize");
-                char* h = stage.p + buf * half;
-                bh::convert(host + b * bh::st_dtype_bytes(e.dtype), e.dtype, h, BH_BF16, m, e.name);
-                bh::hip_check(hipMemcpyAsync(dev + 2 * b, h, static_cast<size_t>(m) * 2,
-                                             hipMemcpyHostToDevice, st),
-                              "hipMemcpyAsync (weights)");
-                bh::hip_check(hipEventRecord(stage.done[buf], st), "hipEventRecord");
-                used[buf] = true;
-                buf ^= 1;
-            }
-        }
-        bh::hip_check(hipStreamSynchronize(st), "hipStreamSynchronize (weights)");
+        w->bytes = bh::upload_arena(*ck, want, static_cast<hipStream_t>(stream), &w->arena);
         w->view.blocks = w->blocks.data();
         *out = w.release();
     });
 }
+
+int bh_vae_weights_load(const bh_checkpoint* ck, const bh_vae_config* cfg, void* stream,
+                        bh_vae_device_weights** out) {
+    return bh::guarded([&] {
+        bh::require(out != nullptr, "vae_weights_load: null output handle");
+        *out = nullptr;
+        bh::require(ck != nullptr && cfg != nullptr, "vae_weights_load: null checkpoint or config");
+        bh::require(cfg->num_blocks >= 1 && cfg->num_blocks <= 8 && cfg->layers_per_block >= 0 &&
+                        cfg->latent_channels > 0,
+                    "vae_weights_load: configuration out of range");
+        auto w = std::make_unique<bh_vae_device_weights>();
+        const auto table = bh::vae_tensor_shapes(*cfg);
+        w->names.reserve(table.size());
+        w->ptrs.assign(table.size(), nullptr);
+        std::vector<bh::Want> want;
+        for (size_t i = 0; i < table.size(); ++i) {
+            w->names.push_back(table[i].first);
+            want.push_back({table[i].first, table[i].second, &w->ptrs[i]});
+        }
+        w->bytes = bh::upload_arena(*ck, want, static_cast<hipStream_t>(stream), &w->arena);
+        for (const auto& n : w->names) w->cnames.push_back(n.c_str());
+        w->view.count = static_cast<int>(w->names.size());
+        w->view.names = w->cnames.data();
+        w->view.tensors = w->ptrs.data();
+        *out = w.release();
+    });
+}
+
+const bh_vae_weights* bh_vae_weights_view(const bh_vae_device_weights* w) { return w ? &w->view : nullptr; }
+
+int64_t bh_vae_weights_bytes(const bh_vae_device_weights* w) { return w ? w->bytes : -1; }
+
+void bh_vae_weights_free(bh_vae_device_weights* w) { delete w; }
 
 const bh_dit_weights* bh_dit_weights_view(const bh_dit_device_weights* w) {
     return w ? &w->view : nullptr;

@@ -12,6 +12,8 @@
 #include <cstdint>
 #include <stdexcept>
 #include <string>
+#include <utility>
+#include <vector>
 
 #include "../../include/burnisher_hip.h"
 
@@ -239,6 +241,8 @@ void launch_conv2d_nchw(const bf16_t* x, const bf16_t* w, const bf16_t* bias, bf
 void launch_group_norm_nchw(const bf16_t* x, const bf16_t* w, const bf16_t* b, bf16_t* out,
                             int64_t rows, int64_t cols, float eps, int64_t groups, int64_t channels,
                             hipStream_t s);
+// The VAE decoder's tensors with their checkpoint shapes (vae_engine.cpp).
+std::vector<std::pair<std::string, std::vector<int64_t>>> vae_tensor_shapes(const bh_vae_config& c);
 // Keys per V^T row for the head_dim-512 attention (S rounded up to 32).
 int64_t vt512_ld(int64_t S);
 // Single-head attention at head_dim 512: q, k, v, out [S, 512]; vt is scratch of 512 x vt512_ld(S).

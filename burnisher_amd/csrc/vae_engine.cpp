@@ -79,36 +79,54 @@ Plan plan_of(const bh_vae_config& c) {
 
 bool mfma_conv(int64_t ci, int64_t co) { return ci % 64 == 0 && co % 8 == 0; }
 
-// Every tensor name the decoder reads (the VAE part of declare_pixart_shapes, weights.cpp:284-320).
-std::vector<std::string> required_names(const bh_vae_config& c) {
-    std::vector<std::string> out;
+}  // namespace
+
+// Every tensor the decoder reads with its checkpoint shape (the VAE part of declare_pixart_shapes,
+// weights.cpp:284-320): convolutions [out, in, k, k], projections [out, in], norms [channels].
+std::vector<std::pair<std::string, std::vector<int64_t>>> vae_tensor_shapes(const bh_vae_config& c) {
+    std::vector<std::pair<std::string, std::vector<int64_t>>> out;
     const Plan p = plan_of(c);
-    auto two = [&](const std::string& n) {
-        out.push_back(n + ".weight");
-        out.push_back(n + ".bias");
+    auto conv = [&](const std::string& n, int64_t ci, int64_t co, int64_t k) {
+        out.push_back({n + ".weight", {co, ci, k, k}});
+        out.push_back({n + ".bias", {co}});
+    };
+    auto norm = [&](const std::string& n, int64_t ch) {
+        out.push_back({n + ".weight", {ch}});
+        out.push_back({n + ".bias", {ch}});
     };
     auto res = [&](const std::string& n, int64_t ci, int64_t co) {
-        for (const char* part : {".norm1", ".conv1", ".norm2", ".conv2"}) two(n + part);
-        if (ci != co) two(n + ".conv_shortcut");
+        norm(n + ".norm1", ci);
+        conv(n + ".conv1", ci, co, 3);
+        norm(n + ".norm2", co);
+        conv(n + ".conv2", co, co, 3);
+        if (ci != co) conv(n + ".conv_shortcut", ci, co, 1);
     };
-    two("post_quant_conv");
-    two("decoder.conv_in");
-    res("decoder.mid_block.resnets.0", p.rev[0], p.rev[0]);
-    res("decoder.mid_block.resnets.1", p.rev[0], p.rev[0]);
-    for (const char* part : {".group_norm", ".to_q", ".to_k", ".to_v", ".to_out.0"})
-        two(std::string("decoder.mid_block.attentions.0") + part);
-    int64_t prev = p.rev[0];
+    const int64_t zc = c.latent_channels, r0 = p.rev[0];
+    conv("post_quant_conv", zc, zc, 1);
+    conv("decoder.conv_in", zc, r0, 3);
+    res("decoder.mid_block.resnets.0", r0, r0);
+    res("decoder.mid_block.resnets.1", r0, r0);
+    norm("decoder.mid_block.attentions.0.group_norm", r0);
+    for (const char* part : {".to_q", ".to_k", ".to_v", ".to_out.0"}) {
+        const std::string n = std::string("decoder.mid_block.attentions.0") + part;
+        out.push_back({n + ".weight", {r0, r0}});
+        out.push_back({n + ".bias", {r0}});
+    }
+    int64_t prev = r0;
     for (size_t i = 0; i < p.rev.size(); ++i) {
         for (int j = 0; j <= c.layers_per_block; ++j)
             res("decoder.up_blocks." + std::to_string(i) + ".resnets." + std::to_string(j),
                 j == 0 ? prev : p.rev[i], p.rev[i]);
         prev = p.rev[i];
-        if (i + 1 != p.rev.size()) two("decoder.up_blocks." + std::to_string(i) + ".upsamplers.0.conv");
+        if (i + 1 != p.rev.size())
+            conv("decoder.up_blocks." + std::to_string(i) + ".upsamplers.0.conv", p.rev[i], p.rev[i], 3);
     }
-    two("decoder.conv_norm_out");
-    two("decoder.conv_out");
+    norm("decoder.conv_norm_out", prev);
+    conv("decoder.conv_out", prev, 3, 3);
     return out;
 }
+
+namespace {
 
 // One decode, everything on stream s.
 struct Run {
@@ -297,7 +315,7 @@ int bh_vae_create(const bh_vae_config* cfg, const bh_vae_weights* w, int64_t lat
             e->w[w->names[i]] = static_cast<const bf16_t*>(w->tensors[i]);
         }
         const bh::Plan p = bh::plan_of(*cfg);
-        for (const std::string& n : bh::required_names(*cfg)) (void)e->at(n);   // all present
+        for (const auto& t : bh::vae_tensor_shapes(*cfg)) (void)e->at(t.first);   // all present
         for (int64_t ch : p.rev) {
             bh::require(ch > 0 && bh::gn_nhwc_supported(ch, cfg->norm_num_groups),
                         "vae_create: every block width must split into the groups in whole 8-channel "

@@ -1,7 +1,12 @@
-"""The `dit-step` stage: one dit-step forward from .npy inputs and a checkpoint directory.
+"""Single stages from .npy inputs and a checkpoint directory: `dit-step` and `vae-decode`.
 
     python -m burnisher_amd.stage dit-step --weights DIR --latent L.npy --caption C.npy \\
         --mask M.npy --out O.npy [--timestep 500] [--layers N] [--warmup 1] [--plan fused]
+    python -m burnisher_amd.stage vae-decode --weights DIR --latent L.npy --out O.npy [--warmup 1]
+
+`vae-decode` mirrors the reference CLI's `decode` command (tools/burnisher_main.cpp:636-690): a
+[1, 4, h, w] float32 latent (h == w here), the `vae/` component of the checkpoint, no division by
+the scaling factor (that is the pipeline's, burnisher_main.cpp:661-663), output [1, 3, 8h, 8w].
 
 Mirrors the reference CLI's `dit-step` command (tools/burnisher_main.cpp:694-747) for the
 `hip-gfx950` implementation: the inputs are little-endian C-order float32 .npy files
@@ -23,8 +28,8 @@ import time
 
 import numpy as np
 
-from . import (BF16, DIT_FUSED, DIT_OPWISE, BurnisherError, Checkpoint, DitDeviceWeights, call,
-               lib)
+from . import (BF16, DIT_FUSED, DIT_OPWISE, BurnisherError, Checkpoint, DitDeviceWeights,
+               VaeDeviceWeights, call, lib)
 from .workload import PIXART_SIGMA, config_struct
 
 
@@ -138,6 +143,54 @@ def dit_step(weights: str, latent_path: str, caption_path: str, mask_path: str, 
             "output_stats": output_stats(host)}
 
 
+def vae_decode(weights: str, latent_path: str, out_path: str, warmup: int = 1) -> dict:
+    """Runs the vae-decode stage; returns the BURNISH_JSON record."""
+    import torch
+
+    from .vae import SDXL_VAE, config_struct as vae_config_struct, scale_factor
+
+    cfg = vae_config_struct(SDXL_VAE)
+    latent = read_npy_f32(latent_path)
+    if latent.ndim != 4 or latent.shape[1] != cfg.latent_channels:
+        raise BurnisherError(f"decode: expected [1, {cfg.latent_channels}, h, w], got {list(latent.shape)}")
+    if latent.shape[0] != 1:   # vae_decoder.cpp:129-134
+        raise BurnisherError("vae: batch 1 only -- classifier-free guidance is resolved into a "
+                             "single latent before the decoder runs")
+    if latent.shape[2] != latent.shape[3]:
+        raise BurnisherError("vae-decode (hip-gfx950): square latents only")
+    hw = latent.shape[2]
+    side = hw * scale_factor(SDXL_VAE)
+    assert torch.cuda.is_available(), "the hip-gfx950 vae-decode needs an MI355X"
+    call("bh_init", 0)
+    d_latent = torch.from_numpy(f32_to_bf16_bits(latent).view(np.int16)).view(torch.bfloat16).cuda()
+    image = torch.zeros((1, 3, side, side), dtype=torch.bfloat16, device="cuda")
+    stream = torch.cuda.current_stream().cuda_stream
+    with Checkpoint.component(weights, "vae") as ck:
+        dw = VaeDeviceWeights(ck, cfg, stream)
+    engine = ctypes.c_void_p()
+    try:
+        call("bh_vae_create", ctypes.byref(cfg), dw.table, hw, ctypes.byref(engine))
+        for _ in range(max(0, warmup)):
+            call("bh_vae_decode", engine, d_latent.data_ptr(), image.data_ptr(), stream)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        call("bh_vae_decode", engine, d_latent.data_ptr(), image.data_ptr(), stream)
+        torch.cuda.synchronize()
+        secs = time.perf_counter() - t0
+        host = bf16_bits_to_f32(image.cpu().view(torch.int16).numpy().view(np.uint16))
+        free, total = torch.cuda.mem_get_info()
+        peak = int(total - free)
+    finally:
+        if engine.value:
+            lib().bh_vae_destroy(engine)
+        dw.free()
+    np.save(out_path, host.astype("<f4"), allow_pickle=False)
+    return {"metrics": {"latency_s": secs, "peak_vram_bytes": peak},
+            "effective": {"stage": "vae-decode", "dtype": "bf16", "impl": "hip-gfx950",
+                          "weights": "checkpoint", "device": "cuda"},
+            "output_stats": output_stats(host)}
+
+
 def main(argv=None) -> int:
     p = argparse.ArgumentParser(prog="python -m burnisher_amd.stage")
     sub = p.add_subparsers(dest="stage", required=True)
@@ -151,10 +204,18 @@ def main(argv=None) -> int:
     d.add_argument("--layers", type=int, default=None)
     d.add_argument("--warmup", type=int, default=1)
     d.add_argument("--plan", choices=["fused", "opwise"], default="fused")
+    v = sub.add_parser("vae-decode", help="decode one latent to pixels")
+    v.add_argument("--weights", required=True, help="checkpoint directory (holds vae/)")
+    v.add_argument("--latent", required=True)
+    v.add_argument("--out", required=True)
+    v.add_argument("--warmup", type=int, default=1)
     a = p.parse_args(argv)
     try:
-        rec = dit_step(a.weights, a.latent, a.caption, a.mask, a.out, a.timestep, a.layers,
-                       a.warmup, a.plan)
+        if a.stage == "vae-decode":
+            rec = vae_decode(a.weights, a.latent, a.out, a.warmup)
+        else:
+            rec = dit_step(a.weights, a.latent, a.caption, a.mask, a.out, a.timestep, a.layers,
+                           a.warmup, a.plan)
     except BurnisherError as e:   # burnisher_main.cpp:1035-1038: a sentence and exit 1
         print(f"!! {e}", file=sys.stderr)
         return 1

@@ -442,6 +442,19 @@ const bh_dit_weights* bh_dit_weights_view(const bh_dit_device_weights* w);
 int64_t bh_dit_weights_bytes(const bh_dit_device_weights* w);
 void bh_dit_weights_free(bh_dit_device_weights* w);
 
+typedef struct bh_vae_device_weights bh_vae_device_weights;
+
+/* DeviceWeights over the VAE decoder's tensors (the `vae/` component; names and shapes of
+ * declare_pixart_shapes' VAE part, weights.cpp:284-320): checked (present, shape, F32 or BF16)
+ * before anything is allocated, converted to bf16 on the host and copied into one device arena.
+ * Allocates. */
+int bh_vae_weights_load(const bh_checkpoint* ck, const bh_vae_config* cfg, void* stream,
+                        bh_vae_device_weights** out);
+/* The loaded weights as the table bh_vae_create takes; valid until bh_vae_weights_free. */
+const bh_vae_weights* bh_vae_weights_view(const bh_vae_device_weights* w);
+int64_t bh_vae_weights_bytes(const bh_vae_device_weights* w);
+void bh_vae_weights_free(bh_vae_device_weights* w);
+
 #ifdef __cplusplus
 }
 #endif

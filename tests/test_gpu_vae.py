@@ -185,3 +185,47 @@ def test_vae_create_refuses_bad_configurations(hip):
     assert bh.lib().bh_vae_create(ctypes.byref(config_struct(SDXL_VAE)), ctypes.byref(w2), 2,
                                   ctypes.byref(h)) != 0
     assert b"missing" in bh.lib().bh_last_error()
+
+
+def test_vae_weights_from_a_checkpoint_and_the_decode_stage(hip, tmp_path):
+    """The `vae/` component of an F32 checkpoint (as the pinned one is published): loaded weights
+    give the same bytes as weights rounded on the host, and the stage meets the decoder gate."""
+    import contextlib
+    import io
+    import json
+
+    import burnisher_amd as bh
+    from burnisher_amd import stage
+    from burnisher_amd.vae import vae_tensors
+    from safetensors.numpy import save_file
+
+    rng = np.random.default_rng(21)
+    f32 = {}
+    for name, shape in vae_tensors(SDXL_VAE).items():
+        std = 0.1 if "norm" in name else (0.02 if name.endswith(".bias") else 1 / np.sqrt(np.prod(shape[1:])))
+        v = (rng.standard_normal(shape) * std).astype(np.float32)
+        if "norm" in name and name.endswith(".weight"):
+            v += 1.0
+        f32[name] = v
+    d = tmp_path / "ckpt" / "vae"
+    d.mkdir(parents=True)
+    save_file(f32, str(d / "diffusion_pytorch_model.safetensors"))
+    wl = make_vae_workload(SDXL_VAE, latent_hw=4, seed=22)
+    from helpers import to_bf16
+    wl.weights = {n: to_bf16(a) for n, a in f32.items()}
+    want = oracle_decode(wl)
+    # the stage, end to end
+    lat = tmp_path / "latent.npy"
+    np.save(lat, from_bf16(wl.latent))
+    out = tmp_path / "image.npy"
+    buf = io.StringIO()
+    with contextlib.redirect_stdout(buf):
+        assert stage.main(["vae-decode", "--weights", str(tmp_path / "ckpt"), "--latent", str(lat),
+                           "--out", str(out)]) == 0
+    rec = json.loads(buf.getvalue().split("BURNISH_JSON: ")[1])
+    img = np.load(out)
+    assert img.shape == (1, 3, 32, 32) and rec["effective"]["stage"] == "vae-decode"
+    assert rec["output_stats"] == stage.output_stats(img)
+    check_decode(to_bf16(img), want, "vae-decode stage")
+    # loaded weights == host-rounded upload, byte for byte
+    assert np.array_equal(to_bf16(img), decode(wl))
