@@ -82,6 +82,9 @@ def parse() -> argparse.Namespace:
     p.add_argument("--vae", action="store_true",
                    help="time the vae-decode stage (SDXL VAE widths, batch 1) at --resolution; "
                         "one JSON line")
+    p.add_argument("--t5", action="store_true",
+                   help="time the t5-encode stage (T5 v1.1 XXL, [batch, caption-len] ids); one "
+                        "JSON line")
     p.add_argument("--kernels", action="store_true",
                    help="time the isolated kernels at 1024px shapes (GEMMs, self- and "
                         "cross-attention, LayerNorm+modulate); one JSON line per kernel")
@@ -369,6 +372,120 @@ def vae(args) -> int:
     return 0
 
 
+def t5(args) -> int:
+    """The t5-encode stage (T5Encoder::forward, t5_encoder.cpp:132-241): T5 v1.1 XXL on
+    [batch, caption_len] token ids (the pipeline's CFG pair: the empty negative prompt, then a
+    caption), seeded synthetic weights drawn on the device, through the library's encoder engine.
+    K encodes timed between HIP events on one stream after W warm-up encodes (the id upload is
+    inside: the engine takes host ids); one more encode runs with the launch profiler for the
+    per-class breakdown. The roofline is the GEMM class (MFMA): its algorithmic FLOP over its
+    summed launch time. The CPU baseline is the stock oracle's encoder restricted to ONE of the
+    layers at the full [batch, caption_len] shape on this host, scaled by the layer count."""
+    import numpy as np
+    import torch
+
+    import burnisher_amd as bh
+    from burnisher_amd.t5 import (T5_XXL, T5Workload, config_struct, make_t5_workload, synthetic_ids,
+                                  t5_encode_flops, t5_tensors)
+
+    bh.check(bh.lib().bh_init(0), "bh_init")
+    B, S = args.batch, args.caption_len
+    cfg = dict(T5_XXL)
+    lengths = [1] + [120] * (B - 1)
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(20261203)
+    tensors = {}
+    for name, shape in t5_tensors(cfg).items():
+        t = torch.randn(shape, generator=gen, device="cuda", dtype=torch.float32)
+        if "layer_norm" in name:
+            t = 1.0 + 0.1 * t
+        elif name.endswith("SelfAttention.q.weight"):
+            t = t / float(np.sqrt(shape[1] * cfg["d_kv"]))
+        elif name != "shared.weight" and "relative_attention_bias" not in name:
+            t = t / float(np.sqrt(shape[1]))
+        tensors[name] = t.to(torch.bfloat16)
+        del t
+    wl = T5Workload(cfg=cfg, batch=B, seq=S)
+    wl.ids = synthetic_ids(B, S, cfg["vocab_size"], lengths, 20261203)
+    c = config_struct(cfg)
+    w, keep = wl.table(tensors)
+    h = ctypes.c_void_p()
+    bh.call("bh_t5_create", ctypes.byref(c), ctypes.byref(w), B, S, ctypes.byref(h))
+    out = torch.zeros((B, S, cfg["d_model"]), dtype=torch.bfloat16, device="cuda")
+    stream = torch.cuda.Stream()
+    sp = stream.cuda_stream
+    steps = max(1, min(args.steps, 20))
+    for _ in range(max(1, args.warmup)):
+        bh.call("bh_t5_encode", h, wl.ids.ctypes.data, out.data_ptr(), sp)
+    torch.cuda.synchronize()
+    with torch.cuda.stream(stream):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        for _ in range(steps):
+            bh.call("bh_t5_encode", h, wl.ids.ctypes.data, out.data_ptr(), sp)
+        b.record(stream)
+    torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / steps
+    o = out.float()
+    assert torch.isfinite(o).all() and o.std() > 1e-3, "degenerate encoder output"
+    bh.check(bh.lib().bh_profile_enable((1 << bh.K_GEMM_QKV + 1) - 1), "bh_profile_enable")
+    bh.call("bh_t5_encode", h, wl.ids.ctypes.data, out.data_ptr(), sp)
+    torch.cuda.synchronize()
+    breakdown = {}
+    for cls, name in enumerate(bh.KERNEL_CLASSES[:6]):
+        tot, n, work = ctypes.c_double(), ctypes.c_int64(), ctypes.c_double()
+        bh.check(bh.lib().bh_profile_read(cls, ctypes.byref(tot), ctypes.byref(n), ctypes.byref(work)))
+        if n.value:
+            breakdown[name] = {"ms": round(tot.value, 4), "launches": n.value, "work": work.value}
+    bh.lib().bh_profile_enable(0)
+    ws = bh.lib().bh_t5_workspace_bytes(h)
+    bh.lib().bh_t5_destroy(h)
+    flops = t5_encode_flops(cfg, B, S)
+    g = breakdown.get("gemm", {"ms": 0.0, "work": 0.0})
+    gemm_tflops = g["work"] / (g["ms"] * 1e-3) / 1e12 if g["ms"] else 0.0
+    tflops = flops["total"] / (ms * 1e-3) / 1e12
+    line = {
+        "metric": f"t5-encode ms bf16 (1 GPU)", "value": round(ms, 4), "unit": "ms", "n_gpus": 1,
+        "steps": steps, "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": False,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic: seeded weights drawn on the device (projections N(0, 1/fan_in), q with a "
+                "further 1/sqrt(d_kv), embedding "
+                "and relative bias N(0, 1), RMSNorm weights 1 + N(0, 0.01)), seeded token ids",
+        "config": {"workload": f"T5 v1.1 XXL encoder, ids [{B}, {S}] (lengths {lengths})",
+                   "layers": cfg["num_layers"], "d_model": cfg["d_model"], "d_ff": cfg["d_ff"],
+                   "heads": cfg["num_heads"], "engine_device_bytes": ws},
+        "roofline": {"bound": "mfma", "kernel": "GEMM class (packed qkv, o, packed wi, wo)",
+                     "achieved": round(gemm_tflops, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(gemm_tflops / PEAK_BF16_TFLOPS, 4), "traffic": None},
+        "step": {"flop": flops["total"], "tflops": round(tflops, 2),
+                 "mfma_frac": round(tflops / PEAK_BF16_TFLOPS, 4),
+                 "ceiling_ms": round(flops["total"] / (PEAK_BF16_TFLOPS * 1e12) * 1e3, 3)},
+        "kernels": breakdown,
+    }
+    del tensors, keep, w
+    torch.cuda.empty_cache()
+    if not args.no_cpu:
+        import oracle
+        threads = args.cpu_threads or min(16, os.cpu_count() or 1)
+        one = dict(cfg, num_layers=1)
+        log(f"cpu baseline: generating one XXL layer on the host")
+        sample = make_t5_workload(one, batch=B, seq=S, lengths=lengths)
+        sc = config_struct(one)
+        sw, skeep = sample.table()
+        res = np.zeros((B, S, cfg["d_model"]), np.uint16)
+        log(f"cpu baseline: stock encoder, 1 layer at [{B}, {S}], {threads} threads")
+        t0 = time.perf_counter()
+        oracle.call(oracle.stock(), "stock_t5_forward", ctypes.byref(sc), ctypes.byref(sw),
+                    sample.ids.ctypes.data, B, S, res.ctypes.data, threads)
+        secs = time.perf_counter() - t0
+        line["cpu_baseline"] = {"value": round(secs * cfg["num_layers"] * 1e3, 1), "unit": "ms",
+                                "cores": threads, "kind": "port",
+                                "sample": f"stock oracle encoder with 1 of the {cfg['num_layers']} layers at "
+                                          f"the full [{B}, {S}] shape, {secs:.2f} s, scaled x{cfg['num_layers']}"}
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 def cpu_baseline(wl, threads: int) -> dict:
     """The stock oracle's whole dit-step (all 28 blocks) on this host, timed once."""
     import numpy as np
@@ -400,6 +517,8 @@ def main() -> int:
         return denoise(args)
     if args.vae:
         return vae(args)
+    if args.t5:
+        return t5(args)
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
               "(the dit-step would shard on the CFG batch, see DESIGN.md)", file=sys.stderr)

@@ -158,6 +158,12 @@ SIGNATURES = {
     "bh_vae_decode": ([_V, _V, _V, _V], _I),
     "bh_vae_workspace_bytes": ([_V], _I64),
     "bh_vae_destroy": ([_V], None),
+    "bh_t5_relative_bucket": ([_I, _I, _I], _I),
+    "bh_gather": ([_V, _V, _V, _I64, _I64, _I64, _I, _V], _I),
+    "bh_t5_create": ([_V, _V, _I64, _I64, _V], _I),
+    "bh_t5_encode": ([_V, _V, _V, _V], _I),
+    "bh_t5_workspace_bytes": ([_V], _I64),
+    "bh_t5_destroy": ([_V], None),
     "bh_conv2d": ([_V, _V, _V, _V, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I, _V], _I),
     "bh_vae_weights_load": ([_V, _V, _V, ctypes.POINTER(_V)], _I),
     "bh_vae_weights_view": ([_V], _V),

@@ -15,7 +15,8 @@
 // head_dim 72 is zero-padded to 96 for the score product (three K=32 steps, the padding lanes
 // are zeroed in registers) and to 80 for the output (five 16-row tiles of V^T, rows 72-79 zero).
 //
-// Numerics follow the reference oracle (ops_cpu.cpp:84-131): scores in fp32 times `scale`, a
+// Numerics follow the reference oracle (ops_cpu.cpp:84-131): scores in fp32 times `scale`, plus
+// the additive bias [heads, q_len, kv_len] when given (T5's relative positions), a
 // masked key scores exactly -1e9 (so an all-masked row is uniform over V, not NaN), exp in fp32,
 // division by the denominator at the end. Unlike the oracle, P is rounded to bf16 for the MFMA
 // and the row max is a running max (online softmax). A block of 64 keys that are all masked is
@@ -43,6 +44,7 @@ struct AttnArgs {
     const bf16_t* v;
     bf16_t* out;
     const void* mask;
+    const bf16_t* bias;   // [H, Sq, Skv] or null
     int mask_f32;
     int64_t B, H, Sq, Skv, D;
     int64_t ld_q, ld_kv, ld_o;
@@ -260,6 +262,8 @@ __global__ void __launch_bounds__(kThreads, 1) k_flash(AttnArgs a) {
                 for (int r = 0; r < 4; ++r) {
                     const int64_t kv = kvb + t * 16 + g * 4 + r;
                     float val = s[t][u][r] * a.scale;
+                    if (a.bias && kv < a.Skv && q0 + u * 16 + c16 < a.Sq)
+                        val = __fadd_rn(val, bf2f(a.bias[(h * a.Sq + q0 + u * 16 + c16) * a.Skv + kv]));
                     if (kv >= a.Skv) val = -INFINITY;
                     else if (mvals[t][r] == 0.0f) val = -1e9f;
                     s[t][u][r] = val;
@@ -424,10 +428,10 @@ bf16_t* vt_workspace(size_t elems) {
 
 void launch_attention_bf16(const bf16_t* q, const bf16_t* k, const bf16_t* v, bf16_t* out,
                            const AttnShape& sh, const void* key_mask, bool mask_f32,
-                           hipStream_t s) {
+                           hipStream_t s, const bf16_t* bias) {
     if (sh.batch * sh.heads * sh.q_len == 0) return;
     // head_dim 512, one head, self-attention, unmasked (the VAE mid-block): its own kernel.
-    if (sh.head_dim == 512 && sh.heads == 1 && sh.q_len == sh.kv_len && !key_mask &&
+    if (sh.head_dim == 512 && sh.heads == 1 && sh.q_len == sh.kv_len && !key_mask && !bias &&
         sh.ld_q == 512 && sh.ld_kv == 512 && sh.ld_o == 512 && aligned16(q) && aligned16(k) &&
         aligned16(v) && aligned16(out)) {
         const int64_t ld = vt512_ld(sh.kv_len);
@@ -439,7 +443,7 @@ void launch_attention_bf16(const bf16_t* q, const bf16_t* k, const bf16_t* v, bf
         return;
     }
     // head_dim 72 (the DiT): V transposed once, then the flash kernel built for that width.
-    const bool fast72 = sh.head_dim == 72 && sh.kv_len <= 16384 && sh.ld_q % 8 == 0 &&
+    const bool fast72 = !bias && sh.head_dim == 72 && sh.kv_len <= 16384 && sh.ld_q % 8 == 0 &&
                         sh.ld_kv % 8 == 0 && sh.ld_o % 4 == 0 && aligned16(q) && aligned16(k) &&
                         aligned16(v) && (reinterpret_cast<uintptr_t>(out) % 8 == 0);
     if (fast72) {
@@ -459,6 +463,7 @@ void launch_attention_bf16(const bf16_t* q, const bf16_t* k, const bf16_t* v, bf
     AttnArgs a;
     a.q = q; a.k = k; a.v = v; a.out = out;
     a.mask = key_mask; a.mask_f32 = mask_f32 ? 1 : 0;
+    a.bias = bias;
     a.B = sh.batch; a.H = sh.heads; a.Sq = sh.q_len; a.Skv = sh.kv_len; a.D = sh.head_dim;
     a.ld_q = sh.ld_q; a.ld_kv = sh.ld_kv; a.ld_o = sh.ld_o;
     a.scale = sh.scale;

@@ -271,7 +271,7 @@ int attention_impl(const void* q, int64_t ld_q, const void* k, const void* v, in
                      scale > 0.0f ? scale : 1.0f / std::sqrt(static_cast<float>(head_dim))};
         const bool flash512 = head_dim == 512 && heads == 1 && q_len == kv_len && !key_mask &&
                               ld_q == 512 && ld_kv == 512 && ld_o == 512;
-        if (f32 || bias || (head_dim > 128 && !flash512)) {
+        if (f32 || (bias && head_dim > 128) || (head_dim > 128 && !flash512)) {
             ProfileScope ps(q_len == kv_len ? K_ATTN_SELF : K_ATTN_CROSS, as_stream(stream),
                             4.0 * batch * heads * static_cast<double>(q_len) * kv_len * head_dim);
             launch_attention_generic(q, k, v, out, sh, bias, key_mask, mask_f32, f32,
@@ -280,7 +280,7 @@ int attention_impl(const void* q, int64_t ld_q, const void* k, const void* v, in
         }
         launch_attention_bf16(static_cast<const bf16_t*>(q), static_cast<const bf16_t*>(k),
                               static_cast<const bf16_t*>(v), static_cast<bf16_t*>(out), sh,
-                              key_mask, mask_f32, as_stream(stream));
+                              key_mask, mask_f32, as_stream(stream), static_cast<const bf16_t*>(bias));
     });
 }
 }  // namespace
@@ -304,6 +304,21 @@ int bh_attention_strided(const void* q, int64_t ld_q, const void* k, const void*
     }
     return attention_impl(q, ld_q, k, v, ld_kv, out, ld_out, batch, heads, q_len, kv_len,
                           head_dim, scale, nullptr, key_mask, mask_dtype, dtype, stream);
+}
+
+int bh_gather(const void* table, const float* ids, void* out, int64_t rows, int64_t cols,
+              int64_t table_rows, int dtype, void* stream) {
+    return guarded([&] {
+        const char* op = "gather (hip-gfx950)";
+        require_nonneg(rows, op, "rows");
+        require_nonneg(cols, op, "cols");
+        require_nonneg(table_rows, op, "table_rows");
+        if (rows == 0 || cols == 0) return;
+        require_device_ptr(table, op, "table");
+        require_device_ptr(ids, op, "ids");
+        require_device_ptr(out, op, "out");
+        launch_gather(table, ids, out, rows, cols, table_rows, is_f32(dtype), as_stream(stream));
+    });
 }
 
 int bh_norm(const void* x, const void* weight, const void* bias, void* out, int64_t rows,

@@ -263,9 +263,10 @@ struct AttnShape {
     int64_t ld_q, ld_kv, ld_o;  // row strides in elements
     float scale;                // resolved (never 0)
 };
+// bias: optional bf16 [heads, q_len, kv_len] added to the scaled scores (head_dim <= 128 only).
 void launch_attention_bf16(const bf16_t* q, const bf16_t* k, const bf16_t* v, bf16_t* out,
                            const AttnShape& sh, const void* key_mask, bool mask_f32,
-                           hipStream_t s);
+                           hipStream_t s, const bf16_t* bias = nullptr);
 // Flash attention at head_dim 72 with V supplied transposed (flash72.hip): vt holds, for each
 // (b, h, d), a row of vt_ld >= flash72_vt_ld(kv_len) keys, zero past kv_len.
 int64_t flash72_vt_ld(int64_t kv_len);
@@ -296,6 +297,16 @@ void launch_modulate(const void* x, const void* scale, const void* shift, void* 
                      const void* gate, bool f32, hipStream_t s);
 void launch_activation(const void* x, void* out, int64_t numel, int kind, const void* gate,
                        bool f32, hipStream_t s);
+// Gated GELU over the rows of a fused [rows, 2F] projection: out[r, j] = gelu_tanh(in[r, j]) *
+// in[r, F + j], as ActivationArgs GeluGated computes it on two separate tensors.
+void launch_gelu_gated_rows(const bf16_t* in, bf16_t* out, int64_t rows, int64_t F, hipStream_t s);
+// ---- the T5 encoder's kernels (t5.hip) ----
+// GatherArgs: out[r, :] = table[(int64)ids[r], :]; an id outside [0, table_rows) gives a NaN row.
+void launch_gather(const void* table, const float* ids, void* out, int64_t rows, int64_t cols,
+                   int64_t table_rows, bool f32, hipStream_t s);
+// bias[h, q, k] = rel[bucket[k - q + S - 1] * heads + h] (bf16 [heads, S, S]).
+void launch_rel_bias(const bf16_t* rel, const int* bucket, bf16_t* bias, int64_t heads, int64_t S,
+                     hipStream_t s);
 void launch_add(const void* a, const void* b, void* out, int64_t outer, int64_t inner,
                 float scale, bool broadcast_b, bool f32, hipStream_t s);
 void launch_chunk(const void* mod, const void* table, void* out, int64_t batch, int64_t channels,

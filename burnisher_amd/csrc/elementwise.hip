@@ -450,6 +450,20 @@ __global__ void __launch_bounds__(256) k_activation(const T* __restrict__ x, T* 
     }
 }
 
+// out[r, j] = round(gelu_tanh(in[r, j]) * in[r, F + j]): the two halves of a fused wi_0/wi_1
+// projection, each already a stored bf16 as in the reference's two GEMM outputs.
+__global__ void __launch_bounds__(256) k_gelu_gated_rows(const bf16_t* __restrict__ in,
+                                                         bf16_t* __restrict__ out, int64_t rows,
+                                                         int64_t F) {
+    const int64_t n = rows * F;
+    for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < n;
+         i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+        const int64_t r = i / F, j = i - r * F;
+        const bf16_t* row = in + r * 2 * F;
+        out[i] = f2bf(__fmul_rn(gelu_tanh(bf2f(row[j])), bf2f(row[F + j])));
+    }
+}
+
 // ---- patchify / unpatchify ------------------------------------------------------------------
 
 // One thread per token element. Forward: token layout (c, ky, kx); inverse: (ky, kx, c).
@@ -649,6 +663,13 @@ void launch_activation(const void* x, void* out, int64_t numel, int kind, const 
             static_cast<const bf16_t*>(gate));
     }
     launch_check("activation");
+}
+
+void launch_gelu_gated_rows(const bf16_t* in, bf16_t* out, int64_t rows, int64_t F, hipStream_t s) {
+    if (rows * F == 0) return;
+    ProfileScope ps(K_ELEMENTWISE, s, 6.0 * rows * F);
+    k_gelu_gated_rows<<<grid_for(rows * F), 256, 0, s>>>(in, out, rows, F);
+    launch_check("gated gelu");
 }
 
 void launch_add(const void* a, const void* b, void* out, int64_t outer, int64_t inner,

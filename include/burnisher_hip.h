@@ -455,6 +455,62 @@ const bh_vae_weights* bh_vae_weights_view(const bh_vae_device_weights* w);
 int64_t bh_vae_weights_bytes(const bh_vae_device_weights* w);
 void bh_vae_weights_free(bh_vae_device_weights* w);
 
+/* ---- the T5 v1.1 text encoder (the t5-encode stage, t5_encoder.cpp) ------------------------ */
+
+/* T5Config (models.h:94-103), plus the relative-position table's bucket count: the first
+ * dimension of relative_attention_bias.weight (weights.cpp:231-232; the reference reads it off
+ * that tensor, t5_encoder.cpp:95). The bucket table's max_distance is 128, as there. */
+typedef struct bh_t5_config {
+    int num_layers;   /* 24 */
+    int d_model;      /* 4096 */
+    int d_ff;         /* 10240 */
+    int d_kv;         /* 64 */
+    int num_heads;    /* 64 */
+    int vocab_size;   /* 32128 */
+    int gated;        /* 1: gelu(wi_0 x) * (wi_1 x); 0: gelu(wi_0 x) */
+    int num_buckets;  /* 32 */
+    double eps;       /* 1e-6 */
+} bh_t5_config;
+
+/* The encoder's weights by checkpoint name (the T5 part of declare_pixart_shapes,
+ * weights.cpp:226-244): bf16 tensors, linear weights [out, in], norms [d_model], the shared
+ * embedding [vocab_size, d_model], the relative bias [num_buckets, num_heads]. */
+typedef struct bh_t5_weights {
+    int count;
+    const char* const* names;
+    const void* const* tensors;
+} bh_t5_weights;
+
+typedef struct bh_t5 bh_t5;
+
+/* t5_relative_bucket (t5_encoder.cpp:34-48): the bidirectional bucket of key minus query
+ * position. Host only; the encoder builds its table with it. */
+int bh_t5_relative_bucket(int relative_position, int num_buckets, int max_distance);
+
+/* GatherArgs (ops.h:198-207): out[r, :] = table[(int64)ids[r], :] for r < rows, ids fp32 on the
+ * device (the reference's contract), table [table_rows, cols]. A row whose id lies outside
+ * [0, table_rows) is written as NaN instead of being read out of bounds. Replaces `gather_cuda`
+ * (src/cuda/ops_cuda.cu:1097-1115). */
+int bh_gather(const void* table, const float* ids, void* out, int64_t rows, int64_t cols,
+              int64_t table_rows, int dtype, void* stream);
+
+/* Prepares T5Encoder::forward (t5_encoder.cpp:132-241) for [batch, seq_len] token ids: checks
+ * the configuration and every weight name, packs each layer's q/k/v weights into one [3*inner,
+ * d_model] operand and wi_0/wi_1 into one [2*d_ff, d_model] operand (engine-owned copies, so
+ * each projection is one GEMM), and allocates every activation once. The caller's weight
+ * pointers must stay valid for the engine's lifetime. Allocates; encode does not. */
+int bh_t5_create(const bh_t5_config* cfg, const bh_t5_weights* w, int64_t batch, int64_t seq_len,
+                 bh_t5** out);
+/* token_ids: HOST fp32 [batch, seq_len] (integers, pad id 0), checked against the vocabulary
+ * before any device work as the reference does (t5_encoder.cpp:146-156); out: device bf16
+ * [batch, seq_len, d_model]. The key mask (id != 0) and the relative-bias table [heads, seq,
+ * seq] are rebuilt from the ids and the weights on every call. On `stream`; it waits only for
+ * the previous call's id upload before reusing that staging buffer. */
+int bh_t5_encode(bh_t5* e, const float* token_ids, void* out, void* stream);
+/* Device bytes the engine holds (activations, packed weights, bias table). */
+int64_t bh_t5_workspace_bytes(const bh_t5* e);
+void bh_t5_destroy(bh_t5* e);
+
 #ifdef __cplusplus
 }
 #endif

@@ -51,6 +51,8 @@ _STOCK_SIGS = {
     "stock_upsample": ([_V, _V, _I64, _I64, _I64, _I64, _I64, _I], _I),
     "stock_transpose": ([_V, _V, _I64, _I64, _I64, _I, _I], _I),
     "stock_vae_forward": ([_V, _V, _V, _I64, _V, _I, _I], _I),
+    "stock_t5_bucket": ([_I, _I, _I], _I),
+    "stock_t5_forward": ([_V, _V, _V, _I64, _I64, _V, _I], _I),
 }
 _REF_SIGS = {
     "ref_last_error": ([], ctypes.c_char_p),
@@ -81,6 +83,8 @@ _REF_SIGS = {
     "ref_upsample": ([_V, _V, _I64, _I64, _I64, _I64, _I64, _I], _I),
     "ref_transpose": ([_V, _V, _I64, _I64, _I64, _I, _I], _I),
     "ref_vae_forward": ([_V, _V, _V, _I64, _V], _I),
+    "ref_t5_bucket": ([_I, _I, _I], _I),
+    "ref_t5_forward": ([_V, _V, _V, _I64, _I64, _V], _I),
 }
 
 _stock = None

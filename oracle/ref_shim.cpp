@@ -112,13 +112,14 @@ class TableWeights : public WeightSource {
 // itself declares for those names.
 class NamedWeights : public WeightSource {
   public:
-    explicit NamedWeights(const bh_vae_weights& w) {
-        for (int i = 0; i < w.count; ++i) ptr_[w.names[i]] = w.tensors[i];
+    explicit NamedWeights(const bh_vae_weights& w) : NamedWeights(w.count, w.names, w.tensors) {}
+    NamedWeights(int count, const char* const* names, const void* const* tensors) {
+        for (int i = 0; i < count; ++i) ptr_[names[i]] = tensors[i];
     }
     bool has(const std::string& name) const override { return ptr_.count(name) != 0; }
     Tensor get(const std::string& name) const override {
         auto it = ptr_.find(name);
-        if (it == ptr_.end()) throw std::runtime_error("ref vae weights: no '" + name + "'");
+        if (it == ptr_.end()) throw std::runtime_error("ref weights: no '" + name + "'");
         return view(it->second, shape_.at(name), BH_BF16);
     }
     void set_shape(const std::string& name, std::vector<int64_t> shape) { shape_[name] = std::move(shape); }
@@ -415,6 +416,40 @@ int ref_vae_forward(const bh_vae_config* cfg, const bh_vae_weights* w, const uin
         Tensor x = view(latent, {1, vc.latent_channels, latent_hw, latent_hw}, BH_BF16);
         Tensor out = dec.forward(x, impls);
         std::memcpy(image, out.data(), static_cast<size_t>(out.numel()) * 2);
+    });
+}
+
+int ref_t5_bucket(int rp, int num_buckets, int max_distance) {
+    return t5_relative_bucket(rp, num_buckets, max_distance);
+}
+
+// T5Encoder::forward (t5_encoder.cpp:132-241) on the reference's own model code; the weight shapes
+// come from its own declaration (declare_pixart_shapes, weights.cpp:226-244).
+int ref_t5_forward(const bh_t5_config* cfg, const bh_t5_weights* w, const float* ids, int64_t batch,
+                   int64_t seq, uint16_t* out) {
+    return guard([&] {
+        T5Config t5;
+        t5.num_layers = cfg->num_layers;
+        t5.d_model = cfg->d_model;
+        t5.d_ff = cfg->d_ff;
+        t5.d_kv = cfg->d_kv;
+        t5.num_heads = cfg->num_heads;
+        t5.vocab_size = cfg->vocab_size;
+        t5.gated = cfg->gated != 0;
+        t5.eps = cfg->eps;
+        if (cfg->num_buckets != 32) throw std::runtime_error("ref t5: the declaration has 32 buckets");
+        NamedWeights nw(w->count, w->names, w->tensors);
+        DiTConfig dit;
+        dit.num_layers = 0;
+        VaeConfig vc;
+        SyntheticWeights decl(DType::BF16, 0);
+        declare_pixart_shapes(decl, t5, dit, vc);
+        for (int i = 0; i < w->count; ++i) nw.set_shape(w->names[i], decl.get(w->names[i]).shape());
+        T5Encoder enc(t5, nw, DType::BF16);
+        const ImplSelection impls = ImplSelection::from_request("stock", Device::CPU);
+        Tensor t = view(ids, {batch, seq}, BH_F32);
+        Tensor o = enc.forward(t, impls);
+        std::memcpy(out, o.data(), static_cast<size_t>(o.numel()) * 2);
     });
 }
 

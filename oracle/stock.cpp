@@ -857,6 +857,91 @@ VaeTable vae_table(const bh_vae_weights& w) {
     return t;
 }
 
+// ---- the T5 v1.1 encoder (t5_encoder.cpp:132-241), rows [batch * seq, d_model] ------------
+
+// t5_relative_bucket (t5_encoder.cpp:34-48): half the buckets for keys before the query (or at
+// it), half for keys after; distances below a quarter of the buckets are exact, the rest are
+// log-spaced up to max_distance and saturate at the last bucket of the half.
+int t5_bucket(int rp, int num_buckets, int max_distance) {
+    const int half = num_buckets / 2;
+    const int side = rp > 0 ? half : 0;
+    const int n = rp < 0 ? -rp : rp;
+    const int exact = half / 2;
+    if (n < exact) return side + n;
+    const double frac = std::log(static_cast<double>(n) / exact) /
+                        std::log(static_cast<double>(max_distance) / exact) * (half - exact);
+    const int large = std::min(exact + static_cast<int>(frac), half - 1);
+    return side + large;
+}
+
+// The encoder (t5_encoder.cpp:132-241): embedding rows of the ids (checked against the
+// vocabulary first, :146-156); a [heads, S, S] bias from the bucket of k - q (:63-120); a key
+// mask of id != 0 (:180-184); per layer RMSNorm, q/k/v projections, attention with scale 1,
+// the bias and the mask, the output projection and a residual add; RMSNorm, the gated-GELU
+// FFN and a residual add; a final RMSNorm. Every intermediate is a bf16 tensor, as there.
+void t5_forward(const bh_t5_config& c, const VaeTable& w, const float* ids, int64_t B, int64_t S,
+                uint16_t* out, int threads) {
+    using Buf = std::vector<uint16_t>;
+    const int64_t d = c.d_model, H = c.num_heads, inner = H * c.d_kv, M = B * S, F = c.d_ff;
+    for (int64_t i = 0; i < M; ++i) {
+        const int64_t id = static_cast<int64_t>(ids[i]);
+        if (id < 0 || id >= c.vocab_size)
+            throw std::runtime_error("t5: token id " + std::to_string(id) + " is outside the vocabulary");
+    }
+    const auto* table = static_cast<const uint16_t*>(w.at("shared.weight"));
+    Buf x(static_cast<size_t>(M * d));
+    for (int64_t i = 0; i < M; ++i)
+        std::memcpy(&x[i * d], table + static_cast<int64_t>(ids[i]) * d, static_cast<size_t>(d) * 2);
+    const auto* rel = static_cast<const uint16_t*>(
+        w.at("encoder.block.0.layer.0.SelfAttention.relative_attention_bias.weight"));
+    Buf bias(static_cast<size_t>(H * S * S));
+    for (int64_t q = 0; q < S; ++q)
+        for (int64_t k = 0; k < S; ++k) {
+            const int bk = t5_bucket(static_cast<int>(k - q), c.num_buckets, 128);
+            for (int64_t h = 0; h < H; ++h) bias[(h * S + q) * S + k] = rel[bk * H + h];
+        }
+    Buf mask(static_cast<size_t>(M));
+    for (int64_t i = 0; i < M; ++i) mask[i] = static_cast<int64_t>(ids[i]) == 0 ? 0 : 0x3f80;
+    Buf normed(x.size()), q(static_cast<size_t>(M * inner)), k(q.size()), v(q.size()), ctx(q.size()),
+        proj(x.size()), h0(static_cast<size_t>(M * F)), h1(h0.size()), hact(h0.size());
+    const float eps = static_cast<float>(c.eps);
+    auto blk = [](int i, const char* tail) { return "encoder.block." + std::to_string(i) + "." + tail; };
+    auto gemm = [&](const Buf& a, const std::string& wn, Buf& o, int64_t n, int64_t kk) {
+        gemm_impl(a.data(), w.at(wn), nullptr, o.data(), M, n, kk, true, BH_EPI_NONE, BH_BF16, threads);
+    };
+    for (int l = 0; l < c.num_layers; ++l) {
+        norm_impl(x.data(), w.at(blk(l, "layer.0.layer_norm.weight")), nullptr, normed.data(), M, d, eps,
+                  true, BH_BF16, threads);
+        gemm(normed, blk(l, "layer.0.SelfAttention.q.weight"), q, inner, d);
+        gemm(normed, blk(l, "layer.0.SelfAttention.k.weight"), k, inner, d);
+        gemm(normed, blk(l, "layer.0.SelfAttention.v.weight"), v, inner, d);
+        attention_impl(q.data(), k.data(), v.data(), ctx.data(),
+                       AttnGeom{B, H, S, S, c.d_kv, inner, inner, inner}, 1.0f, bias.data(), mask.data(),
+                       BH_BF16, BH_BF16, threads, false);
+        gemm(ctx, blk(l, "layer.0.SelfAttention.o.weight"), proj, d, inner);
+        add_impl(x.data(), proj.data(), x.data(), M, d, 1.0f, false, BH_BF16);
+        norm_impl(x.data(), w.at(blk(l, "layer.1.layer_norm.weight")), nullptr, normed.data(), M, d, eps,
+                  true, BH_BF16, threads);
+        gemm(normed, blk(l, "layer.1.DenseReluDense.wi_0.weight"), h0, F, d);
+        if (c.gated) {
+            gemm(normed, blk(l, "layer.1.DenseReluDense.wi_1.weight"), h1, F, d);
+            activation_impl(h0.data(), hact.data(), M * F, BH_EPI_GELU_GATED, h1.data(), BH_BF16);
+        } else {
+            activation_impl(h0.data(), hact.data(), M * F, BH_EPI_GELU, nullptr, BH_BF16);
+        }
+        gemm(hact, blk(l, "layer.1.DenseReluDense.wo.weight"), proj, d, F);
+        add_impl(x.data(), proj.data(), x.data(), M, d, 1.0f, false, BH_BF16);
+    }
+    norm_impl(x.data(), w.at("encoder.final_layer_norm.weight"), nullptr, out, M, d, eps, true, BH_BF16,
+              threads);
+}
+
+VaeTable name_table(int count, const char* const* names, const void* const* tensors) {
+    VaeTable t;
+    for (int i = 0; i < count; ++i) t.t.emplace_back(names[i], tensors[i]);
+    return t;
+}
+
 thread_local std::string g_err;
 
 template <typename Fn>
@@ -1048,6 +1133,18 @@ int stock_vae_forward(const bh_vae_config* cfg, const bh_vae_weights* w, const u
                       int64_t latent_hw, uint16_t* image, int threads, int stop_after) {
     return guard([&] {
         vae_forward(*cfg, vae_table(*w), latent, latent_hw, image, resolve_threads(threads), stop_after);
+    });
+}
+
+int stock_t5_bucket(int rp, int num_buckets, int max_distance) {
+    return t5_bucket(rp, num_buckets, max_distance);
+}
+
+int stock_t5_forward(const bh_t5_config* cfg, const bh_t5_weights* w, const float* ids, int64_t batch,
+                     int64_t seq, uint16_t* out, int threads) {
+    return guard([&] {
+        t5_forward(*cfg, name_table(w->count, w->names, w->tensors), ids, batch, seq, out,
+                   resolve_threads(threads));
     });
 }
 
