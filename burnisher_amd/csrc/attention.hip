@@ -45,6 +45,7 @@ struct AttnArgs {
     bf16_t* out;
     const void* mask;
     const bf16_t* bias;   // [H, Sq, Skv] or null
+    int bias_vec;         // rows of bias are read 8 bytes at a time (Skv % 4 == 0, 8-byte base)
     int mask_f32;
     int64_t B, H, Sq, Skv, D;
     int64_t ld_q, ld_kv, ld_o;
@@ -244,6 +245,29 @@ __global__ void __launch_bounds__(kThreads, 1) k_flash(AttnArgs a) {
             }
         }
 
+        // the bias of this lane's four keys per (t, u): one 8-byte load when rows are 8-byte aligned
+        float bvals[kKT][kQT][4];
+        if (a.bias) {
+#pragma unroll
+            for (int u = 0; u < kQT; ++u) {
+                const int64_t qi = min(q0 + u * 16 + c16, a.Sq - 1);
+                const bf16_t* brow = a.bias + (h * a.Sq + qi) * a.Skv;
+#pragma unroll
+                for (int t = 0; t < kKT; ++t) {
+                    const int64_t kv = kvb + t * 16 + g * 4;
+                    if (a.bias_vec && kv + 3 < a.Skv) {
+                        const uint2 raw = *reinterpret_cast<const uint2*>(brow + kv);
+                        bvals[t][u][0] = __uint_as_float(raw.x << 16);
+                        bvals[t][u][1] = __uint_as_float(raw.x & 0xffff0000u);
+                        bvals[t][u][2] = __uint_as_float(raw.y << 16);
+                        bvals[t][u][3] = __uint_as_float(raw.y & 0xffff0000u);
+                    } else {
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) bvals[t][u][r] = kv + r < a.Skv ? bf2f(brow[kv + r]) : 0.0f;
+                    }
+                }
+            }
+        }
         // scale, mask, running max, exponentials (base 2 with log2(e) folded into the scale)
         float mvals[kKT][4];
 #pragma unroll
@@ -262,8 +286,7 @@ __global__ void __launch_bounds__(kThreads, 1) k_flash(AttnArgs a) {
                 for (int r = 0; r < 4; ++r) {
                     const int64_t kv = kvb + t * 16 + g * 4 + r;
                     float val = s[t][u][r] * a.scale;
-                    if (a.bias && kv < a.Skv && q0 + u * 16 + c16 < a.Sq)
-                        val = __fadd_rn(val, bf2f(a.bias[(h * a.Sq + q0 + u * 16 + c16) * a.Skv + kv]));
+                    if (a.bias) val = __fadd_rn(val, bvals[t][u][r]);
                     if (kv >= a.Skv) val = -INFINITY;
                     else if (mvals[t][r] == 0.0f) val = -1e9f;
                     s[t][u][r] = val;
@@ -464,6 +487,7 @@ void launch_attention_bf16(const bf16_t* q, const bf16_t* k, const bf16_t* v, bf
     a.q = q; a.k = k; a.v = v; a.out = out;
     a.mask = key_mask; a.mask_f32 = mask_f32 ? 1 : 0;
     a.bias = bias;
+    a.bias_vec = bias && sh.kv_len % 4 == 0 && (reinterpret_cast<uintptr_t>(bias) & 7) == 0;
     a.B = sh.batch; a.H = sh.heads; a.Sq = sh.q_len; a.Skv = sh.kv_len; a.D = sh.head_dim;
     a.ld_q = sh.ld_q; a.ld_kv = sh.ld_kv; a.ld_o = sh.ld_o;
     a.scale = sh.scale;

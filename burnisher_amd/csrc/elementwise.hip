@@ -125,6 +125,68 @@ __global__ void __launch_bounds__(256) k_norm(const T* __restrict__ x, const T* 
     }
 }
 
+// The same op for bf16 rows of cols % 8 == 0 and at most NV * 512 columns: one wave per row,
+// the row read ONCE into registers as 16-byte vectors (the generic kernel's three scalar passes
+// over global memory made a 600 x 4096 RMSNorm latency-bound at ~45 us). Statistics in fp64
+// as the oracle forms them; an RMS row's mean is exactly 0.
+template <int NV>
+__global__ void __launch_bounds__(256) k_norm_rows(const bf16_t* __restrict__ x,
+                                                   const bf16_t* __restrict__ w,
+                                                   const bf16_t* __restrict__ b,
+                                                   bf16_t* __restrict__ out, int64_t rows,
+                                                   int64_t cols, float eps, bool rms) {
+    const int lane = threadIdx.x % kWave;
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * (blockDim.x / kWave) + threadIdx.x / kWave;
+    if (row >= rows) return;
+    const int nvec = static_cast<int>(cols / 8);
+    const bf16_t* xr = x + row * cols;
+    V8 v[NV];
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const int vi = lane + j * kWave;
+        v[j] = unpack_v8(vi < nvec ? *reinterpret_cast<const uint4*>(xr + vi * 8) : make_uint4(0, 0, 0, 0));
+    }
+    double mean = 0.0;
+    if (!rms) {
+        double s = 0.0;
+#pragma unroll
+        for (int j = 0; j < NV; ++j)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) s += static_cast<double>(v[j].f[e]);
+        mean = wave_sum(s) / static_cast<double>(cols);
+    }
+    double q = 0.0;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        if (lane + j * kWave < nvec) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const double d = static_cast<double>(v[j].f[e]) - mean;
+                q += d * d;
+            }
+        }
+    }
+    const double var = wave_sum(q) / static_cast<double>(cols);
+    const float inv = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(static_cast<float>(var), eps)));
+    const float fmean = static_cast<float>(mean);
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const int vi = lane + j * kWave;
+        if (vi >= nvec) continue;
+        V8 o;
+        const V8 wv = w ? load8(w + vi * 8) : V8{};
+        const V8 bv = b ? load8(b + vi * 8) : V8{};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            float t = __fmul_rn(__fsub_rn(v[j].f[e], fmean), inv);
+            if (w) t = __fmul_rn(t, wv.f[e]);
+            if (b) t = __fadd_rn(t, bv.f[e]);
+            o.f[e] = t;
+        }
+        store8(out + row * cols + vi * 8, o);
+    }
+}
+
 // ---- LayerNorm fused with the adaLN chunk and modulation (the hot row kernel) ---------------
 
 // Row statistics exactly as the oracle forms them: fp64 mean, fp64 sum of squared deviations,
@@ -455,6 +517,20 @@ __global__ void __launch_bounds__(256) k_activation(const T* __restrict__ x, T* 
 __global__ void __launch_bounds__(256) k_gelu_gated_rows(const bf16_t* __restrict__ in,
                                                          bf16_t* __restrict__ out, int64_t rows,
                                                          int64_t F) {
+    if (F % 8 == 0) {   // 16-byte vectors (the launcher checks alignment)
+        const int64_t per = F / 8, n = rows * per;
+        for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < n;
+             i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+            const int64_t r = i / per, j = (i - r * per) * 8;
+            const bf16_t* row = in + r * 2 * F;
+            const V8 h0 = load8(row + j), h1 = load8(row + F + j);
+            V8 o;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) o.f[e] = __fmul_rn(gelu_tanh(h0.f[e]), h1.f[e]);
+            store8(out + r * F + j, o);
+        }
+        return;
+    }
     const int64_t n = rows * F;
     for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < n;
          i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
@@ -531,6 +607,22 @@ void launch_norm(const void* x, const void* weight, const void* bias, void* out,
                                            static_cast<const float*>(bias),
                                            static_cast<float*>(out), rows, cols, eps, rms);
     } else {
+        const bool vec = cols % 8 == 0 && cols <= 8192 && (reinterpret_cast<uintptr_t>(x) & 15) == 0 &&
+                         (reinterpret_cast<uintptr_t>(out) & 15) == 0 &&
+                         (reinterpret_cast<uintptr_t>(weight) & 15) == 0 &&
+                         (reinterpret_cast<uintptr_t>(bias) & 15) == 0;
+        if (vec) {
+            const auto* xb = static_cast<const bf16_t*>(x);
+            const auto* wb = static_cast<const bf16_t*>(weight);
+            const auto* bb = static_cast<const bf16_t*>(bias);
+            auto* ob = static_cast<bf16_t*>(out);
+            if (cols <= 1024) k_norm_rows<2><<<grid, 256, 0, s>>>(xb, wb, bb, ob, rows, cols, eps, rms);
+            else if (cols <= 2048) k_norm_rows<4><<<grid, 256, 0, s>>>(xb, wb, bb, ob, rows, cols, eps, rms);
+            else if (cols <= 4096) k_norm_rows<8><<<grid, 256, 0, s>>>(xb, wb, bb, ob, rows, cols, eps, rms);
+            else k_norm_rows<16><<<grid, 256, 0, s>>>(xb, wb, bb, ob, rows, cols, eps, rms);
+            launch_check("norm");
+            return;
+        }
         k_norm<bf16_t><<<grid, 256, 0, s>>>(static_cast<const bf16_t*>(x),
                                             static_cast<const bf16_t*>(weight),
                                             static_cast<const bf16_t*>(bias),
@@ -668,7 +760,11 @@ void launch_activation(const void* x, void* out, int64_t numel, int kind, const 
 void launch_gelu_gated_rows(const bf16_t* in, bf16_t* out, int64_t rows, int64_t F, hipStream_t s) {
     if (rows * F == 0) return;
     ProfileScope ps(K_ELEMENTWISE, s, 6.0 * rows * F);
-    k_gelu_gated_rows<<<grid_for(rows * F), 256, 0, s>>>(in, out, rows, F);
+    const bool vec = F % 8 == 0 && (reinterpret_cast<uintptr_t>(in) & 15) == 0 &&
+                     (reinterpret_cast<uintptr_t>(out) & 15) == 0;
+    // the kernel takes the vector path whenever F % 8 == 0, which needs 16-byte aligned rows
+    require(vec || F % 8 != 0, "gated gelu: 16-byte aligned rows expected");
+    k_gelu_gated_rows<<<grid_for(vec ? rows * F / 8 : rows * F), 256, 0, s>>>(in, out, rows, F);
     launch_check("gated gelu");
 }
 
