@@ -164,6 +164,10 @@ SIGNATURES = {
     "bh_t5_encode": ([_V, _V, _V, _V], _I),
     "bh_t5_workspace_bytes": ([_V], _I64),
     "bh_t5_destroy": ([_V], None),
+    "bh_t5_weights_load": ([_V, _V, _V, _V], _I),
+    "bh_t5_weights_view": ([_V], _V),
+    "bh_t5_weights_bytes": ([_V], _I64),
+    "bh_t5_weights_free": ([_V], None),
     "bh_conv2d": ([_V, _V, _V, _V, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I, _V], _I),
     "bh_vae_weights_load": ([_V, _V, _V, ctypes.POINTER(_V)], _I),
     "bh_vae_weights_view": ([_V], _V),
@@ -321,6 +325,30 @@ class DitDeviceWeights:
             lib().bh_dit_weights_free(self._h)
             self._h = None
             self.weights = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class T5DeviceWeights:
+    """The T5 encoder's weights from a checkpoint's `text_encoder/` component, bf16 in one device
+    arena (bh_t5_weights_load). `table` is the address of the bh_t5_weights bh_t5_create takes."""
+
+    def __init__(self, checkpoint: Checkpoint, cfg, stream=None):
+        h = ctypes.c_void_p()
+        call("bh_t5_weights_load", checkpoint.handle, ctypes.byref(cfg), stream, ctypes.byref(h))
+        self._h = h
+        self.table = lib().bh_t5_weights_view(h)
+        self.bytes = lib().bh_t5_weights_bytes(h)
+
+    def free(self) -> None:
+        if self._h is not None:
+            lib().bh_t5_weights_free(self._h)
+            self._h = None
+            self.table = None
 
     def __del__(self):
         try:

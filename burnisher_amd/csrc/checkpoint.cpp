@@ -484,6 +484,18 @@ struct bh_dit_device_weights {
     }
 };
 
+struct bh_t5_device_weights {
+    void* arena = nullptr;
+    int64_t bytes = 0;
+    std::vector<std::string> names;
+    std::vector<const char*> cnames;
+    std::vector<const void*> ptrs;
+    bh_t5_weights view{};
+    ~bh_t5_device_weights() {
+        if (arena) (void)hipFree(arena);
+    }
+};
+
 struct bh_vae_device_weights {
     void* arena = nullptr;
     int64_t bytes = 0;
@@ -797,6 +809,39 @@ int bh_vae_weights_load(const bh_checkpoint* ck, const bh_vae_config* cfg, void*
         *out = w.release();
     });
 }
+
+int bh_t5_weights_load(const bh_checkpoint* ck, const bh_t5_config* cfg, void* stream,
+                       bh_t5_device_weights** out) {
+    return bh::guarded([&] {
+        bh::require(out != nullptr, "t5_weights_load: null output handle");
+        *out = nullptr;
+        bh::require(ck != nullptr && cfg != nullptr, "t5_weights_load: null checkpoint or config");
+        bh::require(cfg->num_layers >= 0 && cfg->d_model > 0 && cfg->d_ff > 0 && cfg->d_kv > 0 &&
+                        cfg->num_heads > 0 && cfg->vocab_size > 0 && cfg->num_buckets > 0,
+                    "t5_weights_load: configuration out of range");
+        auto w = std::make_unique<bh_t5_device_weights>();
+        const auto table = bh::t5_tensor_shapes(*cfg);
+        w->names.reserve(table.size());
+        w->ptrs.assign(table.size(), nullptr);
+        std::vector<bh::Want> want;
+        for (size_t i = 0; i < table.size(); ++i) {
+            w->names.push_back(table[i].first);
+            want.push_back({table[i].first, table[i].second, &w->ptrs[i]});
+        }
+        w->bytes = bh::upload_arena(*ck, want, static_cast<hipStream_t>(stream), &w->arena);
+        for (const auto& n : w->names) w->cnames.push_back(n.c_str());
+        w->view.count = static_cast<int>(w->names.size());
+        w->view.names = w->cnames.data();
+        w->view.tensors = w->ptrs.data();
+        *out = w.release();
+    });
+}
+
+const bh_t5_weights* bh_t5_weights_view(const bh_t5_device_weights* w) { return w ? &w->view : nullptr; }
+
+int64_t bh_t5_weights_bytes(const bh_t5_device_weights* w) { return w ? w->bytes : -1; }
+
+void bh_t5_weights_free(bh_t5_device_weights* w) { delete w; }
 
 const bh_vae_weights* bh_vae_weights_view(const bh_vae_device_weights* w) { return w ? &w->view : nullptr; }
 

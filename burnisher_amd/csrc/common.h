@@ -241,6 +241,8 @@ void launch_conv2d_nchw(const bf16_t* x, const bf16_t* w, const bf16_t* bias, bf
 void launch_group_norm_nchw(const bf16_t* x, const bf16_t* w, const bf16_t* b, bf16_t* out,
                             int64_t rows, int64_t cols, float eps, int64_t groups, int64_t channels,
                             hipStream_t s);
+// The T5 encoder's tensors with their checkpoint shapes (t5_engine.cpp).
+std::vector<std::pair<std::string, std::vector<int64_t>>> t5_tensor_shapes(const bh_t5_config& c);
 // The VAE decoder's tensors with their checkpoint shapes (vae_engine.cpp).
 std::vector<std::pair<std::string, std::vector<int64_t>>> vae_tensor_shapes(const bh_vae_config& c);
 // Keys per V^T row for the head_dim-512 attention (S rounded up to 32).

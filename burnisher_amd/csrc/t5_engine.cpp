@@ -94,20 +94,6 @@ struct bh_t5 {
 
 namespace {
 
-std::vector<std::string> t5_names(const bh_t5_config& c) {
-    std::vector<std::string> n{"shared.weight", "encoder.final_layer_norm.weight",
-                               "encoder.block.0.layer.0.SelfAttention.relative_attention_bias.weight"};
-    for (int i = 0; i < c.num_layers; ++i) {
-        for (const char* t : {"layer.0.layer_norm.weight", "layer.1.layer_norm.weight",
-                              "layer.0.SelfAttention.q.weight", "layer.0.SelfAttention.k.weight",
-                              "layer.0.SelfAttention.v.weight", "layer.0.SelfAttention.o.weight",
-                              "layer.1.DenseReluDense.wi_0.weight", "layer.1.DenseReluDense.wo.weight"})
-            n.push_back(blk(i, t));
-        if (c.gated) n.push_back(blk(i, "layer.1.DenseReluDense.wi_1.weight"));
-    }
-    return n;
-}
-
 void encode(bh_t5* e, const float* ids_in, bf16_t* out, hipStream_t s) {
     const bh_t5_config& c = e->cfg;
     const int64_t M = e->M, d = e->d, inner = e->inner, F = e->F;
@@ -168,6 +154,31 @@ void encode(bh_t5* e, const float* ids_in, bf16_t* out, hipStream_t s) {
 
 }  // namespace
 
+namespace bh {
+
+// The T5 part of declare_pixart_shapes (weights.cpp:226-244), in its order.
+std::vector<std::pair<std::string, std::vector<int64_t>>> t5_tensor_shapes(const bh_t5_config& c) {
+    const int64_t d = c.d_model, inner = static_cast<int64_t>(c.num_heads) * c.d_kv, f = c.d_ff;
+    std::vector<std::pair<std::string, std::vector<int64_t>>> t{
+        {"shared.weight", {c.vocab_size, d}},
+        {"encoder.final_layer_norm.weight", {d}},
+        {"encoder.block.0.layer.0.SelfAttention.relative_attention_bias.weight", {c.num_buckets, c.num_heads}}};
+    for (int i = 0; i < c.num_layers; ++i) {
+        t.push_back({blk(i, "layer.0.layer_norm.weight"), {d}});
+        t.push_back({blk(i, "layer.1.layer_norm.weight"), {d}});
+        for (const char* p : {"layer.0.SelfAttention.q.weight", "layer.0.SelfAttention.k.weight",
+                              "layer.0.SelfAttention.v.weight"})
+            t.push_back({blk(i, p), {inner, d}});
+        t.push_back({blk(i, "layer.0.SelfAttention.o.weight"), {d, inner}});
+        t.push_back({blk(i, "layer.1.DenseReluDense.wi_0.weight"), {f, d}});
+        if (c.gated) t.push_back({blk(i, "layer.1.DenseReluDense.wi_1.weight"), {f, d}});
+        t.push_back({blk(i, "layer.1.DenseReluDense.wo.weight"), {d, f}});
+    }
+    return t;
+}
+
+}  // namespace bh
+
 extern "C" {
 
 int bh_t5_relative_bucket(int relative_position, int num_buckets, int max_distance) {
@@ -203,7 +214,7 @@ int bh_t5_create(const bh_t5_config* cfg, const bh_t5_weights* w, int64_t batch,
             bh::require(w->names[i] && w->tensors[i], "t5_create: null weight name or tensor");
             e->w[w->names[i]] = static_cast<const bf16_t*>(w->tensors[i]);
         }
-        for (const auto& n : t5_names(c)) (void)e->at(n);   // all present
+        for (const auto& t : bh::t5_tensor_shapes(c)) (void)e->at(t.first);   // all present
         const int64_t M = e->M, d = e->d, inner = e->inner, F = e->F;
         e->x = e->alloc_bf(M * d);
         e->normed = e->alloc_bf(M * d);

@@ -29,7 +29,7 @@ import time
 import numpy as np
 
 from . import (BF16, DIT_FUSED, DIT_OPWISE, BurnisherError, Checkpoint, DitDeviceWeights,
-               VaeDeviceWeights, call, lib)
+               T5DeviceWeights, VaeDeviceWeights, call, lib)
 from .workload import PIXART_SIGMA, config_struct
 
 
@@ -191,6 +191,53 @@ def vae_decode(weights: str, latent_path: str, out_path: str, warmup: int = 1) -
             "output_stats": output_stats(host)}
 
 
+def t5_encode(weights: str, ids_path: str, out_path: str, warmup: int = 1,
+              config: dict | None = None) -> dict:
+    """Runs the t5-encode stage on token ids ([batch, seq] integers in a .npy, pad id 0); writes
+    the encoder output [batch, seq, d_model] as fp32 and returns the BURNISH_JSON record."""
+    import torch
+
+    from .t5 import T5_XXL, config_struct as t5_config_struct
+
+    spec = dict(T5_XXL, **(config or {}))
+    cfg = t5_config_struct(spec)
+    raw = np.load(ids_path, allow_pickle=False)
+    if raw.ndim != 2:
+        raise BurnisherError(f"t5-encode: expected ids [batch, seq], got {list(raw.shape)}")
+    ids = np.ascontiguousarray(raw, dtype=np.float32)
+    if not np.array_equal(ids, raw.astype(np.float64)):
+        raise BurnisherError("t5-encode: token ids must be integers exactly representable in fp32")
+    batch, seq = ids.shape
+    assert torch.cuda.is_available(), "the hip-gfx950 t5-encode needs an MI355X"
+    call("bh_init", 0)
+    out = torch.zeros((batch, seq, spec["d_model"]), dtype=torch.bfloat16, device="cuda")
+    stream = torch.cuda.current_stream().cuda_stream
+    with Checkpoint.component(weights, "text_encoder") as ck:
+        dw = T5DeviceWeights(ck, cfg, stream)
+    engine = ctypes.c_void_p()
+    try:
+        call("bh_t5_create", ctypes.byref(cfg), dw.table, batch, seq, ctypes.byref(engine))
+        for _ in range(max(0, warmup)):
+            call("bh_t5_encode", engine, ids.ctypes.data, out.data_ptr(), stream)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        call("bh_t5_encode", engine, ids.ctypes.data, out.data_ptr(), stream)
+        torch.cuda.synchronize()
+        secs = time.perf_counter() - t0
+        host = bf16_bits_to_f32(out.cpu().view(torch.int16).numpy().view(np.uint16))
+        free, total = torch.cuda.mem_get_info()
+        peak = int(total - free)
+    finally:
+        if engine.value:
+            lib().bh_t5_destroy(engine)
+        dw.free()
+    np.save(out_path, host.astype("<f4"), allow_pickle=False)
+    return {"metrics": {"latency_s": secs, "peak_vram_bytes": peak},
+            "effective": {"stage": "t5-encode", "dtype": "bf16", "impl": "hip-gfx950",
+                          "weights": "checkpoint", "device": "cuda"},
+            "output_stats": output_stats(host)}
+
+
 def main(argv=None) -> int:
     p = argparse.ArgumentParser(prog="python -m burnisher_amd.stage")
     sub = p.add_subparsers(dest="stage", required=True)
@@ -209,9 +256,17 @@ def main(argv=None) -> int:
     v.add_argument("--latent", required=True)
     v.add_argument("--out", required=True)
     v.add_argument("--warmup", type=int, default=1)
+    t = sub.add_parser("t5-encode", help="encode token ids with the T5 encoder")
+    t.add_argument("--weights", required=True, help="checkpoint directory (holds text_encoder/)")
+    t.add_argument("--ids", required=True, help=".npy of [batch, seq] integer token ids, pad 0")
+    t.add_argument("--out", required=True)
+    t.add_argument("--warmup", type=int, default=1)
+    t.add_argument("--config", default=None, help="JSON object of T5Config fields overriding XXL")
     a = p.parse_args(argv)
     try:
-        if a.stage == "vae-decode":
+        if a.stage == "t5-encode":
+            rec = t5_encode(a.weights, a.ids, a.out, a.warmup, json.loads(a.config) if a.config else None)
+        elif a.stage == "vae-decode":
             rec = vae_decode(a.weights, a.latent, a.out, a.warmup)
         else:
             rec = dit_step(a.weights, a.latent, a.caption, a.mask, a.out, a.timestep, a.layers,

@@ -511,6 +511,19 @@ int bh_t5_encode(bh_t5* e, const float* token_ids, void* out, void* stream);
 int64_t bh_t5_workspace_bytes(const bh_t5* e);
 void bh_t5_destroy(bh_t5* e);
 
+typedef struct bh_t5_device_weights bh_t5_device_weights;
+
+/* DeviceWeights over the T5 encoder's tensors (the `text_encoder/` component, sharded or not;
+ * names and shapes of declare_pixart_shapes' T5 part, weights.cpp:226-244): checked (present,
+ * shape, F32 or BF16) before anything is allocated, converted to bf16 on the host and copied into
+ * one device arena. Allocates. */
+int bh_t5_weights_load(const bh_checkpoint* ck, const bh_t5_config* cfg, void* stream,
+                       bh_t5_device_weights** out);
+/* The loaded weights as the table bh_t5_create takes; valid until bh_t5_weights_free. */
+const bh_t5_weights* bh_t5_weights_view(const bh_t5_device_weights* w);
+int64_t bh_t5_weights_bytes(const bh_t5_device_weights* w);
+void bh_t5_weights_free(bh_t5_device_weights* w);
+
 #ifdef __cplusplus
 }
 #endif

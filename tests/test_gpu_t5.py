@@ -122,3 +122,60 @@ def check(got, want, where):
 def test_encoder_matches_oracle(hip, cfg, batch, seq, lengths):
     wl = make_t5_workload(cfg, batch=batch, seq=seq, lengths=lengths, seed=9)
     check(device_encode(wl), stock_encode(wl), f"{cfg['d_model']}x{cfg['num_layers']} B{batch} S{seq}")
+
+
+def test_t5_weights_from_a_sharded_checkpoint_and_the_encode_stage(hip, tmp_path):
+    """The `text_encoder/` component split over two F32 shards with an index (as T5 XXL is
+    published): loaded weights give the same bytes as weights rounded on the host, and the
+    t5-encode stage meets the encoder gate."""
+    import contextlib
+    import io
+    import json
+
+    from burnisher_amd import stage
+    from burnisher_amd.t5 import t5_tensors
+    from helpers import to_bf16
+    from safetensors.numpy import save_file
+
+    cfg = dict(SMALL, num_layers=2)
+    rng = np.random.default_rng(31)
+    f32 = {}
+    for name, shape in t5_tensors(cfg).items():
+        std = 0.1 if "layer_norm" in name else (1.0 if name == "shared.weight" or "relative" in name
+                                                else 1 / np.sqrt(shape[1]))
+        v = (rng.standard_normal(shape) * std).astype(np.float32)
+        if "layer_norm" in name:
+            v += 1.0
+        f32[name] = v
+    d = tmp_path / "ckpt" / "text_encoder"
+    d.mkdir(parents=True)
+    names = list(f32)
+    halves = [names[: len(names) // 2], names[len(names) // 2:]]
+    weight_map = {}
+    for i, part in enumerate(halves):
+        fn = f"model-0000{i + 1}-of-00002.safetensors"
+        save_file({n: f32[n] for n in part}, str(d / fn))
+        weight_map.update({n: fn for n in part})
+    (d / "model.safetensors.index.json").write_text(json.dumps({"metadata": {}, "weight_map": weight_map}))
+    wl = make_t5_workload(cfg, batch=2, seq=9, lengths=[3, 9], seed=32)
+    wl.weights = {n: to_bf16(a) for n, a in f32.items()}
+    want = stock_encode(wl)
+    ids = tmp_path / "ids.npy"
+    np.save(ids, wl.ids.astype(np.int64))
+    out = tmp_path / "caption.npy"
+    buf = io.StringIO()
+    with contextlib.redirect_stdout(buf):
+        assert stage.main(["t5-encode", "--weights", str(tmp_path / "ckpt"), "--ids", str(ids), "--out",
+                           str(out), "--config", json.dumps(cfg)]) == 0
+    rec = json.loads(buf.getvalue().split("BURNISH_JSON: ")[1])
+    got = np.load(out)
+    assert got.shape == (2, 9, cfg["d_model"]) and rec["effective"]["stage"] == "t5-encode"
+    check(to_bf16(got), want, "t5-encode stage")
+    assert np.array_equal(to_bf16(got), device_encode(wl))
+    # a missing tensor is refused before anything is allocated
+    bad = tmp_path / "bad" / "text_encoder"
+    bad.mkdir(parents=True)
+    save_file({n: f32[n] for n in names if n != "encoder.final_layer_norm.weight"}, str(bad / "model.safetensors"))
+    with contextlib.redirect_stdout(io.StringIO()):
+        assert stage.main(["t5-encode", "--weights", str(tmp_path / "bad"), "--ids", str(ids), "--out",
+                           str(out), "--config", json.dumps(cfg)]) == 1
