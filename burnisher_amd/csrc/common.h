@@ -255,6 +255,14 @@ void launch_attention512(const bf16_t* q, const bf16_t* k, const bf16_t* v, bf16
 // small-M kernel or the reference-order kernel by shape.
 void launch_gemm_bf16(const bf16_t* a, const bf16_t* b, const bf16_t* bias, bf16_t* out,
                       int64_t m, int64_t n, int64_t k, const GemmEpilogue& ep, hipStream_t s);
+// Split-K for GEMMs with too few output tiles to fill the CUs: the number of K slices (1: none)
+// that keeps every slice's workgroups resident at once.
+int gemm_splitk_choice(int64_t m, int64_t n, int64_t k);
+// out = bf16(residual + bf16(A . B^T)) through `splits` fp32 partials (partial holds
+// splits * m * n floats) summed in slice order; out may alias residual.
+void launch_gemm_splitk_residual(const bf16_t* a, const bf16_t* b, float* partial, int splits,
+                                 const bf16_t* residual, bf16_t* out, int64_t m, int64_t n, int64_t k,
+                                 hipStream_t s);
 // Any dtype / layout, reference summation order: one thread per output (tests, fp32, [K,N] B).
 void launch_gemm_generic(const void* a, const void* b, const void* bias, void* out, int64_t m,
                          int64_t n, int64_t k, bool b_transposed, int act, bool f32,

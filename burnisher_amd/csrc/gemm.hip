@@ -54,6 +54,7 @@ enum EpiMode {
     EPI_ROW_ADD = 1,   // out = v' + row_add[row % period, n]
     EPI_RESIDUAL = 2,  // out = residual[row, n] + v'
     EPI_GATED = 3,     // out = residual[row, n] + gate[row / gate_rows, n] * v'
+    EPI_F32 = 4,       // (float*)out = acc: a split-K partial (no bias, activation or rounding)
 };                     // v' = round_mid ? bf16(v) : v
 
 struct Epi {
@@ -66,6 +67,7 @@ struct Epi {
     const bf16_t* gate;
     int64_t gate_rows;
     int64_t ld_out;
+    int64_t ld_k;               // row stride of A and B in elements (0: K); split-K reads a slice
     bf16_t* vt;                 // transposed V columns (see GemmEpilogue)
     int64_t vt_period, vt_col0, vt_seq, vt_ld;
     int vt_heads, vt_dim;
@@ -206,6 +208,7 @@ struct Operands {
     const bf16_t* B;
     int64_t M, N, K;
     ConvGeom cv;   // cv.in != null: A is the implicit im2col of a 3x3 convolution (see below)
+    int64_t ldk;   // row stride of A and B (K, or the full K of a split-K slice)
 };
 
 // This lane's source address (at k = 0) for each of the wave's 13 DMA items of a tile: items
@@ -222,12 +225,12 @@ __device__ __forceinline__ void dma_sources(const bf16_t* (&src)[kDmaItems], con
             const int row_in = (r * 4 + wave) * 8 + sub;
             const int c = slot ^ ((row_in >> 1) & 7);
             const int64_t row = min(m0 + a_row(row_in), o.M - 1);
-            src[r] = o.A + row * o.K + c * 8;
+            src[r] = o.A + row * o.ldk + c * 8;
         } else {
             const int row_in = min((r - BM / 32) * 4 + wave, BN / 8 - 1) * 8 + sub;
             const int c = slot ^ ((row_in >> 1) & 7);
             const int64_t row = min(n0 + b_col(row_in), o.N - 1);
-            src[r] = o.B + row * o.K + c * 8;
+            src[r] = o.B + row * o.ldk + c * 8;
         }
     }
 }
@@ -484,6 +487,19 @@ __device__ __forceinline__ void chunk_store(const f32x4_t (&acc)[kMT][kNT],
     constexpr int W = kW<P>;
     const int64_t n = n0 + chunk_col<P>(hi);
     if (n >= N) return;
+    if constexpr (MODE == EPI_F32) {
+#pragma unroll
+        for (int i = 0; i < kMT; ++i) {
+            const int64_t m = mb + i;
+            if (m >= M) continue;
+            float* dst = reinterpret_cast<float*>(out) + m * e.ld_out + n;
+#pragma unroll
+            for (int q = 0; q < W; q += 4)
+                *reinterpret_cast<f32x4_t*>(dst + q) = f32x4_t{acc_at<P>(acc, i, q), acc_at<P>(acc, i, q + 1),
+                                                              acc_at<P>(acc, i, q + 2), acc_at<P>(acc, i, q + 3)};
+        }
+        return;
+    }
     float b[W], gt[W];
     if (e.bias) unpack(in.bias, b);
     if (MODE == EPI_GATED && gate_uniform) unpack(in.gate, gt);
@@ -720,6 +736,12 @@ __device__ __forceinline__ void store_staged(const char* smem, const Epi& e, bf1
             const int r = rb + i * kRowStep;
             const int64_t m = m0 + r;
             if (r >= BM || m >= M) continue;
+            if constexpr (MODE == EPI_F32) {
+                float* dst = reinterpret_cast<float*>(out) + m * e.ld_out + n;
+                *reinterpret_cast<f32x4_t*>(dst) = f32x4_t{v[i][0], v[i][1], v[i][2], v[i][3]};
+                *reinterpret_cast<f32x4_t*>(dst + 4) = f32x4_t{v[i][4], v[i][5], v[i][6], v[i][7]};
+                continue;
+            }
             float x[8], t[8];
 #pragma unroll
             for (int q = 0; q < 8; ++q) x[q] = act_fast<ACT>(e.bias ? __fadd_rn(v[i][q], bias[q]) : v[i][q]);
@@ -795,8 +817,14 @@ k_gemm_tn(const bf16_t* __restrict__ A, const bf16_t* __restrict__ B, bf16_t* ou
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     const int KT = static_cast<int>(K / BK);
+    const int64_t ldk = e.ld_k > 0 ? e.ld_k : K;
+    if (MODE == EPI_F32 && gridDim.y > 1) {   // split-K: slice blockIdx.y of K, its own partial
+        A += static_cast<int64_t>(blockIdx.y) * K;
+        B += static_cast<int64_t>(blockIdx.y) * K;
+        out += static_cast<int64_t>(blockIdx.y) * M * e.ld_out * 2;   // float elements
+    }
     if (wave >= kConsumers) {
-        produce<CONV>(smem, Operands{A, B, M, N, K, cv}, KT, my_tiles, tiles_m, tiles_n, group_m,
+        produce<CONV>(smem, Operands{A, B, M, N, K, cv, ldk}, KT, my_tiles, tiles_m, tiles_n, group_m,
                       wave - kConsumers, lane);
     } else {
         consume<ACT, MODE>(smem, e, out, M, N, KT, my_tiles, tiles_m, tiles_n, group_m, wave, lane);
@@ -999,6 +1027,49 @@ void launch_tn(const bf16_t* a, const bf16_t* b, bf16_t* out, int64_t m, int64_t
     k_gemm_tn<ACT, MODE, CONV><<<grid, kWgThreads, 0, s>>>(a, b, out, m, n, k, e, tiles_m, tiles_n, 4, cv);
 }
 
+// Split-K partials: `splits` slices of K in one launch (grid.y = slice), each persistent
+// workgroup set over the same output tiles, slice s writing fp32 partial[s][m][n].
+void launch_tn_splitk(const bf16_t* a, const bf16_t* b, float* partial, int64_t m, int64_t n, int64_t k,
+                      int splits, hipStream_t s) {
+    const int tiles_m = static_cast<int>((m + BM - 1) / BM);
+    const int tiles_n = static_cast<int>((n + BN - 1) / BN);
+    const int tiles = tiles_m * tiles_n;
+    const int grid = max(1, min(tiles, device_cus() / splits));
+    Epi e{};
+    e.row_add_period = 1;
+    e.gate_rows = 1;
+    e.ld_out = n;
+    e.ld_k = k;
+    e.vt_dim = 72;
+    k_gemm_tn<0, EPI_F32, false><<<dim3(grid, splits), kWgThreads, 0, s>>>(
+        a, b, reinterpret_cast<bf16_t*>(partial), m, n, k / splits, e, tiles_m, tiles_n, 4, ConvGeom{});
+}
+
+// out[m, n] = bf16(residual[m, n] + bf16(sum_s partial[s][m][n])), the slices summed in order.
+__global__ void __launch_bounds__(256) k_splitk_residual(const float* __restrict__ partial, int splits,
+                                                         const bf16_t* residual, bf16_t* out, int64_t mn) {
+    for (int64_t i = (blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x) * 4; i < mn;
+         i += static_cast<int64_t>(gridDim.x) * blockDim.x * 4) {
+        f32x4_t acc = *reinterpret_cast<const f32x4_t*>(partial + i);
+        for (int sp = 1; sp < splits; ++sp) {
+            const f32x4_t p = *reinterpret_cast<const f32x4_t*>(partial + sp * mn + i);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) acc[q] = __fadd_rn(acc[q], p[q]);
+        }
+        const uint2 r = *reinterpret_cast<const uint2*>(residual + i);
+        const float res[4] = {__uint_as_float(r.x << 16), __uint_as_float(r.x & 0xffff0000u),
+                              __uint_as_float(r.y << 16), __uint_as_float(r.y & 0xffff0000u)};
+        uint32_t o[2];
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            const float lo = __fadd_rn(res[2 * q], round_bf16(acc[2 * q]));
+            const float hi = __fadd_rn(res[2 * q + 1], round_bf16(acc[2 * q + 1]));
+            o[q] = static_cast<uint32_t>(f2bf(lo)) | (static_cast<uint32_t>(f2bf(hi)) << 16);
+        }
+        *reinterpret_cast<uint2*>(out + i) = make_uint2(o[0], o[1]);
+    }
+}
+
 template <int ACT>
 void launch_tn_mode(int mode, const bf16_t* a, const bf16_t* b, bf16_t* out, int64_t m, int64_t n,
                     int64_t k, const Epi& e, hipStream_t s) {
@@ -1036,7 +1107,7 @@ void launch_gemm_bf16(const bf16_t* a, const bf16_t* b, const bf16_t* bias, bf16
     if (m == 0 || n == 0) return;
     require(!ep.gate || ep.residual, "gemm: a gate needs a residual");
     Epi e{bias, ep.act, ep.round_mid, ep.row_add, ep.row_add_period > 0 ? ep.row_add_period : 1,
-          ep.residual, ep.gate, ep.gate_rows > 0 ? ep.gate_rows : 1, ep.ld_out > 0 ? ep.ld_out : n,
+          ep.residual, ep.gate, ep.gate_rows > 0 ? ep.gate_rows : 1, ep.ld_out > 0 ? ep.ld_out : n, 0,
           ep.vt, ep.vt_period, ep.vt_col0, ep.vt_seq, ep.vt_ld, ep.vt_heads, ep.vt_dim};
     if (ep.vt) {
         require(!ep.residual && !ep.row_add && !ep.round_mid,
@@ -1107,7 +1178,7 @@ void launch_conv3x3_bf16(const ConvGeom& cv, const bf16_t* wr, const bf16_t* bia
     require(static_cast<int64_t>(cv.in_h) * cv.in_w * cv.c_in < (int64_t{1} << 31),
             "conv3x3: input too large for 32-bit pixel offsets");
     Epi e{bias, ep.act, ep.round_mid, nullptr, 1, ep.residual, nullptr, 1,
-          ep.ld_out > 0 ? ep.ld_out : c_out, nullptr, 0, 0, 0, 0, 0, 72};
+          ep.ld_out > 0 ? ep.ld_out : c_out, 0, nullptr, 0, 0, 0, 0, 0, 72};
     require(ep.act == 0, "conv3x3: no activation epilogue (the decoder's SiLU follows a GroupNorm)");
     ProfileScope ps(K_GEMM, s, 2.0 * static_cast<double>(m) * c_out * k);
     if (ep.residual) launch_tn<0, EPI_RESIDUAL, true>(cv.in, wr, out, m, c_out, k, e, s, cv);
@@ -1115,4 +1186,35 @@ void launch_conv3x3_bf16(const ConvGeom& cv, const bf16_t* wr, const bf16_t* bia
     launch_check("conv3x3 (mfma)");
 }
 
+int gemm_splitk_choice(int64_t m, int64_t n, int64_t k) {
+    if (m <= kGemvMaxM || n % 8 != 0 || k % BK != 0) return 1;
+    const int64_t tiles = ((m + BM - 1) / BM) * ((n + BN - 1) / BN);
+    const int cus = device_cus();
+    int best = 1;
+    for (int sp = 2; sp <= 4; ++sp)
+        if (tiles * sp <= cus && k % (BK * sp) == 0 && k / sp >= 4 * BK) best = sp;
+    return best;
+}
+
+void launch_gemm_splitk_residual(const bf16_t* a, const bf16_t* b, float* partial, int splits,
+                                 const bf16_t* residual, bf16_t* out, int64_t m, int64_t n, int64_t k,
+                                 hipStream_t s) {
+    if (m == 0 || n == 0) return;
+    require(splits >= 2 && splits <= 8 && k % (BK * splits) == 0 && n % 8 == 0 && m > kGemvMaxM,
+            "gemm split-K: K must split into whole 64-wide k-tiles, N % 8 == 0");
+    require(aligned(a, 16) && aligned(b, 16) && aligned(partial, 16) && aligned(residual, 8) && aligned(out, 8),
+            "gemm split-K: operands must be 16-byte aligned");
+    {
+        ProfileScope ps(K_GEMM, s, 2.0 * static_cast<double>(m) * n * k);
+        launch_tn_splitk(a, b, partial, m, n, k, splits, s);
+        launch_check("gemm (split-K partials)");
+    }
+    ProfileScope ps(K_ELEMENTWISE, s, static_cast<double>(m) * n * (4.0 * splits + 4.0));
+    const int64_t mn = m * n;
+    const int64_t blocks = std::min<int64_t>((mn / 4 + 255) / 256, 8192);
+    k_splitk_residual<<<static_cast<int>(blocks), 256, 0, s>>>(partial, splits, residual, out, mn);
+    launch_check("gemm (split-K reduce)");
+}
+
 }  // namespace bh
+

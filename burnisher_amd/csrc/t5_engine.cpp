@@ -60,6 +60,8 @@ struct bh_t5 {
            *hact = nullptr, *bias = nullptr, *mask = nullptr;
     float* ids = nullptr;
     int* bucket = nullptr;
+    float* partial = nullptr;        // split-K partials of the two output projections
+    int split_o = 1, split_wo = 1;
     float* ids_host = nullptr;       // pinned staging of one call's ids
     bf16_t* mask_host = nullptr;     // and its key mask
     hipEvent_t staged = nullptr;
@@ -134,8 +136,12 @@ void encode(bh_t5* e, const float* ids_in, bf16_t* out, hipStream_t s) {
         bh::launch_gemm_bf16(e->normed, e->qkv_w[l], nullptr, e->qkv, M, 3 * inner, d, plain, s);
         bh::launch_attention_bf16(e->qkv, e->qkv + inner, e->qkv + 2 * inner, e->ctx, sh, e->mask, false, s,
                                   e->bias);
-        bh::launch_gemm_bf16(e->ctx, e->at(blk(l, "layer.0.SelfAttention.o.weight")), nullptr, e->x, M, d,
-                             inner, residual, s);
+        if (e->split_o > 1)
+            bh::launch_gemm_splitk_residual(e->ctx, e->at(blk(l, "layer.0.SelfAttention.o.weight")), e->partial,
+                                            e->split_o, e->x, e->x, M, d, inner, s);
+        else
+            bh::launch_gemm_bf16(e->ctx, e->at(blk(l, "layer.0.SelfAttention.o.weight")), nullptr, e->x, M, d,
+                                 inner, residual, s);
         bh::launch_norm(e->x, e->at(blk(l, "layer.1.layer_norm.weight")), nullptr, e->normed, M, d, eps,
                         true, false, s);
         if (c.gated) {
@@ -146,8 +152,12 @@ void encode(bh_t5* e, const float* ids_in, bf16_t* out, hipStream_t s) {
                                  e->h01, M, F, d, plain, s);
             bh::launch_activation(e->h01, e->hact, M * F, BH_EPI_GELU, nullptr, false, s);
         }
-        bh::launch_gemm_bf16(e->hact, e->at(blk(l, "layer.1.DenseReluDense.wo.weight")), nullptr, e->x, M, d,
-                             F, residual, s);
+        if (e->split_wo > 1)
+            bh::launch_gemm_splitk_residual(e->hact, e->at(blk(l, "layer.1.DenseReluDense.wo.weight")),
+                                            e->partial, e->split_wo, e->x, e->x, M, d, F, s);
+        else
+            bh::launch_gemm_bf16(e->hact, e->at(blk(l, "layer.1.DenseReluDense.wo.weight")), nullptr, e->x, M, d,
+                                 F, residual, s);
     }
     bh::launch_norm(e->x, e->at("encoder.final_layer_norm.weight"), nullptr, out, M, d, eps, true, false, s);
 }
@@ -226,6 +236,12 @@ int bh_t5_create(const bh_t5_config* cfg, const bh_t5_weights* w, int64_t batch,
         e->mask = e->alloc_bf(M);
         e->ids = static_cast<float*>(e->alloc(M * 4));
         e->bucket = static_cast<int*>(e->alloc((2 * e->S - 1) * 4));
+        // the two d_model-wide output projections have the fewest output tiles: split their K
+        // when that fills more CUs (fp32 partials summed in a fixed order, then the residual)
+        e->split_o = bh::gemm_splitk_choice(M, d, inner);
+        e->split_wo = bh::gemm_splitk_choice(M, d, F);
+        if (std::max(e->split_o, e->split_wo) > 1)
+            e->partial = static_cast<float*>(e->alloc(std::max(e->split_o, e->split_wo) * M * d * 4));
         std::vector<int> bucket(static_cast<size_t>(2 * e->S - 1));
         for (int64_t r = -(e->S - 1); r <= e->S - 1; ++r)
             bucket[r + e->S - 1] = relative_bucket(static_cast<int>(r), c.num_buckets, kMaxDistance);
