@@ -85,13 +85,12 @@ __global__ void __launch_bounds__(kThreads, 1) k_flash(AttnArgs a) {
     // ---- key-block skipping flags (only with a mask) ----
     const bool use_flags = a.mask != nullptr && nblk <= kMaxFlagBlocks;
     if (use_flags) {
-        for (int blk = tid; blk < nblk; blk += kThreads) {
-            int ok = 0;
-            const int64_t end = min(static_cast<int64_t>(blk + 1) * kKvBlk, a.Skv);
-            for (int64_t j = static_cast<int64_t>(blk) * kKvBlk; j < end; ++j)
-                ok |= mask_at(a.mask, a.mask_f32, b * a.Skv + j) != 0.0f;
-            blk_ok[blk] = ok;
-        }
+        // one key per thread (a serial scan per block was 64 dependent loads per thread); threads
+        // that find an unmasked key all store the same 1, so the race is benign
+        for (int blk = tid; blk < nblk; blk += kThreads) blk_ok[blk] = 0;
+        __syncthreads();
+        for (int64_t j = tid; j < a.Skv; j += kThreads)
+            if (mask_at(a.mask, a.mask_f32, b * a.Skv + j) != 0.0f) blk_ok[j / kKvBlk] = 1;
     }
     // V^T rows at and beyond head_dim stay zero for the whole kernel (both stages).
     for (int s = 0; s < 2; ++s) {
