@@ -141,10 +141,12 @@ __global__ void __launch_bounds__(256) k_norm_rows(const bf16_t* __restrict__ x,
     const int nvec = static_cast<int>(cols / 8);
     const bf16_t* xr = x + row * cols;
     V8 v[NV];
+    uint4 wraw[NV];   // the weight vectors, loaded with the row so their latency overlaps it
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
         const int vi = lane + j * kWave;
         v[j] = unpack_v8(vi < nvec ? *reinterpret_cast<const uint4*>(xr + vi * 8) : make_uint4(0, 0, 0, 0));
+        wraw[j] = (w && vi < nvec) ? *reinterpret_cast<const uint4*>(w + vi * 8) : make_uint4(0, 0, 0, 0);
     }
     double mean = 0.0;
     if (!rms) {
@@ -174,7 +176,7 @@ __global__ void __launch_bounds__(256) k_norm_rows(const bf16_t* __restrict__ x,
         const int vi = lane + j * kWave;
         if (vi >= nvec) continue;
         V8 o;
-        const V8 wv = w ? load8(w + vi * 8) : V8{};
+        const V8 wv = unpack_v8(wraw[j]);
         const V8 bv = b ? load8(b + vi * 8) : V8{};
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
