@@ -521,7 +521,7 @@ def main() -> int:
         return t5(args)
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
-              "(the dit-step would shard on the CFG batch, see DESIGN.md)", file=sys.stderr)
+              "(the dit-step would shard on the CFG batch: one batch row per GPU)", file=sys.stderr)
         return 2
     import numpy as np
     import torch

@@ -16,7 +16,7 @@
  *
  * The per-op entry points below are one-to-one with the reference's op surface
  * (/root/reference/include/burnisher/ops.h) so a reference `register_impl<Args>` lambda can
- * forward an Args struct field by field; INTEGRATION.md shows that adapter.
+ * forward an Args struct field by field.
  */
 #ifndef BURNISHER_HIP_H
 #define BURNISHER_HIP_H
