@@ -486,8 +486,8 @@ def t5(args) -> int:
     return 0
 
 
-def cpu_baseline(wl, threads: int) -> dict:
-    """The stock oracle's whole dit-step (all 28 blocks) on this host, timed once."""
+def stock_step(wl, threads: int):
+    """The stock oracle's dit-step (all of wl's blocks) on this host: (output bf16 bits, seconds)."""
     import numpy as np
     import oracle
     from burnisher_amd.workload import config_struct
@@ -499,12 +499,137 @@ def cpu_baseline(wl, threads: int) -> dict:
     oracle.call(oracle.stock(), "stock_dit_forward", ctypes.byref(cfg), ctypes.byref(w),
                 wl.batch, wl.latent_hw, wl.caption_len, wl.latent.ctypes.data, wl.timestep,
                 wl.caption.ctypes.data, wl.mask.ctypes.data, 0, out.ctypes.data, threads, -1)
-    step_s = time.perf_counter() - t0
-    log(f"cpu baseline: one full dit-step in {step_s:.2f} s")
-    return {"value": round(step_s * 1e3, 1), "unit": "ms", "cores": threads, "kind": "port",
-            "sample": (f"one whole dit-step of the stock oracle (oracle/stock.cpp, the reference's "
-                       f"stock numerics) at the same {wl.latent_hw * 8}px B=2 workload and seeds, "
-                       f"{threads} threads, not extrapolated")}
+    return out, time.perf_counter() - t0
+
+
+def parity(got, want) -> dict:
+    """max-abs, relative L2 and cosine of the device output against the oracle's, and the
+    configs/tolerance.json dit_step gate they are held to."""
+    import numpy as np
+
+    g = (got.astype(np.uint32) << 16).view(np.float32).astype(np.float64).ravel()
+    r = (want.astype(np.uint32) << 16).view(np.float32).astype(np.float64).ravel()
+    gate = json.loads((ROOT / "configs" / "tolerance.json").read_text())["dit_step"]
+    d = g - r
+    res = {"max_abs": float(np.max(np.abs(d))),
+           "rel_l2": float(np.linalg.norm(d) / np.linalg.norm(r)),
+           "cosine": float(np.dot(g, r) / (np.linalg.norm(g) * np.linalg.norm(r))),
+           "finite": bool(np.all(np.isfinite(g)))}
+    res["gate"] = {k: gate[k] for k in ("max_abs", "rel_l2", "cosine")}
+    res["pass"] = (res["finite"] and res["max_abs"] <= gate["max_abs"] and
+                   res["rel_l2"] <= gate["rel_l2"] and res["cosine"] >= gate["cosine"])
+    return res
+
+
+def timed_steps(step, stream, steps: int) -> float:
+    """ms per step over `steps` back-to-back steps between two HIP events on the stream."""
+    import torch
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    with torch.cuda.stream(stream):
+        start.record(stream)
+        for _ in range(steps):
+            step()
+        stop.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(stop) / steps
+
+
+def synced_median(step, stream, iters: int) -> float:
+    """The reference's method (burnisher_main.cpp:451-464): each iteration timed on the host
+    clock from launch to device synchronisation; the median, in ms."""
+    import torch
+    times = []
+    for _ in range(iters):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        with torch.cuda.stream(stream):
+            step()
+        torch.cuda.synchronize()
+        times.append((time.perf_counter() - t0) * 1e3)
+    times.sort()
+    n = len(times)
+    return times[n // 2] if n % 2 else 0.5 * (times[n // 2 - 1] + times[n // 2])
+
+
+def device_probe() -> dict:
+    """What this device sustains (bh_probe_device: a register-only MFMA loop with the shader clock
+    it holds, and a 1 GiB device copy), plus this library's GEMM at 8192^3 (the reference's
+    `probe` times a vendor GEMM of that size, device.cu:284-318)."""
+    import torch
+
+    import burnisher_amd as bh
+
+    src = torch.ones(1 << 29, device="cuda", dtype=torch.bfloat16)   # 1 GiB
+    dst = torch.empty_like(src)
+    res = bh.ProbeResult()
+    bh.call("bh_probe_device", src.data_ptr(), dst.data_ptr(), src.numel() * 2, ctypes.byref(res))
+    del src, dst
+    out = res.as_dict()
+    n = 8192
+    gen = torch.Generator(device="cuda").manual_seed(1)
+    a = torch.randn(n, n, device="cuda", generator=gen).bfloat16()
+    b = (torch.randn(n, n, device="cuda", generator=gen) * 0.02).bfloat16()
+    c = torch.empty(n, n, device="cuda", dtype=torch.bfloat16)
+    launch = lambda: bh.call("bh_gemm", a.data_ptr(), b.data_ptr(), None, c.data_ptr(), n, n, n, 1, 0,
+                             bh.BF16, None)
+    launch()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(5):
+        launch()
+    e1.record()
+    torch.cuda.synchronize()
+    out["gemm_8192_tflops"] = round(2.0 * n ** 3 / (e0.elapsed_time(e1) / 5 * 1e-3) / 1e12, 1)
+    del a, b, c
+    torch.cuda.empty_cache()
+    return out
+
+
+class Engine:
+    """One bh_dit engine over device weights shared between engines, with its own inputs."""
+
+    def __init__(self, wl, top, blocks, mode, stream):
+        import numpy as np
+        import torch
+
+        import burnisher_amd as bh
+        from burnisher_amd.workload import config_struct
+
+        self.bh, self.wl, self.stream = bh, wl, stream
+        t = lambda a: torch.from_numpy(a.view(np.int16)).view(torch.bfloat16).cuda()
+        self.latent, self.caption = t(wl.latent), t(wl.caption)
+        self.mask = torch.from_numpy(wl.mask).cuda()
+        self.cfg = config_struct(wl.cfg)
+        self.w, self._keep = wl.weight_struct(top, blocks)
+        self.handle = ctypes.c_void_p()
+        bh.call("bh_dit_create", ctypes.byref(self.cfg), ctypes.byref(self.w), wl.batch,
+                wl.latent_hw, wl.caption_len, mode, ctypes.byref(self.handle))
+        self.out = torch.zeros((wl.batch, self.cfg.out_channels, wl.latent_hw, wl.latent_hw),
+                               dtype=torch.bfloat16, device="cuda")
+
+    def step(self):
+        self.bh.call("bh_dit_forward", self.handle, self.latent.data_ptr(), self.wl.timestep,
+                     self.caption.data_ptr(), self.mask.data_ptr(), self.bh.F32,
+                     self.out.data_ptr(), self.stream.cuda_stream)
+
+    def workspace(self) -> int:
+        return int(self.bh.lib().bh_dit_workspace_bytes(self.handle))
+
+    def input_bytes(self) -> int:
+        return sum(t.numel() * t.element_size() for t in (self.latent, self.caption, self.mask, self.out))
+
+    def output(self):
+        import numpy as np
+        import torch
+        torch.cuda.synchronize()
+        return self.out.cpu().view(torch.int16).numpy().view(np.uint16).copy()
+
+    def close(self):
+        if self.handle:
+            self.bh.lib().bh_dit_destroy(self.handle)
+            self.handle = ctypes.c_void_p()
 
 
 def main() -> int:
@@ -527,30 +652,30 @@ def main() -> int:
     import torch
 
     import burnisher_amd as bh
-    from burnisher_amd.workload import PIXART_SIGMA, config_struct, dit_step_flops, make_workload
+    from burnisher_amd.workload import PIXART_SIGMA, dit_step_flops, make_workload
 
     bh.check(bh.lib().bh_init(0), "bh_init")
+    probed = device_probe()
+    log(f"device probe: {json.dumps(probed)}")
     hw = HW[args.resolution]
     log(f"generating the {args.resolution}px workload (seeded synthetic bf16)")
     wl = make_workload(PIXART_SIGMA, batch=args.batch, latent_hw=hw, caption_len=args.caption_len)
-    top, blocks, latent, caption, mask = wl.to_device()
-    cfg = config_struct(wl.cfg)
-    w, keep = wl.weight_struct(top, blocks)
-    handle = ctypes.c_void_p()
-    bh.call("bh_dit_create", ctypes.byref(cfg), ctypes.byref(w), wl.batch, hw, wl.caption_len,
-            bh.DIT_FUSED, ctypes.byref(handle))
-    out = torch.zeros((wl.batch, cfg.out_channels, hw, hw), dtype=torch.bfloat16, device="cuda")
+    free0 = torch.cuda.mem_get_info()[0]
+    t = lambda a: torch.from_numpy(a.view(np.int16)).view(torch.bfloat16).cuda()
+    top = {k: t(v) for k, v in wl.top.items()}
+    blocks = [{k: t(v) for k, v in b.items()} for b in wl.blocks]
+    weight_bytes = sum(x.numel() * 2 for x in top.values()) + \
+        sum(x.numel() * 2 for b in blocks for x in b.values())
     stream = torch.cuda.Stream()
-    sp = stream.cuda_stream
-
-    def step():
-        bh.call("bh_dit_forward", handle, latent.data_ptr(), wl.timestep, caption.data_ptr(),
-                mask.data_ptr(), bh.F32, out.data_ptr(), sp)
+    eng = Engine(wl, top, blocks, bh.DIT_FUSED, stream)
+    torch.cuda.synchronize()
+    driver_used = free0 - torch.cuda.mem_get_info()[0]
+    peak_bytes = weight_bytes + eng.input_bytes() + eng.workspace()
 
     flops = dit_step_flops(wl.cfg, batch=wl.batch, latent_hw=hw, caption_len=wl.caption_len)
     with torch.cuda.stream(stream):
         for _ in range(max(1, args.warmup)):
-            step()
+            eng.step()
     torch.cuda.synchronize()
     log("warmup done")
 
@@ -558,7 +683,7 @@ def main() -> int:
     classes = {name: i for i, name in enumerate(bh.KERNEL_CLASSES)}
     bh.call("bh_profile_enable", (1 << len(classes)) - 1)
     with torch.cuda.stream(stream):
-        step()
+        eng.step()
     torch.cuda.synchronize()
     breakdown = {}
     for name, i in classes.items():
@@ -573,16 +698,7 @@ def main() -> int:
 
     # the timed region: K steps, HIP events around the dominant kernel's launches
     bh.call("bh_profile_enable", 1 << classes[dominant])
-    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    with torch.cuda.stream(stream):
-        start.record(stream)
-        for _ in range(args.steps):
-            step()
-        stop.record(stream)
-    torch.cuda.synchronize()
-    total_ms = start.elapsed_time(stop)
-    ms_per_step = total_ms / args.steps
+    ms_per_step = timed_steps(eng.step, stream, args.steps)
     dms, dn, dwork = ctypes.c_double(), ctypes.c_int64(), ctypes.c_double()
     bh.call("bh_profile_read", classes[dominant], ctypes.byref(dms), ctypes.byref(dn), ctypes.byref(dwork))
     bh.call("bh_profile_enable", 0)
@@ -591,10 +707,12 @@ def main() -> int:
     achieved = work_per_launch / (avg_launch_ms * 1e-3) / 1e12
     log(f"timed {args.steps} steps: {ms_per_step:.3f} ms/step; {dominant}: {dn.value} launches, "
         f"{avg_launch_ms * 1e3:.1f} us avg, {achieved:.1f} TFLOP/s")
+    got = eng.output()
 
-    # parity sanity on the timed output: finite and not constant
-    res = out.float()
-    assert torch.isfinite(res).all() and res.std() > 1e-3, "degenerate dit-step output"
+    # the same steps with no event inside a step, and the reference's synchronised median
+    plain_ms = timed_steps(eng.step, stream, args.steps)
+    median_ms = synced_median(eng.step, stream, max(5, min(args.steps, 20)))
+    log(f"profiler off: {plain_ms:.3f} ms/step; synchronised median {median_ms:.3f} ms")
 
     step_tflops = flops["total"] / (ms_per_step * 1e-3) / 1e12
     line = {
@@ -612,14 +730,24 @@ def main() -> int:
                              "on an RTX 5090 (eval/cells/BG-1/reference.json:28); lower is better",
         "dtype": "bf16",
         "data": "synthetic: seeded N(0,0.02) bf16 weights, N(0,1) latent and caption, timestep 500",
-        "config": {"workload": f"PixArt-Sigma dit-step {args.resolution}px, batch 2 (CFG), "
+        "config": {"workload": f"PixArt-Sigma dit-step {args.resolution}px, batch {wl.batch} (CFG), "
                                f"caption {wl.caption_len}, 28 blocks",
                    "resolution": args.resolution, "latent": [wl.batch, 4, hw, hw],
                    "tokens": wl.tokens, "batch": wl.batch, "caption_len": wl.caption_len,
                    "layers": wl.cfg["num_layers"], "engine": "bh_dit_forward (fused plan)"},
+        "timing": {"ms_per_step_events": round(ms_per_step, 4),
+                   "ms_per_step_profiler_off": round(plain_ms, 4),
+                   "sync_median_ms": round(median_ms, 4),
+                   "basis": "value: K back-to-back steps between HIP events on the engine's stream, "
+                            "with HIP events also around each launch of the dominant kernel (the "
+                            "roofline's live measurement); profiler_off: the same with no event "
+                            "inside a step; sync_median: the reference's method, each step timed "
+                            "on the host clock from launch to device synchronisation, median"},
         "roofline": {"bound": "mfma", "kernel": dominant,
                      "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+                     "probed_peak": probed["mfma_tflops"],
+                     "probed_frac": round(achieved / probed["mfma_tflops"], 4),
                      "traffic": traffic_bytes(dominant, args.resolution),
                      "traffic_basis": "HBM bytes per launch: rocprofv3 FETCH_SIZE (x2.000) + "
                                       "WRITE_SIZE (x1.000), each scaled by a 256 MiB copy; "
@@ -628,16 +756,87 @@ def main() -> int:
                      "flop_per_launch": work_per_launch},
         "step": {"flop": flops["total"], "tflops": round(step_tflops, 2),
                  "mfma_frac": round(step_tflops / PEAK_BF16_TFLOPS, 4),
-                 "ceiling_ms": round(flops["total"] / (PEAK_BF16_TFLOPS * 1e12) * 1e3, 3)},
+                 "ceiling_ms": round(flops["total"] / (PEAK_BF16_TFLOPS * 1e12) * 1e3, 3),
+                 "probed_frac": round(step_tflops / probed["mfma_tflops"], 4)},
+        "probe": probed,
+        "memory": {"peak_device_bytes": int(peak_bytes), "weights_bytes": int(weight_bytes),
+                   "engine_workspace_bytes": eng.workspace(),
+                   "driver_used_bytes": int(driver_used),
+                   "basis": "peak_device_bytes: what the runtime asked for (weights + inputs + "
+                            "output + the engine's intermediates, all allocated before the first "
+                            "forward; forward allocates nothing), as the reference's "
+                            "device::peak_allocated_bytes counts it (device.h:31-35); "
+                            "driver_used_bytes: the drop in the driver's free memory over the same "
+                            "allocations, allocator granularity included"},
         "kernels": breakdown,
     }
-    bh.lib().bh_dit_destroy(handle)
+    eng.close()
+
+    # the op-by-op plan (the registry drop-in path: one bh_* op per reference op), same steps
+    op = Engine(wl, top, blocks, bh.DIT_OPWISE, stream)
+    with torch.cuda.stream(stream):
+        op.step()
+    opwise_ms = timed_steps(op.step, stream, max(3, args.steps // 2))
+    line["opwise_ms_per_step"] = round(opwise_ms, 4)
+    opwise_out = op.output()
+    op.close()
+    log(f"op-by-op plan: {opwise_ms:.3f} ms/step")
+    line["opwise_equals_fused"] = bool(np.array_equal(opwise_out, got))
+
+    # the other full-step configs (BASELINE configs[2] and [4]) on the same device weights
+    others = {}
+    for res in (512, 2048):
+        if res == args.resolution:
+            continue
+        owl = make_workload(PIXART_SIGMA, batch=wl.batch, latent_hw=HW[res], caption_len=wl.caption_len,
+                            layers=0)
+        owl.cfg["num_layers"] = wl.cfg["num_layers"]
+        owl.top, owl.blocks = wl.top, wl.blocks
+        oe = Engine(owl, top, blocks, bh.DIT_FUSED, stream)
+        with torch.cuda.stream(stream):
+            oe.step()
+        o_ms = timed_steps(oe.step, stream, 5 if res > 1024 else 10)
+        of = dit_step_flops(owl.cfg, batch=owl.batch, latent_hw=HW[res], caption_len=owl.caption_len)
+        ores = oe.output()
+        oe.close()
+        fo = (ores.astype(np.uint32) << 16).view(np.float32)
+        others[f"{res}px"] = {"ms_per_step": round(o_ms, 4), "flop": of["total"],
+                              "mfma_frac": round(of["total"] / (o_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+                              "finite": bool(np.all(np.isfinite(fo)))}
+        log(f"{res}px: {o_ms:.3f} ms/step")
+    line["other_configs"] = others
+    del top, blocks
+    torch.cuda.empty_cache()
+
+    status = 0
     if not args.no_cpu:
         threads = args.cpu_threads or min(16, os.cpu_count() or 1)
-        log(f"cpu baseline on {threads} threads")
-        line["cpu_baseline"] = cpu_baseline(wl, threads)
+        log(f"cpu baseline on {threads} threads: the full {args.resolution}px step")
+        want, secs = stock_step(wl, threads)
+        log(f"cpu baseline: one full dit-step in {secs:.2f} s")
+        line["cpu_baseline"] = {
+            "value": round(secs * 1e3, 1), "unit": "ms", "cores": threads, "kind": "port",
+            "sample": (f"one whole dit-step of the stock oracle (oracle/stock.cpp, the reference's "
+                       f"stock numerics) at the same {args.resolution}px B={wl.batch} workload and "
+                       f"seeds, {threads} threads, not extrapolated")}
+        line["parity"] = parity(got, want)
+        log(f"parity vs the stock oracle: {json.dumps(line['parity'])}")
+        if not line["parity"]["pass"]:
+            status = 1
+        # BASELINE configs[0] (one block, 512px, batch 1, caption 120) and configs[2] (the full
+        # 512px step), timed on the same host
+        cpu_cfg = {}
+        c0 = make_workload(PIXART_SIGMA, batch=1, latent_hw=64, caption_len=120, layers=1)
+        _, s0 = stock_step(c0, threads)
+        cpu_cfg["config0_block_512px_b1_cap120_ms"] = round(s0 * 1e3, 1)
+        if args.resolution != 512:
+            c2 = make_workload(PIXART_SIGMA, batch=2, latent_hw=64, caption_len=wl.caption_len)
+            _, s2 = stock_step(c2, threads)
+            cpu_cfg["config2_step_512px_ms"] = round(s2 * 1e3, 1)
+        line["cpu_baseline"]["other_configs"] = cpu_cfg
+        log(f"cpu baseline, other configs: {cpu_cfg}")
     print(json.dumps(line), flush=True)
-    return 0
+    return status
 
 
 if __name__ == "__main__":

@@ -86,6 +86,16 @@ class SchedConfig(ctypes.Structure):
         return cls(**fields)
 
 
+class ProbeResult(ctypes.Structure):
+    _fields_ = [(f, ctypes.c_double) for f in (
+        "mfma_tflops", "mfma_shader_mhz", "mfma_shader_mhz_min", "mfma_shader_mhz_max",
+        "mfma_peak_at_clock_tflops", "copy_gbs", "max_clock_mhz", "wall_clock_mhz")] + \
+        [("cus", ctypes.c_int)]
+
+    def as_dict(self) -> dict:
+        return {f: (round(getattr(self, f), 2) if f != "cus" else self.cus) for f, _ in self._fields_}
+
+
 class SchedCoefficients(ctypes.Structure):
     _fields_ = [("order", ctypes.c_int)] + [
         (f, ctypes.c_double) for f in ("sigma_s0", "sigma_t", "sigma_vp_s0", "sigma_vp_t",
@@ -120,6 +130,10 @@ SIGNATURES = {
                        ctypes.POINTER(_V)], _I),
     "bh_dit_forward": ([_V, _V, _D, _V, _V, _I, _V, _V], _I),
     "bh_dit_workspace_bytes": ([_V], _I64),
+    "bh_dit_position_table": ([_V, _V, _V], _I),
+    "bh_scale": ([_V, _V, _I64, _F, _I, _V], _I),
+    "bh_timestep_embedding": ([_D, _I, _I64, _V, _I, _V], _I),
+    "bh_probe_device": ([_V, _V, _I64, ctypes.POINTER(ProbeResult)], _I),
     "bh_dit_destroy": ([_V], None),
     "bh_profile_enable": ([_I], _I),
     "bh_profile_read": ([_I, ctypes.POINTER(_D), ctypes.POINTER(_I64), ctypes.POINTER(_D)], _I),

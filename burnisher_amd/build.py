@@ -51,9 +51,17 @@ def sources() -> list[Path]:
 # copies all 80 of them between the register files), and it is compiled without IEEE NaN rules
 # so a maximum over MFMA results is one v_max3 per two inputs, not a quieting v_max per input.
 # denoise.hip evaluates the guidance combine and the solver update in fp64 exactly as the
-# reference's x86-64 build does, which forms no multiply-add.
+# reference's x86-64 build does, which forms no multiply-add. elementwise.hip holds the kernels
+# that reproduce the oracle's arithmetic bit for bit (norms, modulate, add, chunk, activation,
+# patch, scale, the timestep embedding), so it forms no contraction either: under the default
+# -ffp-contract=fast the compiler also fuses an fp64 -> fp32 -> bf16 conversion chain into one
+# rounding, which differs from the reference's two at bf16 ties. probe.hip keeps its MFMA loop's
+# accumulators in VGPRs: in the AGPR form the compiler rotates them through ~50 copies per
+# eight MFMAs, which would measure the copies rather than the matrix cores.
 EXTRA_FLAGS = {"flash72.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form", "-fno-honor-nans"],
-               "denoise.hip": ["-ffp-contract=off"]}
+               "denoise.hip": ["-ffp-contract=off"],
+               "elementwise.hip": ["-ffp-contract=off"],
+               "probe.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 
 
 def _compile(src: Path) -> Path:

@@ -31,25 +31,6 @@ bool is_f32(int dtype) {
     throw Error("dtype " + std::to_string(dtype) + " has no kernel in hip-gfx950 (bf16 or fp32)");
 }
 
-// A pointer the GPU cannot dereference is refused here rather than faulting in a kernel.
-void require_device_ptr(const void* p, const char* op, const char* operand) {
-    if (!p) throw Error(std::string(op) + ": " + operand + " is null");
-    hipPointerAttribute_t attr;
-    if (hipPointerGetAttributes(&attr, p) != hipSuccess) {
-        (void)hipGetLastError();
-        throw Error(std::string(op) + ": " + operand +
-                    " is not memory the HIP runtime knows; host and device operands cannot be "
-                    "mixed in one op");
-    }
-    if (attr.type != hipMemoryTypeDevice && attr.type != hipMemoryTypeManaged) {
-        throw Error(std::string(op) + ": " + operand +
-                    " is a HOST pointer. Mixing host and device operands in one op is a fault, "
-                    "not a slow path.");
-    }
-}
-void optional_device_ptr(const void* p, const char* op, const char* operand) {
-    if (p) require_device_ptr(p, op, operand);
-}
 void require_nonneg(int64_t v, const char* op, const char* what) {
     if (v < 0) throw Error(std::string(op) + ": " + what + " is negative");
 }
@@ -440,6 +421,29 @@ int bh_patch(const void* in, void* out, int64_t batch, int64_t channels, int64_t
                         2.0 * batch * channels * grid * grid * patch * patch * (is_f32(dtype) ? 4 : 2));
         launch_patch(in, out, batch, channels, grid, patch, inverse != 0, is_f32(dtype),
                      as_stream(stream));
+    });
+}
+
+int bh_scale(const void* in, void* out, int64_t numel, float scale, int dtype, void* stream) {
+    return guarded([&] {
+        const char* op = "scale (hip-gfx950)";
+        require_nonneg(numel, op, "numel");
+        if (numel == 0) return;
+        require_device_ptr(in, op, "in");
+        require_device_ptr(out, op, "out");
+        ProfileScope ps(K_ELEMENTWISE, as_stream(stream), 2.0 * numel * (is_f32(dtype) ? 4 : 2));
+        launch_scale(in, out, numel, scale, is_f32(dtype), as_stream(stream));
+    });
+}
+
+int bh_timestep_embedding(double t, int dim, int64_t batch, void* out, int dtype, void* stream) {
+    return guarded([&] {
+        const char* op = "timestep_embedding (hip-gfx950)";
+        require(dim > 0 && dim % 2 == 0, "timestep embedding needs an even dimension");
+        require_nonneg(batch, op, "batch");
+        if (batch == 0) return;
+        require_device_ptr(out, op, "out");
+        launch_timestep_embedding(t, dim, batch, out, is_f32(dtype), as_stream(stream));
     });
 }
 

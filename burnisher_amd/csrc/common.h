@@ -57,6 +57,20 @@ __host__ __device__ inline bf16_t f2bf(float f) {
 // What a store through the tensor dtype does to a float.
 __host__ __device__ inline float round_bf16(float f) { return bf2f(f2bf(f)); }
 
+// bf16 of an fp64 value the way the reference's host code stores one: Tensor::set(static_cast<
+// float>(v)) rounds to float, then to bf16 (two roundings; the second one sees a tie when the
+// float lands exactly halfway between two bf16 values). The second rounding works on the float's
+// bits: with the hardware conversion, the compiler may fuse fptrunc f64->f32->bf16 into one
+// f64->bf16 rounding (round-to-odd to f32, then RNE), which breaks exactly those ties.
+__host__ __device__ inline bf16_t bf16_from_f64(double v) {
+    const float f = static_cast<float>(v);
+    uint32_t u;
+    __builtin_memcpy(&u, &f, 4);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<bf16_t>((u >> 16) | 0x0040u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return static_cast<bf16_t>(u >> 16);
+}
+
 // s_waitcnt through the builtin (gfx9 encoding: vmcnt in bits 3:0 and 15:14, expcnt 6:4, lgkmcnt
 // 11:8; expcnt is left unconstrained). Unlike inline assembly, the compiler's own wait insertion
 // sees this wait: after an opaque one it must assume that scalar loads issued before a loop may
@@ -101,6 +115,28 @@ inline void require(bool ok, const std::string& msg) {
 
 // The C boundary: the message of the last failing call on this host thread (capi.cpp).
 void set_last_error(const std::string& msg);
+
+// A pointer the GPU cannot dereference is refused at the boundary rather than faulting in a
+// kernel (the reference's `require_device`, ops_cuda.cu:79-88): null, memory the HIP runtime
+// does not know, and registered or pinned HOST memory are all errors naming the operand.
+inline void require_device_ptr(const void* p, const char* op, const char* operand) {
+    if (!p) throw Error(std::string(op) + ": " + operand + " is null");
+    hipPointerAttribute_t attr;
+    if (hipPointerGetAttributes(&attr, p) != hipSuccess) {
+        (void)hipGetLastError();
+        throw Error(std::string(op) + ": " + operand +
+                    " is not memory the HIP runtime knows; host and device operands cannot be "
+                    "mixed in one op");
+    }
+    if (attr.type != hipMemoryTypeDevice && attr.type != hipMemoryTypeManaged) {
+        throw Error(std::string(op) + ": " + operand +
+                    " is a HOST pointer. Mixing host and device operands in one op is a fault, "
+                    "not a slow path.");
+    }
+}
+inline void optional_device_ptr(const void* p, const char* op, const char* operand) {
+    if (p) require_device_ptr(p, op, operand);
+}
 
 // Runs `fn`, turning an exception into status 1 plus a message for bh_last_error().
 template <typename Fn>
@@ -336,6 +372,8 @@ void launch_patch(const void* in, void* out, int64_t batch, int64_t channels, in
                   int64_t patch, bool inverse, bool f32, hipStream_t s);
 // Cos-first sinusoidal timestep embedding, fp64, rounded to bf16, broadcast to `batch` rows
 // (weights.cpp:107-121 and the host broadcast at pixart_dit.cpp:156-160).
-void launch_timestep_embedding(double t, int dim, int64_t batch, bf16_t* out, hipStream_t s);
+void launch_timestep_embedding(double t, int dim, int64_t batch, void* out, bool f32, hipStream_t s);
+// ScaleArgs: out[i] = in[i] * scale, one rounding (out may alias in).
+void launch_scale(const void* in, void* out, int64_t n, float scale, bool f32, hipStream_t s);
 
 }  // namespace bh

@@ -343,7 +343,8 @@ int bh_repeat(const void* in, void* out, int64_t outer, int64_t inner, int dtype
         const size_t es = bh::elem_size(dtype);
         bh::require(outer >= 0 && inner >= 0, "repeat: negative extent");
         if (outer * inner == 0) return;
-        bh::require(in && out, "repeat: null pointer");
+        bh::require_device_ptr(in, "repeat (hip-gfx950)", "in");
+        bh::require_device_ptr(out, "repeat (hip-gfx950)", "out");
         bh::ProfileScope ps(bh::K_ELEMENTWISE, static_cast<hipStream_t>(stream),
                             static_cast<double>((outer + 1) * inner * static_cast<int64_t>(es)));
         bh::launch_repeat(in, out, outer, inner, es, static_cast<hipStream_t>(stream));
@@ -358,7 +359,8 @@ int bh_guidance(const void* prediction, void* out, int64_t out_channels, int64_t
                     "guidance: negative extent");
         bh::require(channels <= out_channels, "guidance: channels exceeds out_channels");
         if (channels * spatial == 0) return;
-        bh::require(prediction && out, "guidance: null pointer");
+        bh::require_device_ptr(prediction, "guidance (hip-gfx950)", "prediction");
+        bh::require_device_ptr(out, "guidance (hip-gfx950)", "out");
         bh::ProfileScope ps(bh::K_ELEMENTWISE, static_cast<hipStream_t>(stream),
                             3.0 * channels * spatial * static_cast<double>(es));
         bh::launch_guidance(prediction, true, out, out_channels, channels, spatial, scale,
@@ -476,7 +478,10 @@ int bh_sched_step(bh_sched* s, const void* model_output, int i, void* sample, in
         bh::require(s != nullptr, "sched: null handle");
         bh::require(numel >= 0, "sched: negative size");
         bh::elem_size(dtype);
-        bh::require(numel == 0 || (model_output && sample), "sched: null pointer");
+        if (numel > 0) {
+            bh::require_device_ptr(model_output, "sched_step", "model_output");
+            bh::require_device_ptr(sample, "sched_step", "sample");
+        }
         bh::ProfileScope ps(bh::K_ELEMENTWISE, static_cast<hipStream_t>(stream),
                             static_cast<double>(numel) * 5.0 * static_cast<double>(bh::elem_size(dtype)));
         s->step(model_output, i, sample, numel, dtype, static_cast<hipStream_t>(stream));
@@ -526,7 +531,9 @@ int bh_denoiser_run(bh_denoiser* d, void* latent, const void* caption, const voi
                     int mask_dtype, int use_graph, void* stream) {
     return bh::guarded([&] {
         bh::require(d != nullptr, "denoiser_run: null handle");
-        bh::require(latent && caption && caption_mask, "denoiser_run: null pointer");
+        bh::require_device_ptr(latent, "denoiser_run", "latent");
+        bh::require_device_ptr(caption, "denoiser_run", "caption");
+        bh::require_device_ptr(caption_mask, "denoiser_run", "caption_mask");
         bh::require(mask_dtype == BH_F32 || mask_dtype == BH_BF16, "denoiser_run: mask dtype");
         bh::require(!d->sched->ts.empty(), "denoiser_run: the scheduler has no timesteps set");
         d->sched->reserve(d->per, BH_BF16);

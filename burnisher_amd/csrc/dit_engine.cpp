@@ -142,6 +142,7 @@ void check_weights(const bh_dit_config& c, const bh_dit_weights& w) {
     for (const void* p : top) {
         require(p != nullptr, "dit: a model weight pointer is null. A model that ran with a missing "
                               "weight would produce a plausible image from wrong numbers.");
+        require_device_ptr(p, "dit_create", "a model weight");
     }
     require(w.blocks != nullptr, "dit: null block weight table");
     for (int l = 0; l < c.num_layers; ++l) {
@@ -153,6 +154,7 @@ void check_weights(const bh_dit_config& c, const bh_dit_weights& w) {
         for (const void* p : ps) {
             require(p != nullptr, "dit: transformer_blocks." + std::to_string(l) +
                                       " has a null weight pointer");
+            require_device_ptr(p, "dit_create", "a transformer block weight");
         }
     }
 }
@@ -179,7 +181,7 @@ void forward_opwise(bh_dit& e, const void* latent, double t, const void* caption
 
     {
         ProfileScope ps(K_ELEMENTWISE, s, 0.0);
-        launch_timestep_embedding(t, 256, B, e.temb.bf(), s);
+        launch_timestep_embedding(t, 256, B, e.temb.p, false, s);
     }
     ok(bh_gemm(e.temb.p, e.w.t_emb1_w, e.w.t_emb1_b, e.h_t.p, B, d, 256, 1, BH_EPI_SILU, BF, st));
     ok(bh_gemm(e.h_t.p, e.w.t_emb2_w, e.w.t_emb2_b, e.emb_t.p, B, d, d, 1, BH_EPI_NONE, BF, st));
@@ -274,7 +276,7 @@ void forward_fused(bh_dit& e, const void* latent, double t, const void* caption,
     {   // adaLN-single: one modulation vector per step
         {
             ProfileScope ps(K_ELEMENTWISE, s, 2.0 * B * 256);
-            launch_timestep_embedding(t, 256, B, e.temb.bf(), s);
+            launch_timestep_embedding(t, 256, B, e.temb.p, false, s);
         }
         GemmEpilogue silu;
         silu.act = 2;
@@ -549,6 +551,11 @@ int bh_dit_create(const bh_dit_config* cfg, const bh_dit_weights* w, int64_t bat
 int bh_dit_forward(bh_dit* e, const void* latent, double timestep, const void* caption,
                    const void* caption_mask, int mask_dtype, void* out, void* stream) {
     return guarded([&] {
+        require(e != nullptr, "dit_forward: null engine");
+        require_device_ptr(latent, "dit_forward", "latent");
+        require_device_ptr(caption, "dit_forward", "caption");
+        require_device_ptr(caption_mask, "dit_forward", "caption_mask");
+        require_device_ptr(out, "dit_forward", "out");
         dit_forward_step(e, latent, timestep, caption, caption_mask, mask_dtype, out,
                          static_cast<hipStream_t>(stream), false);
     });
@@ -573,6 +580,14 @@ void bh::dit_forward_step(bh_dit* e, const void* latent, double timestep, const 
 extern "C" {
 
 int64_t bh_dit_workspace_bytes(const bh_dit* e) { return e ? e->workspace : 0; }
+
+int bh_dit_position_table(const bh_dit* e, void* out, void* stream) {
+    return guarded([&] {
+        require(e != nullptr, "dit_position_table: null engine");
+        require_device_ptr(out, "dit_position_table", "out");
+        d2d(out, e->pos_table.p, e->pos_table.bytes, static_cast<hipStream_t>(stream));
+    });
+}
 
 void bh_dit_destroy(bh_dit* e) { delete e; }
 

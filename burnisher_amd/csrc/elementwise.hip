@@ -576,18 +576,32 @@ __global__ void __launch_bounds__(256) k_patch(const T* __restrict__ in, T* __re
 
 // ---- timestep embedding ---------------------------------------------------------------------
 
-__global__ void k_timestep_embedding(double t, int dim, int64_t batch, bf16_t* out) {
+// cos first, then sin (weights.cpp:107-121), each computed in fp64 and stored as the reference
+// stores it: Tensor::set(static_cast<float>(v)), i.e. rounded to float and then through the
+// storage type; the row is repeated `batch` times.
+__device__ inline void store_f64(float* p, int64_t i, double v) { p[i] = static_cast<float>(v); }
+__device__ inline void store_f64(bf16_t* p, int64_t i, double v) { p[i] = bf16_from_f64(v); }
+
+template <typename T>
+__global__ void k_timestep_embedding(double t, int dim, int64_t batch, T* out) {
     const int half = dim / 2;
     for (int i = threadIdx.x; i < half; i += blockDim.x) {
         const double freq = exp(-log(10000.0) * static_cast<double>(i) / half);
         const double a = t * freq;
-        const bf16_t c = f2bf(static_cast<float>(cos(a)));
-        const bf16_t s = f2bf(static_cast<float>(sin(a)));
+        const double c = cos(a), s = sin(a);
         for (int64_t b = 0; b < batch; ++b) {
-            out[b * dim + i] = c;
-            out[b * dim + half + i] = s;
+            store_f64(out, b * dim + i, c);
+            store_f64(out, b * dim + half + i, s);
         }
     }
+}
+
+// ScaleArgs (ops_cpu.cpp:351-353): one multiply per element, one rounding at the store.
+template <typename T>
+__global__ void __launch_bounds__(256) k_scale(const T* in, T* out, int64_t n, float scale) {
+    for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < n;
+         i += static_cast<int64_t>(gridDim.x) * blockDim.x)
+        Io<T>::st(out, i, __fmul_rn(Io<T>::ld(in, i), scale));
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
@@ -832,8 +846,18 @@ void launch_patch(const void* in, void* out, int64_t batch, int64_t channels, in
     launch_check("patch");
 }
 
-void launch_timestep_embedding(double t, int dim, int64_t batch, bf16_t* out, hipStream_t s) {
-    k_timestep_embedding<<<1, 128, 0, s>>>(t, dim, batch, out);
+void launch_scale(const void* in, void* out, int64_t n, float scale, bool f32, hipStream_t s) {
+    if (n == 0) return;
+    const int grid = grid_for(n);
+    if (f32) k_scale<float><<<grid, 256, 0, s>>>(static_cast<const float*>(in), static_cast<float*>(out), n, scale);
+    else k_scale<bf16_t><<<grid, 256, 0, s>>>(static_cast<const bf16_t*>(in), static_cast<bf16_t*>(out), n, scale);
+    launch_check("scale");
+}
+
+void launch_timestep_embedding(double t, int dim, int64_t batch, void* out, bool f32, hipStream_t s) {
+    require(dim > 0 && dim % 2 == 0, "timestep embedding needs an even dimension");
+    if (f32) k_timestep_embedding<float><<<1, 128, 0, s>>>(t, dim, batch, static_cast<float*>(out));
+    else k_timestep_embedding<bf16_t><<<1, 128, 0, s>>>(t, dim, batch, static_cast<bf16_t*>(out));
     launch_check("timestep_embedding");
 }
 

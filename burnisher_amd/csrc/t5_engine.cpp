@@ -279,7 +279,8 @@ int bh_t5_create(const bh_t5_config* cfg, const bh_t5_weights* w, int64_t batch,
 int bh_t5_encode(bh_t5* e, const float* token_ids, void* out, void* stream) {
     return bh::guarded([&] {
         bh::require(e != nullptr, "t5_encode: null engine");
-        bh::require(token_ids != nullptr && out != nullptr, "t5_encode: null ids or output");
+        bh::require(token_ids != nullptr, "t5_encode: null ids");
+        bh::require_device_ptr(out, "t5_encode", "out");
         encode(e, token_ids, static_cast<bf16_t*>(out), static_cast<hipStream_t>(stream));
     });
 }

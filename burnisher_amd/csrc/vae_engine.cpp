@@ -392,7 +392,9 @@ int bh_vae_create(const bh_vae_config* cfg, const bh_vae_weights* w, int64_t lat
 
 int bh_vae_decode(bh_vae* e, const void* latent, void* image, void* stream) {
     return bh::guarded([&] {
-        bh::require(e && latent && image, "vae_decode: null engine or operand");
+        bh::require(e != nullptr, "vae_decode: null engine");
+        bh::require_device_ptr(latent, "vae_decode", "latent");
+        bh::require_device_ptr(image, "vae_decode", "image");
         bh::Run r{*e, static_cast<hipStream_t>(stream)};
         r.decode(static_cast<const bf16_t*>(latent), static_cast<bf16_t*>(image));
     });
@@ -412,7 +414,11 @@ int bh_conv2d(const void* x, const void* weight, const void* bias, void* out, in
                     "conv2d (hip-gfx950): only stride-1 'same' convolutions (2 * pad == k - 1) have a kernel");
         bh::require(dtype == BH_BF16, "conv2d (hip-gfx950): bf16 only (fp32 has no kernel here)");
         if (batch == 0 || c_out == 0 || h == 0 || w == 0) return;
-        bh::require(x && weight && out, "conv2d: null operand");
+        const char* op = "conv2d (hip-gfx950)";
+        bh::require_device_ptr(x, op, "x");
+        bh::require_device_ptr(weight, op, "weight");
+        bh::optional_device_ptr(bias, op, "bias");
+        bh::require_device_ptr(out, op, "out");
         bh::launch_conv2d_nchw(static_cast<const bf16_t*>(x), static_cast<const bf16_t*>(weight),
                                static_cast<const bf16_t*>(bias), static_cast<bf16_t*>(out), batch,
                                c_in, h, w, c_out, k, pad, static_cast<hipStream_t>(stream));
@@ -426,7 +432,8 @@ int bh_upsample(const void* in, void* out, int64_t batch, int64_t channels, int6
                     "upsample: negative size or factor below 1");
         bh::require(dtype == BH_BF16, "upsample (hip-gfx950): bf16 only");
         if (batch * channels * h * w == 0) return;
-        bh::require(in && out, "upsample: null operand");
+        bh::require_device_ptr(in, "upsample (hip-gfx950)", "in");
+        bh::require_device_ptr(out, "upsample (hip-gfx950)", "out");
         bh::launch_upsample_nchw(static_cast<const bf16_t*>(in), static_cast<bf16_t*>(out),
                                  batch * channels, h, w, factor, static_cast<hipStream_t>(stream));
     });
@@ -438,7 +445,8 @@ int bh_transpose(const void* in, void* out, int64_t batch, int64_t channels, int
         bh::require(batch >= 0 && channels >= 0 && spatial >= 0, "transpose: negative size");
         bh::require(dtype == BH_BF16, "transpose (hip-gfx950): bf16 only");
         if (batch * channels * spatial == 0) return;
-        bh::require(in && out, "transpose: null operand");
+        bh::require_device_ptr(in, "transpose (hip-gfx950)", "in");
+        bh::require_device_ptr(out, "transpose (hip-gfx950)", "out");
         if (to_channels_first)
             bh::launch_transpose_bf16(static_cast<const bf16_t*>(in), static_cast<bf16_t*>(out), batch,
                                       spatial, channels, static_cast<hipStream_t>(stream));

@@ -144,6 +144,41 @@ int bh_upsample(const void* in, void* out, int64_t batch, int64_t channels, int6
 int bh_transpose(const void* in, void* out, int64_t batch, int64_t channels, int64_t spatial,
                  int to_channels_first, int dtype, void* stream);
 
+/* ScaleArgs (ops.h:210-215): out[i] = in[i] * scale, one rounding at the store (out may alias
+ * in). Replaces `scale_cuda` (src/cuda/ops_cuda.cu:1018-1031). */
+int bh_scale(const void* in, void* out, int64_t numel, float scale, int dtype, void* stream);
+
+/* The timestep embedding of the DiT's adaLN-single (`sinusoidal_timestep_embedding`,
+ * src/models/weights.cpp:107-121, broadcast over the batch as pixart_dit.cpp:156-160 does):
+ * out[b, i] = cos(t * f_i), out[b, dim/2 + i] = sin(t * f_i) with f_i = exp(-ln(10000) i / (dim/2)),
+ * computed in fp64 on the device and rounded once through float to `dtype`; out is [batch, dim].
+ * An odd dim is refused, as the reference refuses it. */
+int bh_timestep_embedding(double t, int dim, int64_t batch, void* out, int dtype, void* stream);
+
+/* ---- device probe ---------------------------------------------------------------------------- */
+
+/* What the device sustains, measured by this library's own kernels (the reference's `probe`
+ * command, src/cuda/device.cu:257-357, which times a stream copy and a vendor GEMM):
+ *   mfma_tflops        a register-only bf16 MFMA loop (v_mfma_f32_16x16x32_bf16, eight
+ *                      independent accumulators, four waves per SIMD on every CU): the rate no
+ *                      MFMA kernel can exceed on this device at the clock it holds;
+ *   mfma_shader_mhz    the shader clock during that loop, per wave from the shader clock counter
+ *                      over the constant-rate wall clock (median, min and max over waves);
+ *   mfma_peak_at_clock_tflops  CUs x 4096 FLOP/clock x that clock;
+ *   copy_gbs           a device-to-device copy of copy_bytes (read + write bytes over time);
+ *   max_clock_mhz, wall_clock_mhz, cus   what the device reports.
+ * copy_src and copy_dst are device buffers of copy_bytes (>= 1 MiB, a multiple of 16). Runs on the
+ * default stream and synchronises; allocates two small buffers for the loop's results. */
+typedef struct bh_probe_result {
+    double mfma_tflops;
+    double mfma_shader_mhz, mfma_shader_mhz_min, mfma_shader_mhz_max;
+    double mfma_peak_at_clock_tflops;
+    double copy_gbs;
+    double max_clock_mhz, wall_clock_mhz;
+    int cus;
+} bh_probe_result;
+int bh_probe_device(void* copy_src, void* copy_dst, int64_t copy_bytes, bh_probe_result* out);
+
 /* ---- fused ops (no single reference op; each equals a fixed reference op sequence) -------- */
 
 /* norm -> chunk(shift) -> chunk(scale) -> modulate, as the reference DiT block runs them
@@ -233,6 +268,10 @@ int bh_dit_forward(bh_dit* e, const void* latent, double timestep, const void* c
                    const void* caption_mask, int mask_dtype, void* out, void* stream);
 /* Device bytes the engine holds (intermediates plus repacked weights). */
 int64_t bh_dit_workspace_bytes(const bh_dit* e);
+/* Copies the engine's 2-D sin/cos position table (`dit_position_embedding` + `position_table`,
+ * src/models/pixart_dit.cpp:53-105: fp64 on the host, interpolation scale 2, base
+ * sample_size / patch_size, stored bf16), [grid*grid, hidden], into the device buffer `out`. */
+int bh_dit_position_table(const bh_dit* e, void* out, void* stream);
 void bh_dit_destroy(bh_dit* e);
 
 /* ---- the denoise loop around the dit-step (pipeline.cpp:104-131) -------------------------- */

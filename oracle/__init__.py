@@ -35,6 +35,7 @@ _STOCK_SIGS = {
     "stock_position_embedding": ([ctypes.POINTER(_D), _I, _I, _I, _D], _I),
     "stock_timestep_embedding": ([_D, _I, ctypes.POINTER(_F)], _I),
     "stock_dit_forward": ([_V, _V, _I64, _I64, _I64, _V, _D, _V, _V, _I, _V, _I, _I], _I),
+    "stock_scale": ([_V, _V, _I64, _F, _I], _I),
     "stock_repeat": ([_V, _V, _I64, _I64, _I], _I),
     "stock_guidance": ([_V, _V, _I64, _I64, _I64, _F, _I], _I),
     "stock_sched_create": ([_V, ctypes.POINTER(_V)], _I),
@@ -67,6 +68,7 @@ _REF_SIGS = {
     "ref_position_embedding": ([ctypes.POINTER(_D), _I, _I, _I, _D], _I),
     "ref_timestep_embedding": ([_D, _I, ctypes.POINTER(_F)], _I),
     "ref_dit_forward": ([_V, _V, _I64, _I64, _I64, _V, _D, _V, _V, _I, _V, _I], _I),
+    "ref_scale": ([_V, _V, _I64, _F, _I], _I),
     "ref_repeat": ([_V, _V, _I64, _I64, _I], _I),
     "ref_guidance": ([_V, _V, _I64, _I64, _I64, _F, _I], _I),
     "ref_sched_create": ([_V, ctypes.POINTER(_V)], _I),
@@ -104,10 +106,22 @@ def _load(path: Path, sigs: dict) -> ctypes.CDLL:
 
 
 def build(reference: bool = True) -> None:
-    """make -C oracle (and the `ref` target when /root/reference exists)."""
+    """make -C oracle (and the `ref` and `registry` targets when /root/reference exists; the
+    registry driver also needs the built burnisher_amd/lib/libburnisher_hip.so)."""
     subprocess.run(["make", "-s", "-C", str(HERE)], check=True)
     if reference and REFERENCE_ROOT.exists():
         subprocess.run(["make", "-s", "-C", str(HERE), "ref"], check=True)
+        if (HERE.parent / "burnisher_amd" / "lib" / "libburnisher_hip.so").exists():
+            subprocess.run(["make", "-s", "-C", str(HERE), "registry"], check=True)
+
+
+REGISTRY_MAIN = HERE / "_ref" / "registry_main"
+
+
+def registry_main() -> Path | None:
+    """oracle/_ref/registry_main (the reference runtime with the hip-gfx950 registrations and the
+    HIP device layer), or None where it was not built."""
+    return REGISTRY_MAIN if REGISTRY_MAIN.exists() else None
 
 
 def stock() -> ctypes.CDLL:

@@ -275,6 +275,14 @@ int ref_dit_forward(const bh_dit_config* cfg, const bh_dit_weights* w, int64_t b
 }
 
 
+int ref_scale(const void* in, void* out, int64_t numel, float scale, int dtype) {
+    return guard([&] {
+        Tensor x = view(in, {numel}, dtype);
+        Tensor y = view(out, {numel}, dtype);
+        ScaleRegistry::instance().get("stock")(ScaleArgs{&x, &y, numel, scale});
+    });
+}
+
 int ref_repeat(const void* in, void* out, int64_t outer, int64_t inner, int dtype) {
     return guard([&] {
         Tensor x = view(in, {inner}, dtype);

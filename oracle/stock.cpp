@@ -501,6 +501,14 @@ void dit_forward(const bh_dit_config& c, const bh_dit_weights& w, int64_t B, int
     patch_impl(tokens.p(), image, B, c.out_channels, grid, P, true, BF);
 }
 
+// ---- ScaleArgs (ops_cpu.cpp:351-353): one multiply per element, one rounding -------------------
+
+void scale_impl(const void* in, void* out, int64_t n, float scale, int dt) {
+    View x{in, dt};
+    Out y{out, dt};
+    for (int64_t i = 0; i < n; ++i) y.set(i, x.get(i) * scale);
+}
+
 // ---- the denoise loop's two ops (ops_cpu.cpp:355-369) -----------------------------------------
 
 void repeat_impl(const void* in, void* out, int64_t outer, int64_t inner, int dt) {
@@ -1042,6 +1050,10 @@ int stock_dit_forward(const bh_dit_config* cfg, const bh_dit_weights* w, int64_t
     });
 }
 
+
+int stock_scale(const void* in, void* out, int64_t numel, float scale, int dtype) {
+    return guard([&] { scale_impl(in, out, numel, scale, dtype); });
+}
 
 int stock_repeat(const void* in, void* out, int64_t outer, int64_t inner, int dtype) {
     return guard([&] { repeat_impl(in, out, outer, inner, dtype); });

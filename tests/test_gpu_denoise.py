@@ -75,6 +75,21 @@ def test_guidance_matches_oracle(hip, stock, dtype, scale):
     assert np.array_equal(host(do, want), want)
 
 
+@pytest.mark.parametrize("dtype", [F32, BF16], ids=["f32", "bf16"])
+def test_guidance_matches_oracle_at_bf16_ties(hip, stock, dtype):
+    # 4M outputs at an irregular scale: the fp64 combine is inexact in float, so a few dozen
+    # floats land exactly on a bf16 tie, where one fused f64 -> bf16 rounding and the reference's
+    # two roundings (f64 -> f32 -> bf16) disagree.
+    oc, ch, sp = 8, 4, 1024 * 1024
+    pred = enc(dtype)(np.random.default_rng(11).standard_normal(2 * oc * sp) * 2)
+    want = np.zeros(ch * sp, pred.dtype)
+    oracle.call(stock, "stock_guidance", addr(pred), addr(want), oc, ch, sp, 4.1, dtype)
+    dp, do = dev(pred), dev(np.zeros_like(want))
+    bh.call("bh_guidance", dp.data_ptr(), do.data_ptr(), oc, ch, sp, 4.1, dtype, None)
+    got = host(do, want)
+    assert np.array_equal(got, want), f"{np.sum(got != want)} of {want.size} differ"
+
+
 class DeviceSampler:
     def __init__(self, steps, **overrides):
         self.h = ctypes.c_void_p()

@@ -2,6 +2,7 @@
 the same seeded weights and inputs, and the reference's graph invariants on the device
 (/root/reference/tests/test_models.cpp:274-348)."""
 import ctypes
+import os
 
 import numpy as np
 import pytest
@@ -50,18 +51,23 @@ class Engine:
             self.handle = ctypes.c_void_p()
 
 
+# The oracle runs on the host's share of cores (16 per GPU on the GPU boxes), whatever the
+# machine reports; its result does not depend on the thread count.
+THREADS = min(16, os.cpu_count() or 1)
+
+
 def oracle_forward(wl, layers=-1):
     cfg = config_struct(wl.cfg)
     w, keep = wl.weight_struct(wl.top, wl.blocks)
     out = np.zeros((wl.batch, wl.cfg["out_channels"], wl.latent_hw, wl.latent_hw), np.uint16)
     oracle.call(oracle.stock(), "stock_dit_forward", ctypes.byref(cfg), ctypes.byref(w), wl.batch,
                 wl.latent_hw, wl.caption_len, addr(wl.latent), wl.timestep, addr(wl.caption),
-                addr(wl.mask), F32, addr(out), 0, layers)
+                addr(wl.mask), F32, addr(out), THREADS, layers)
     return out
 
 
-def check_step(got, want, where):
-    tol = TOLERANCE["dit_step"]
+def check_step(got, want, where, gate="dit_step"):
+    tol = TOLERANCE[gate]
     s = stats(from_bf16(got), from_bf16(want))
     print(f"dit-step parity {where}: {s}")
     assert np.all(np.isfinite(from_bf16(got))), where
@@ -106,7 +112,7 @@ def test_one_block_1024px_matches_oracle(hip):
     wl = make_workload(PIXART_SIGMA, batch=2, latent_hw=128, caption_len=300, layers=1)
     e = Engine(wl, 0)
     try:
-        check_step(e.forward(), oracle_forward(wl), "1024px, 1 block")
+        check_step(e.forward(), oracle_forward(wl), "1024px, 1 block", "dit_block")
     finally:
         e.close()
 
@@ -116,6 +122,63 @@ def test_full_depth_512px_matches_oracle(hip):
     e = Engine(wl, 0)
     try:
         check_step(e.forward(), oracle_forward(wl), "512px, 28 blocks")
+    finally:
+        e.close()
+
+
+def test_config0_one_block_512px_batch1_caption120(hip):
+    # one block, 512px (1024 tokens), batch 1, a 120-token caption.
+    wl = make_workload(PIXART_SIGMA, batch=1, latent_hw=64, caption_len=120, layers=1)
+    for mode in (0, 1):
+        e = Engine(wl, mode)
+        try:
+            check_step(e.forward(), oracle_forward(wl), f"512px B=1 caption 120, 1 block, mode={mode}",
+                       "dit_block")
+        finally:
+            e.close()
+
+
+def test_full_depth_1024px_matches_oracle(hip):
+    # The headline configuration at full depth against the oracle.
+    wl = make_workload(PIXART_SIGMA, batch=2, latent_hw=128, caption_len=300)
+    e = Engine(wl, 0)
+    try:
+        got = e.forward()
+    finally:
+        e.close()
+    check_step(got, oracle_forward(wl), "1024px, 28 blocks")
+
+
+def test_one_block_2048px_matches_oracle(hip):
+    # BASELINE configs[4]'s shape (16384 image tokens, the long-sequence case), one block.
+    wl = make_workload(PIXART_SIGMA, batch=2, latent_hw=256, caption_len=300, layers=1)
+    e = Engine(wl, 0)
+    try:
+        got = e.forward()
+    finally:
+        e.close()
+    check_step(got, oracle_forward(wl), "2048px, 1 block", "dit_block")
+
+
+def test_full_depth_2048px_invariants(hip):
+    # configs[4] at full depth: finite, varied, replayable, timestep- and caption-sensitive, and
+    # blind to masked caption positions. (The oracle's full 2048px step is ~100 TFLOP of host
+    # work; one block is checked against it above.)
+    import torch
+    wl = make_workload(PIXART_SIGMA, batch=2, latent_hw=256, caption_len=300)
+    e = Engine(wl, 0)
+    try:
+        a = e.forward()
+        fa = from_bf16(a)
+        assert np.all(np.isfinite(fa)) and fa.std() > 1e-3
+        assert np.array_equal(a, e.forward())
+        assert np.max(np.abs(fa - from_bf16(e.forward(timestep=100.0)))) > 1e-3
+        cap = e.caption.clone()
+        for b in range(wl.batch):
+            keep = int(wl.mask[b].sum())
+            cap[b, keep:, :] = 99.0
+        assert np.array_equal(a, e.forward(caption=cap))
+        assert np.max(np.abs(fa - from_bf16(e.forward(mask=torch.ones_like(e.mask))))) > 1e-3
     finally:
         e.close()
 
@@ -137,6 +200,30 @@ def test_full_depth_1024px_invariants(hip):
             cap[b, keep:, :] = 99.0
         assert np.array_equal(a, e.forward(caption=cap))
         assert np.max(np.abs(fa - from_bf16(e.forward(mask=torch.ones_like(e.mask))))) > 1e-3
+    finally:
+        e.close()
+
+
+def test_forward_refuses_host_operands(hip):
+    import burnisher_amd as bh
+    wl = make_workload(SMALL, batch=2, latent_hw=8, caption_len=5)
+    e = Engine(wl, 0)
+    try:
+        host_latent = np.zeros(wl.latent.size, np.uint16)
+        lib = bh.lib()
+        assert lib.bh_dit_forward(e.handle, host_latent.ctypes.data, 500.0, e.caption.data_ptr(),
+                                  e.mask.data_ptr(), F32, e.out.data_ptr(), None) != 0
+        assert b"HOST" in lib.bh_last_error() and b"latent" in lib.bh_last_error()
+        host_out = np.zeros(e.out.numel(), np.uint16)
+        assert lib.bh_dit_forward(e.handle, e.latent.data_ptr(), 500.0, e.caption.data_ptr(),
+                                  e.mask.data_ptr(), F32, host_out.ctypes.data, None) != 0
+        assert b"out" in lib.bh_last_error()
+        # host weights are refused at create
+        cfg = config_struct(wl.cfg)
+        w, keep = wl.weight_struct(wl.top, wl.blocks)
+        h = ctypes.c_void_p()
+        assert lib.bh_dit_create(ctypes.byref(cfg), ctypes.byref(w), 2, 8, 5, 0, ctypes.byref(h)) != 0
+        assert b"HOST" in lib.bh_last_error()
     finally:
         e.close()
 

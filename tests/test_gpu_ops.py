@@ -344,6 +344,45 @@ def test_add_chunk_activation_patch(hip):
     assert np.array_equal(host(got, want), want)
 
 
+@pytest.mark.parametrize("dtype", [F32, BF16], ids=["f32", "bf16"])
+def test_scale_matches_oracle(hip, dtype):
+    x = ramp((5003,), 0.29) * np.float32(4.0)
+    xin = x if dtype == F32 else to_bf16(x)
+    want = np.zeros_like(xin)
+    st("stock_scale", addr(xin), addr(want), xin.size, 0.18215, dtype)
+    got = empty(xin.shape, bf16=dtype == BF16)
+    call("bh_scale", P(dev(xin)), P(got), xin.size, 0.18215, dtype, None)
+    assert np.array_equal(host(got, want), want)
+    # in place
+    d = dev(xin)
+    call("bh_scale", P(d), P(d), xin.size, 0.18215, dtype, None)
+    assert np.array_equal(host(d, want), want)
+
+
+def test_host_operands_refused_by_every_op(hip):
+    # Each op's entry point refuses a host operand with an error before any launch
+    # (the reference's require_device, ops_cuda.cu:79-88).
+    import burnisher_amd as bh
+    lib = bh.lib()
+    h = np.zeros(4096, np.uint16)
+    d = empty((4096,))
+    H, D = h.ctypes.data, P(d)
+    cases = {
+        "conv2d": lambda: lib.bh_conv2d(H, D, None, D, 1, 4, 4, 4, 4, 3, 1, BF16, None),
+        "conv2d out": lambda: lib.bh_conv2d(D, D, None, H, 1, 4, 4, 4, 4, 3, 1, BF16, None),
+        "upsample": lambda: lib.bh_upsample(H, D, 1, 4, 4, 4, 2, BF16, None),
+        "transpose": lambda: lib.bh_transpose(D, H, 1, 4, 16, 0, BF16, None),
+        "repeat": lambda: lib.bh_repeat(H, D, 2, 16, BF16, None),
+        "guidance": lambda: lib.bh_guidance(D, H, 8, 4, 16, 4.5, BF16, None),
+        "scale": lambda: lib.bh_scale(H, D, 16, 2.0, BF16, None),
+        "timestep": lambda: lib.bh_timestep_embedding(1.0, 8, 1, H, BF16, None),
+        "modulate": lambda: lib.bh_modulate(D, D, H, D, 1, 4, 4, None, None, BF16, None),
+    }
+    for name, fn in cases.items():
+        assert fn() != 0, name
+        assert b"HOST" in lib.bh_last_error(), (name, lib.bh_last_error())
+
+
 def test_contract_errors(hip):
     import burnisher_amd as bh
     host_a = np.zeros((4, 8), np.uint16)

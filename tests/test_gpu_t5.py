@@ -90,6 +90,9 @@ def device_encode(wl):
     bh.call("bh_t5_create", ctypes.byref(cfg), ctypes.byref(w), wl.batch, wl.seq, ctypes.byref(h))
     try:
         out = torch.zeros((wl.batch, wl.seq, wl.cfg["d_model"]), dtype=torch.bfloat16, device="cuda")
+        host_out = np.zeros((wl.batch, wl.seq, wl.cfg["d_model"]), np.uint16)
+        assert bh.lib().bh_t5_encode(h, wl.ids.ctypes.data, host_out.ctypes.data, None) != 0
+        assert b"HOST" in bh.lib().bh_last_error()
         bh.call("bh_t5_encode", h, wl.ids.ctypes.data, out.data_ptr(), None)
         first = host(out)
         bh.call("bh_t5_encode", h, wl.ids.ctypes.data, out.data_ptr(), None)

@@ -133,6 +133,10 @@ def decode(wl):
     bh.call("bh_vae_create", ctypes.byref(cfg), ctypes.byref(w), wl.latent_hw, ctypes.byref(h))
     try:
         out = empty((1, 3, wl.image_hw, wl.image_hw))
+        # a host operand is refused before any launch
+        host_latent = np.zeros(latent.numel(), np.uint16)
+        assert bh.lib().bh_vae_decode(h, host_latent.ctypes.data, out.data_ptr(), None) != 0
+        assert b"HOST" in bh.lib().bh_last_error()
         bh.call("bh_vae_decode", h, latent.data_ptr(), out.data_ptr(), None)
         first = host(out)
         bh.call("bh_vae_decode", h, latent.data_ptr(), out.data_ptr(), None)

@@ -51,6 +51,9 @@ def test_arguments_refused_before_any_device_work():
     assert b"bf16 only" in lib.bh_last_error()
     assert lib.bh_chunk(None, None, None, 2, 4, 6, 9, -1, 1, None) != 0
     assert b"chunk" in lib.bh_last_error()
+    # an odd timestep-embedding width is refused as the reference refuses it (weights.cpp:111)
+    assert lib.bh_timestep_embedding(500.0, 7, 2, None, 1, None) != 0
+    assert b"even dimension" in lib.bh_last_error()
     # an empty op is a no-op, not an error
     assert lib.bh_gemm(None, None, None, None, 0, 4, 4, 1, 0, 1, None) == 0
     assert lib.bh_last_error() == b""

@@ -312,3 +312,19 @@ def test_embeddings_match_reference(stock, ref):
     stock_call(stock, "stock_timestep_embedding", 500.0, 256, a.ctypes.data_as(P))
     oracle.call(ref, "ref_timestep_embedding", 500.0, 256, b.ctypes.data_as(P))
     assert np.array_equal(a, b)
+
+
+@pytest.mark.parametrize("dtype", [F32, BF16], ids=["f32", "bf16"])
+def test_stock_scale_matches_reference(stock, ref, dtype):
+    # ScaleArgs (ops_cpu.cpp:351-353): one multiply, one rounding; equal to the reference bit for bit
+    # and, being a single IEEE multiply, to numpy's float32 product rounded the same way.
+    x = ramp((4099,), 0.37) * np.float32(3.0)
+    xin = x if dtype == F32 else to_bf16(x)
+    o1 = np.zeros_like(xin)
+    o2 = np.zeros_like(xin)
+    oracle.call(stock, "stock_scale", addr(xin), addr(o1), xin.size, 0.18215, dtype)
+    oracle.call(ref, "ref_scale", addr(xin), addr(o2), xin.size, 0.18215, dtype)
+    assert np.array_equal(o1, o2)
+    xf = xin if dtype == F32 else from_bf16(xin)
+    want = (xf * np.float32(0.18215)).astype(np.float32)
+    assert np.array_equal(o1, want if dtype == F32 else to_bf16(want))
