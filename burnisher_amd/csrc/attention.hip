@@ -446,31 +446,60 @@ bf16_t* vt_workspace(size_t elems) {
     }
     return static_cast<bf16_t*>(ptr[dev]);
 }
-}  // namespace
 
-void launch_attention_bf16(const bf16_t* q, const bf16_t* k, const bf16_t* v, bf16_t* out,
-                           const AttnShape& sh, const void* key_mask, bool mask_f32,
-                           hipStream_t s, const bf16_t* bias) {
-    if (sh.batch * sh.heads * sh.q_len == 0) return;
+// Which kernel launch_attention_bf16 runs for these operands, and the V^T elements it needs.
+struct AttnPlan {
+    enum Kind { FLASH512, FLASH72, FLASH } kind;
+    int64_t vt_elems;
+};
+
+AttnPlan plan_attention(const bf16_t* q, const bf16_t* k, const bf16_t* v, const bf16_t* out,
+                        const AttnShape& sh, const void* key_mask, const bf16_t* bias) {
     // head_dim 512, one head, self-attention, unmasked (the VAE mid-block): its own kernel.
     if (sh.head_dim == 512 && sh.heads == 1 && sh.q_len == sh.kv_len && !key_mask && !bias &&
         sh.ld_q == 512 && sh.ld_kv == 512 && sh.ld_o == 512 && aligned16(q) && aligned16(k) &&
-        aligned16(v) && aligned16(out)) {
-        const int64_t ld = vt512_ld(sh.kv_len);
-        bf16_t* vt = vt_workspace(static_cast<size_t>(512 * ld));
+        aligned16(v) && aligned16(out))
+        return {AttnPlan::FLASH512, 512 * vt512_ld(sh.kv_len)};
+    // head_dim 72 (the DiT): V transposed once, then the flash kernel built for that width.
+    const bool fast72 = !bias && sh.head_dim == 72 && sh.kv_len <= 16384 && sh.ld_q % 8 == 0 &&
+                        sh.ld_kv % 8 == 0 && sh.ld_o % 4 == 0 && aligned16(q) && aligned16(k) &&
+                        aligned16(v) && (reinterpret_cast<uintptr_t>(out) % 8 == 0);
+    if (fast72) return {AttnPlan::FLASH72, sh.batch * sh.heads * 72 * flash72_vt_ld(sh.kv_len)};
+    return {AttnPlan::FLASH, 0};
+}
+
+}  // namespace
+
+int64_t attention_vt_elems(const bf16_t* q, const bf16_t* k, const bf16_t* v, const bf16_t* out,
+                           const AttnShape& sh, const void* key_mask, const bf16_t* bias) {
+    if (sh.batch * sh.heads * sh.q_len == 0) return 0;
+    return plan_attention(q, k, v, out, sh, key_mask, bias).vt_elems;
+}
+
+void launch_attention_bf16(const bf16_t* q, const bf16_t* k, const bf16_t* v, bf16_t* out,
+                           const AttnShape& sh, const void* key_mask, bool mask_f32,
+                           hipStream_t s, const bf16_t* bias, bf16_t* vt_buf, int64_t vt_buf_elems) {
+    if (sh.batch * sh.heads * sh.q_len == 0) return;
+    const AttnPlan plan = plan_attention(q, k, v, out, sh, key_mask, bias);
+    // V^T goes to the caller's buffer when one is given (it must be large enough), else to the
+    // per-device workspace.
+    auto vt_for = [&](int64_t elems) {
+        if (!vt_buf) return vt_workspace(static_cast<size_t>(elems));
+        require(vt_buf_elems >= elems, "attention: the V^T buffer holds " + std::to_string(vt_buf_elems) +
+                                           " elements, this call needs " + std::to_string(elems));
+        return vt_buf;
+    };
+    if (plan.kind == AttnPlan::FLASH512) {
+        bf16_t* vt = vt_for(plan.vt_elems);
         for (int64_t b = 0; b < sh.batch; ++b) {
             const int64_t off = b * sh.q_len * 512;
             launch_attention512(q + off, k + off, v + off, vt, out + off, sh.q_len, sh.scale, s);
         }
         return;
     }
-    // head_dim 72 (the DiT): V transposed once, then the flash kernel built for that width.
-    const bool fast72 = !bias && sh.head_dim == 72 && sh.kv_len <= 16384 && sh.ld_q % 8 == 0 &&
-                        sh.ld_kv % 8 == 0 && sh.ld_o % 4 == 0 && aligned16(q) && aligned16(k) &&
-                        aligned16(v) && (reinterpret_cast<uintptr_t>(out) % 8 == 0);
-    if (fast72) {
+    if (plan.kind == AttnPlan::FLASH72) {
         const int64_t vt_ld = flash72_vt_ld(sh.kv_len);
-        bf16_t* vt = vt_workspace(static_cast<size_t>(sh.batch * sh.heads * 72 * vt_ld));
+        bf16_t* vt = vt_for(plan.vt_elems);
         launch_transpose_v72(v, sh.ld_kv, sh.batch, sh.heads, sh.kv_len, vt, vt_ld, s);
         launch_flash72(q, sh.ld_q, k, sh.ld_kv, vt, vt_ld, out, sh.ld_o, sh.batch, sh.heads,
                        sh.q_len, sh.kv_len, sh.scale, key_mask, mask_f32, s);

@@ -310,9 +310,16 @@ struct AttnShape {
     float scale;                // resolved (never 0)
 };
 // bias: optional bf16 [heads, q_len, kv_len] added to the scaled scores (head_dim <= 128 only).
+// The head_dim-72 and -512 kernels read V transposed: into `vt_buf` (vt_buf_elems elements, at
+// least attention_vt_elems of the call, else an error) when given, else into a per-device
+// workspace that grows on demand and that calls overlapping on one device share.
 void launch_attention_bf16(const bf16_t* q, const bf16_t* k, const bf16_t* v, bf16_t* out,
                            const AttnShape& sh, const void* key_mask, bool mask_f32,
-                           hipStream_t s, const bf16_t* bias = nullptr);
+                           hipStream_t s, const bf16_t* bias = nullptr, bf16_t* vt_buf = nullptr,
+                           int64_t vt_buf_elems = 0);
+// The V^T elements launch_attention_bf16 needs for these operands (0: the kernel reads V as is).
+int64_t attention_vt_elems(const bf16_t* q, const bf16_t* k, const bf16_t* v, const bf16_t* out,
+                           const AttnShape& sh, const void* key_mask, const bf16_t* bias);
 // Flash attention at head_dim 72 with V supplied transposed (flash72.hip): vt holds, for each
 // (b, h, d), a row of vt_ld >= flash72_vt_ld(kv_len) keys, zero past kv_len.
 int64_t flash72_vt_ld(int64_t kv_len);

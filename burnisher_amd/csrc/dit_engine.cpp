@@ -22,6 +22,7 @@
 // embedding is computed on the device from the scalar timestep, so no upload happens per step.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstring>
 #include <memory>
@@ -115,6 +116,8 @@ struct bh_dit {
     DevBuf shift, scale, gate, zero, tokens;
     DevBuf w_qkv, b_qkv, w_kv, b_kv;   // repacked weights (fused plan)
     DevBuf vt_self, vt_cross;         // V transposed for the attention kernel (fused plan)
+    DevBuf vt_op;                     // head_dim 72 without the transposed store: the engine's
+    int64_t vt_op_elems = 0;          // own V^T buffer (never the op-level shared workspace)
     int64_t vt_ld_self = 0, vt_ld_cross = 0;
     bool vt72 = false;
     int64_t workspace = 0;
@@ -352,7 +355,7 @@ void forward_fused(bh_dit& e, const void* latent, double t, const void* caption,
         } else {
             launch_attention_bf16(e.qkv.bf(), e.qkv.bf() + d, e.qkv.bf() + 2 * d, e.ctx.bf(),
                                   AttnShape{B, H, N, N, Dh, 3 * d, 3 * d, d, scale}, nullptr,
-                                  false, s);
+                                  false, s, nullptr, e.vt_op.bf(), e.vt_op_elems);
         }
         {
             GemmEpilogue ep;
@@ -372,7 +375,7 @@ void forward_fused(bh_dit& e, const void* latent, double t, const void* caption,
             launch_attention_bf16(e.q2.bf(), e.kv_all.bf() + l * 2 * d,
                                   e.kv_all.bf() + l * 2 * d + d, e.ctx.bf(),
                                   AttnShape{B, H, N, e.cap_len, Dh, d, L * 2 * d, d, scale}, mask,
-                                  mask_f32, s);
+                                  mask_f32, s, nullptr, e.vt_op.bf(), e.vt_op_elems);
         }
         {
             GemmEpilogue ep;
@@ -512,6 +515,11 @@ int bh_dit_create(const bh_dit_config* cfg, const bh_dit_weights* w, int64_t bat
                 e->vt_ld_cross = flash72_vt_ld(caption_len);
                 e->vt_self = e->make(B * c.num_heads * 72 * e->vt_ld_self);
                 e->vt_cross = e->make(L * B * c.num_heads * 72 * e->vt_ld_cross);
+            } else if (c.head_dim == 72) {
+                // The attention transposes V itself; it does so into this buffer, which the
+                // engine owns, so a captured forward never holds a pointer another call frees.
+                e->vt_op_elems = B * c.num_heads * 72 * flash72_vt_ld(std::max(e->N, caption_len));
+                e->vt_op = e->make(e->vt_op_elems);
             }
             e->w_qkv = e->make(L * 3 * d * d);
             e->b_qkv = e->make(L * 3 * d);
