@@ -116,6 +116,7 @@ SIGNATURES = {
     "bh_gemm": ([_V, _V, _V, _V, _I64, _I64, _I64, _I, _I, _I, _V], _I),
     "bh_gemm_fused_run": ([_V, _V, _V, _V, _I64, _I64, _I64, ctypes.POINTER(GemmFused), _V], _I),
     "bh_attention": ([_V, _V, _V, _V, _I64, _I64, _I64, _I64, _I64, _F, _V, _V, _I, _I, _V], _I),
+    "bh_attention_noalloc": ([_V, _V, _V, _V, _I64, _I64, _I64, _I64, _I64, _F, _V, _V, _I, _I, _V], _I),
     "bh_attention_strided": ([_V, _I64, _V, _V, _I64, _V, _I64, _I64, _I64, _I64, _I64, _I64, _F,
                               _V, _I, _I, _V], _I),
     "bh_norm": ([_V, _V, _V, _V, _I64, _I64, _F, _I, _I64, _I64, _I, _V], _I),

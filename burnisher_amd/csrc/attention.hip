@@ -427,6 +427,12 @@ __global__ void __launch_bounds__(128) k_attention_generic(const T* __restrict__
 namespace {
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
+// The allocation-free entry point's V^T scratch: one fixed array per device, in the code
+// object's device memory (each GPU the library runs on holds its own copy until the process
+// ends). Host code never uses this name as an address: its device address, per device, comes
+// from hipGetSymbolAddress at set-up (noalloc_scratch below).
+__device__ __align__(256) bf16_t scratch[kNoAllocScratchBytes / sizeof(bf16_t)];
+
 // V^T scratch for the head_dim-72 path of the op-level entry point: grown on demand, kept until
 // the process ends, one per device. Calls that overlap on one device share it.
 bf16_t* vt_workspace(size_t elems) {
@@ -474,6 +480,22 @@ int64_t attention_vt_elems(const bf16_t* q, const bf16_t* k, const bf16_t* v, co
                            const AttnShape& sh, const void* key_mask, const bf16_t* bias) {
     if (sh.batch * sh.heads * sh.q_len == 0) return 0;
     return plan_attention(q, k, v, out, sh, key_mask, bias).vt_elems;
+}
+
+bf16_t* noalloc_scratch() {
+    static std::mutex mu;
+    static void* ptr[64] = {};
+    int dev = 0;
+    hip_check(hipGetDevice(&dev), "hipGetDevice");
+    require(dev >= 0 && dev < 64, "attention: device index out of range");
+    std::lock_guard<std::mutex> lock(mu);
+    if (!ptr[dev]) {
+        void* p = nullptr;
+        hip_check(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress (attention scratch)");
+        require(p != nullptr, "attention: the scratch array has no device address");
+        ptr[dev] = p;
+    }
+    return static_cast<bf16_t*>(ptr[dev]);
 }
 
 void launch_attention_bf16(const bf16_t* q, const bf16_t* k, const bf16_t* v, bf16_t* out,

@@ -150,6 +150,8 @@ int bh_init(int device) {
         require(arch.rfind("gfx950", 0) == 0,
                 "bh_init: device " + std::to_string(device) + " is " + arch +
                     "; this library holds gfx950 code only");
+        // the allocation-free attention's scratch address on this device, looked up once
+        (void)noalloc_scratch();
     });
 }
 
@@ -229,9 +231,10 @@ namespace {
 int attention_impl(const void* q, int64_t ld_q, const void* k, const void* v, int64_t ld_kv,
                    void* out, int64_t ld_o, int64_t batch, int64_t heads, int64_t q_len,
                    int64_t kv_len, int64_t head_dim, float scale, const void* bias,
-                   const void* key_mask, int mask_dtype, int dtype, void* stream) {
+                   const void* key_mask, int mask_dtype, int dtype, void* stream,
+                   bool noalloc = false) {
     return guarded([&] {
-        const char* op = "attention (hip-gfx950)";
+        const char* op = noalloc ? "attention_noalloc (hip-gfx950)" : "attention (hip-gfx950)";
         require_nonneg(batch, op, "batch");
         require_nonneg(heads, op, "heads");
         require_nonneg(q_len, op, "q_len");
@@ -259,9 +262,25 @@ int attention_impl(const void* q, int64_t ld_q, const void* k, const void* v, in
                                      as_stream(stream));
             return;
         }
-        launch_attention_bf16(static_cast<const bf16_t*>(q), static_cast<const bf16_t*>(k),
-                              static_cast<const bf16_t*>(v), static_cast<bf16_t*>(out), sh,
-                              key_mask, mask_f32, as_stream(stream), static_cast<const bf16_t*>(bias));
+        const auto* qb = static_cast<const bf16_t*>(q);
+        const auto* kb = static_cast<const bf16_t*>(k);
+        const auto* vb = static_cast<const bf16_t*>(v);
+        auto* ob = static_cast<bf16_t*>(out);
+        const auto* bb = static_cast<const bf16_t*>(bias);
+        if (!noalloc) {
+            launch_attention_bf16(qb, kb, vb, ob, sh, key_mask, mask_f32, as_stream(stream), bb);
+            return;
+        }
+        // V^T into the fixed per-device scratch: nothing is allocated, so the call is refused
+        // when the transposed V would not fit.
+        const int64_t need = attention_vt_elems(qb, kb, vb, ob, sh, key_mask, bb);
+        const int64_t cap = kNoAllocScratchBytes / static_cast<int64_t>(sizeof(bf16_t));
+        require(need <= cap, "attention_noalloc: V^T needs " + std::to_string(need * 2) +
+                                 " bytes of scratch, above the fixed maximum of " +
+                                 std::to_string(kNoAllocScratchBytes) +
+                                 " bytes (use bh_attention, which grows its workspace)");
+        launch_attention_bf16(qb, kb, vb, ob, sh, key_mask, mask_f32, as_stream(stream), bb,
+                              need > 0 ? noalloc_scratch() : nullptr, cap);
     });
 }
 }  // namespace
@@ -272,6 +291,15 @@ int bh_attention(const void* q, const void* k, const void* v, void* out, int64_t
     const int64_t ld = heads * head_dim;
     return attention_impl(q, ld, k, v, ld, out, ld, batch, heads, q_len, kv_len, head_dim, scale,
                           bias, key_mask, mask_dtype, dtype, stream);
+}
+
+int bh_attention_noalloc(const void* q, const void* k, const void* v, void* out, int64_t batch,
+                         int64_t heads, int64_t q_len, int64_t kv_len, int64_t head_dim, float scale,
+                         const void* bias, const void* key_mask, int mask_dtype, int dtype,
+                         void* stream) {
+    const int64_t ld = heads * head_dim;
+    return attention_impl(q, ld, k, v, ld, out, ld, batch, heads, q_len, kv_len, head_dim, scale,
+                          bias, key_mask, mask_dtype, dtype, stream, true);
 }
 
 int bh_attention_strided(const void* q, int64_t ld_q, const void* k, const void* v, int64_t ld_kv,

@@ -320,6 +320,10 @@ void launch_attention_bf16(const bf16_t* q, const bf16_t* k, const bf16_t* v, bf
 // The V^T elements launch_attention_bf16 needs for these operands (0: the kernel reads V as is).
 int64_t attention_vt_elems(const bf16_t* q, const bf16_t* k, const bf16_t* v, const bf16_t* out,
                            const AttnShape& sh, const void* key_mask, const bf16_t* bias);
+// The allocation-free attention's scratch: a fixed device array of kNoAllocScratchBytes per device,
+// its address looked up (hipGetSymbolAddress) on the first call with that device current.
+constexpr int64_t kNoAllocScratchBytes = int64_t{32} << 20;
+bf16_t* noalloc_scratch();
 // Flash attention at head_dim 72 with V supplied transposed (flash72.hip): vt holds, for each
 // (b, h, d), a row of vt_ld >= flash72_vt_ld(kv_len) keys, zero past kv_len.
 int64_t flash72_vt_ld(int64_t kv_len);

@@ -86,6 +86,21 @@ int bh_attention(const void* q, const void* k, const void* v, void* out, int64_t
                  int64_t heads, int64_t q_len, int64_t kv_len, int64_t head_dim, float scale,
                  const void* bias, const void* key_mask, int mask_dtype, int dtype, void* stream);
 
+/* bh_attention without any allocation, for callers that cannot allocate: code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc. It has no counterpart in the
+ * reference. Same arguments, kernels and results as bh_attention; where bh_attention transposes V
+ * into a workspace it grows on demand (head_dim 72 and the single-head head_dim-512 kernel), this
+ * one uses a fixed array in the library's device memory of 32 MiB per device (V^T of
+ * batch x heads x 72 x kv_len rounded up to 64 keys, or 512 x kv_len rounded up to 32, bf16), and a
+ * call that needs more is refused with an error. The array's address is looked up by bh_init (or
+ * by the first call on a device). Every call on one device shares that array and each call
+ * rewrites all of it that it reads, so nothing carries over between calls; calls that overlap on
+ * one device (two streams, or two threads) race on it and must be ordered by the caller. */
+int bh_attention_noalloc(const void* q, const void* k, const void* v, void* out, int64_t batch,
+                         int64_t heads, int64_t q_len, int64_t kv_len, int64_t head_dim, float scale,
+                         const void* bias, const void* key_mask, int mask_dtype, int dtype,
+                         void* stream);
+
 /* The same op over row-strided operands: element (b,s,h,d) of q lives at
  * q[(b*q_len + s)*ld_q + h*head_dim + d], likewise k/v with ld_kv and out with ld_out.
  * Lets attention read Q,K,V straight out of one fused [M, 3*d] projection. No bias. */
