@@ -72,6 +72,10 @@ def parse() -> argparse.Namespace:
     p.add_argument("--caption-len", type=int, default=300)
     p.add_argument("--batch", type=int, default=2)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    p.add_argument("--headline-only", action="store_true",
+                   help="time the headline engine only: no device probe, row-split schedule, "
+                        "op-by-op plan or other resolutions (implies --no-cpu); for kernel traces "
+                        "whose every launch belongs to the headline step")
     p.add_argument("--cpu-threads", type=int, default=0)
     p.add_argument("--probe", choices=sorted(KERNEL_SHAPES),
                    help="for counter collection: run a 256 MiB device copy (calibration) and the "
@@ -139,6 +143,7 @@ KERNEL_SHAPES = {
     "gemm_qkv": ("gemm", (8192, 3456, 1152)),
     "gemm_ff0": ("gemm", (8192, 4608, 1152)),
     "gemm_ff2": ("gemm", (8192, 1152, 4608)),
+    "gemm_8192": ("gemm", (8192, 8192, 8192)),    # the reference probe's GEMM (device.cu:284-318)
     "attention_self": ("attention", (2, 16, 4096, 4096, 72)),
     "attention_cross": ("attention", (2, 16, 4096, 300, 72)),
     "norm_modulate": ("norm", (8192, 1152)),
@@ -655,7 +660,9 @@ def main() -> int:
     from burnisher_amd.workload import PIXART_SIGMA, dit_step_flops, make_workload
 
     bh.check(bh.lib().bh_init(0), "bh_init")
-    probed = device_probe()
+    if args.headline_only:
+        args.no_cpu = True
+    probed = {"mfma_tflops": None} if args.headline_only else device_probe()
     log(f"device probe: {json.dumps(probed)}")
     hw = HW[args.resolution]
     log(f"generating the {args.resolution}px workload (seeded synthetic bf16)")
@@ -714,6 +721,17 @@ def main() -> int:
     median_ms = synced_median(eng.step, stream, max(5, min(args.steps, 20)))
     log(f"profiler off: {plain_ms:.3f} ms/step; synchronised median {median_ms:.3f} ms")
 
+    # the engine's other row schedule: the two CFG rows on two streams (bh_dit_set_rows)
+    split_ms, split_equal = None, None
+    if wl.batch >= 2 and not args.headline_only:
+        bh.call("bh_dit_set_rows", eng.handle, bh.ROWS_SPLIT)
+        with torch.cuda.stream(stream):
+            eng.step()
+        split_ms = timed_steps(eng.step, stream, args.steps)
+        split_equal = bool(np.array_equal(eng.output(), got))
+        bh.call("bh_dit_set_rows", eng.handle, bh.ROWS_JOINED)
+        log(f"rows split over two streams: {split_ms:.3f} ms/step, output identical: {split_equal}")
+
     step_tflops = flops["total"] / (ms_per_step * 1e-3) / 1e12
     line = {
         "metric": METRIC,
@@ -738,16 +756,22 @@ def main() -> int:
         "timing": {"ms_per_step_events": round(ms_per_step, 4),
                    "ms_per_step_profiler_off": round(plain_ms, 4),
                    "sync_median_ms": round(median_ms, 4),
+                   "ms_per_step_rows_split": None if split_ms is None else round(split_ms, 4),
+                   "rows_split_output_identical": split_equal,
                    "basis": "value: K back-to-back steps between HIP events on the engine's stream, "
                             "with HIP events also around each launch of the dominant kernel (the "
                             "roofline's live measurement); profiler_off: the same with no event "
                             "inside a step; sync_median: the reference's method, each step timed "
-                            "on the host clock from launch to device synchronisation, median"},
+                            "on the host clock from launch to device synchronisation, median; "
+                            "rows_split: the same engine with its two CFG rows on two streams "
+                            "(BH_DIT_ROWS_SPLIT), profiler off -- not the value, whose per-launch "
+                            "roofline needs each launch to run alone"},
         "roofline": {"bound": "mfma", "kernel": dominant,
                      "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
                      "probed_peak": probed["mfma_tflops"],
-                     "probed_frac": round(achieved / probed["mfma_tflops"], 4),
+                     "probed_frac": (round(achieved / probed["mfma_tflops"], 4)
+                                     if probed["mfma_tflops"] else None),
                      "traffic": traffic_bytes(dominant, args.resolution),
                      "traffic_basis": "HBM bytes per launch: rocprofv3 FETCH_SIZE (x2.000) + "
                                       "WRITE_SIZE (x1.000), each scaled by a 256 MiB copy; "
@@ -757,7 +781,8 @@ def main() -> int:
         "step": {"flop": flops["total"], "tflops": round(step_tflops, 2),
                  "mfma_frac": round(step_tflops / PEAK_BF16_TFLOPS, 4),
                  "ceiling_ms": round(flops["total"] / (PEAK_BF16_TFLOPS * 1e12) * 1e3, 3),
-                 "probed_frac": round(step_tflops / probed["mfma_tflops"], 4)},
+                 "probed_frac": (round(step_tflops / probed["mfma_tflops"], 4)
+                                 if probed["mfma_tflops"] else None)},
         "probe": probed,
         "memory": {"peak_device_bytes": int(peak_bytes), "weights_bytes": int(weight_bytes),
                    "engine_workspace_bytes": eng.workspace(),
@@ -771,6 +796,9 @@ def main() -> int:
         "kernels": breakdown,
     }
     eng.close()
+    if args.headline_only:
+        print(json.dumps(line), flush=True)
+        return 0
 
     # the op-by-op plan (the registry drop-in path: one bh_* op per reference op), same steps
     op = Engine(wl, top, blocks, bh.DIT_OPWISE, stream)

@@ -21,6 +21,7 @@ ST_F32, ST_BF16, ST_F16, ST_F8_E4M3 = 0, 1, 2, 3
 ST_DTYPES = {ST_F32: "F32", ST_BF16: "BF16", ST_F16: "F16", ST_F8_E4M3: "F8_E4M3"}
 EPI_NONE, EPI_GELU, EPI_SILU, EPI_GELU_GATED = 0, 1, 2, 3
 DIT_FUSED, DIT_OPWISE = 0, 1
+ROWS_JOINED, ROWS_SPLIT = 0, 1
 (K_GEMM, K_GEMV, K_ATTN_SELF, K_ATTN_CROSS, K_NORM, K_ELEMENTWISE, K_GEMM_FF0, K_GEMM_FF2,
  K_GEMM_QKV) = range(9)
 KERNEL_CLASSES = ["gemm", "gemv", "attention_self", "attention_cross", "norm", "elementwise",
@@ -132,6 +133,7 @@ SIGNATURES = {
     "bh_dit_forward": ([_V, _V, _D, _V, _V, _I, _V, _V], _I),
     "bh_dit_workspace_bytes": ([_V], _I64),
     "bh_dit_position_table": ([_V, _V, _V], _I),
+    "bh_dit_set_rows": ([_V, _I], _I),
     "bh_scale": ([_V, _V, _I64, _F, _I, _V], _I),
     "bh_timestep_embedding": ([_D, _I, _I64, _V, _I, _V], _I),
     "bh_probe_device": ([_V, _V, _I64, ctypes.POINTER(ProbeResult)], _I),

@@ -190,6 +190,8 @@ struct DitGeometry {
     int mode;
 };
 DitGeometry dit_geometry(const bh_dit* e);
+// The engine's row schedule (BH_DIT_ROWS_*): a captured forward holds the schedule it ran.
+int dit_rows(const bh_dit* e);
 // bh_dit_forward without the C error boundary (throws Error). With caption_ready, a fused engine
 // reuses the caption projection and cross-attention K/V of its previous forward, which must have
 // had the same caption; the op-by-op plan always recomputes them.

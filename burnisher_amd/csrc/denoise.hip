@@ -300,6 +300,7 @@ struct bh_denoiser {
     const void* b_caption = nullptr;
     const void* b_mask = nullptr;
     int b_mask_dtype = -1;
+    int b_rows = -1;
     uint64_t b_version = 0;
     int end_warm = 0;
     int64_t end_pushes = 0;
@@ -548,7 +549,7 @@ int bh_denoiser_run(bh_denoiser* d, void* latent, const void* caption, const voi
                     "denoiser_run: graph capture needs an engine in BH_DIT_FUSED mode");
         const bool bound = d->exec && d->b_latent == latent && d->b_caption == caption &&
                            d->b_mask == caption_mask && d->b_mask_dtype == mask_dtype &&
-                           d->b_version == d->sched->version;
+                           d->b_version == d->sched->version && d->b_rows == bh::dit_rows(d->dit);
         if (!bound) {
             d->drop_graph();
             // Work already queued on `s` must not race the capture stream's first replay; the
@@ -572,6 +573,7 @@ int bh_denoiser_run(bh_denoiser* d, void* latent, const void* caption, const voi
             d->b_mask = caption_mask;
             d->b_mask_dtype = mask_dtype;
             d->b_version = d->sched->version;
+            d->b_rows = bh::dit_rows(d->dit);
             d->end_warm = d->sched->warm;
             d->end_pushes = d->sched->pushes;
         }

@@ -121,6 +121,17 @@ struct bh_dit {
     int64_t vt_ld_self = 0, vt_ld_cross = 0;
     bool vt72 = false;
     int64_t workspace = 0;
+    // Row-group schedule of the fused plan (BH_DIT_ROWS_*): the second row group's stream and the
+    // fork/join events, created with the engine when the batch has two or more rows.
+    int row_split = BH_DIT_ROWS_JOINED;
+    hipStream_t s2 = nullptr;
+    hipEvent_t fork_ev = nullptr, join_ev = nullptr;
+
+    ~bh_dit() {
+        if (fork_ev) (void)hipEventDestroy(fork_ev);
+        if (join_ev) (void)hipEventDestroy(join_ev);
+        if (s2) (void)hipStreamDestroy(s2);
+    }
 
     DevBuf make(int64_t elems) {
         workspace += elems * 2;
@@ -135,6 +146,8 @@ struct bh_dit {
 DitGeometry bh::dit_geometry(const bh_dit* e) {
     return DitGeometry{e->B, e->cfg.in_channels, e->cfg.out_channels, e->latent, e->mode};
 }
+
+int bh::dit_rows(const bh_dit* e) { return e->row_split; }
 
 namespace {
 
@@ -316,97 +329,131 @@ void forward_fused(bh_dit& e, const void* latent, double t, const void* caption,
     }
     const float scale = 1.0f / std::sqrt(static_cast<float>(Dh));
     const bool mask_f32 = mask_dtype == BH_F32;
-    for (int64_t l = 0; l < L; ++l) {
-        const bh_dit_block_weights& bw = e.blocks[l];
-        const bf16_t* ch = e.chunks.bf() + l * 6 * B * d;   // [6][B][d]
-        const bf16_t* shift_msa = ch, *scale_msa = ch + B * d, *gate_msa = ch + 2 * B * d;
-        const bf16_t* shift_mlp = ch + 3 * B * d, *scale_mlp = ch + 4 * B * d;
-        const bf16_t* gate_mlp = ch + 5 * B * d;
-        const float* chf = static_cast<const float*>(e.chunks_f32.p) + l * 6 * B * d;
-        const bf16_t* wqkv = e.w_qkv.bf() + l * 3 * d * d;
-        const bf16_t* bqkv = e.b_qkv.bf() + l * 3 * d;
+    const size_t mask_elem = mask_f32 ? 4 : 2;
+    const float* chunks_f32 = static_cast<const float*>(e.chunks_f32.p);
 
-        // 1. self-attention
-        {
-            ProfileScope ps(K_NORM, s, 4.0 * M * d);
-            if (e.chunks_f32.p)
-                launch_norm_modulate_f32(e.x.bf(), chf, chf + B * d, e.modded.bf(), B, N, d, eps, s);
-            else
-                launch_norm_modulate_pre(e.x.bf(), shift_msa, scale_msa, e.modded.bf(), B, N, d, eps, s);
-        }
-        {   // Q and K into the [M, 3d] buffer; at head_dim 72, V straight into V^T for the
-            // attention kernel (other widths keep V in the buffer for the generic attention)
-            SubclassScope sc(K_GEMM_QKV);
-            GemmEpilogue ep;
-            if (e.vt72) {
-                ep.vt = e.vt_self.bf();
-                ep.vt_period = 3 * d;
-                ep.vt_col0 = 2 * d;
-                ep.vt_seq = N;
-                ep.vt_ld = e.vt_ld_self;
-                ep.vt_heads = static_cast<int>(H);
-                ep.vt_dim = static_cast<int>(Dh);
-            }
-            gemm(e.modded.bf(), wqkv, bqkv, e.qkv.bf(), M, 3 * d, d, ep, s);
-        }
-        if (e.vt72) {
-            launch_flash72(e.qkv.bf(), 3 * d, e.qkv.bf() + d, 3 * d, e.vt_self.bf(), e.vt_ld_self,
-                           e.ctx.bf(), d, B, H, N, N, scale, nullptr, false, s);
+    // Every per-row buffer is batch-major, so rows [b0, b0 + nb) of the batch are one contiguous
+    // slice of each: a row group is the same launches on offset pointers with batch nb.
+    struct Rows {
+        int64_t b0, nb;
+        hipStream_t s;
+    };
+    // LayerNorm + modulation of x into `modded` with chunk pair (shift c, scale c + 1).
+    auto norm = [&](int64_t l, int c, const Rows& g) {
+        const int64_t o = g.b0 * N * d;
+        ProfileScope ps(K_NORM, g.s, 4.0 * g.nb * N * d);
+        if (chunks_f32) {
+            const float* chf = chunks_f32 + (l * 6 + c) * B * d + g.b0 * d;
+            launch_norm_modulate_f32(e.x.bf() + o, chf, chf + B * d, e.modded.bf() + o, g.nb, N, d, eps,
+                                     g.s);
         } else {
-            launch_attention_bf16(e.qkv.bf(), e.qkv.bf() + d, e.qkv.bf() + 2 * d, e.ctx.bf(),
-                                  AttnShape{B, H, N, N, Dh, 3 * d, 3 * d, d, scale}, nullptr,
-                                  false, s, nullptr, e.vt_op.bf(), e.vt_op_elems);
+            const bf16_t* ch = e.chunks.bf() + (l * 6 + c) * B * d + g.b0 * d;
+            launch_norm_modulate_pre(e.x.bf() + o, ch, ch + B * d, e.modded.bf() + o, g.nb, N, d, eps,
+                                     g.s);
         }
+    };
+    // 1a. norm, then Q and K into the [M, 3d] buffer; at head_dim 72, V straight into V^T for
+    // the attention kernel (other widths keep V in the buffer for the generic attention)
+    auto qkv = [&](int64_t l, const Rows& g) {
+        norm(l, 0, g);
+        SubclassScope sc(K_GEMM_QKV);
+        GemmEpilogue ep;
+        if (e.vt72) {
+            ep.vt = e.vt_self.bf() + g.b0 * H * Dh * e.vt_ld_self;
+            ep.vt_period = 3 * d;
+            ep.vt_col0 = 2 * d;
+            ep.vt_seq = N;
+            ep.vt_ld = e.vt_ld_self;
+            ep.vt_heads = static_cast<int>(H);
+            ep.vt_dim = static_cast<int>(Dh);
+        }
+        gemm(e.modded.bf() + g.b0 * N * d, e.w_qkv.bf() + l * 3 * d * d, e.b_qkv.bf() + l * 3 * d,
+             e.qkv.bf() + g.b0 * N * 3 * d, g.nb * N, 3 * d, d, ep, g.s);
+    };
+    // 1b. self-attention into ctx
+    auto self_attention = [&](const Rows& g) {
+        const bf16_t* q = e.qkv.bf() + g.b0 * N * 3 * d;
+        bf16_t* ctx = e.ctx.bf() + g.b0 * N * d;
+        if (e.vt72) {
+            launch_flash72(q, 3 * d, q + d, 3 * d, e.vt_self.bf() + g.b0 * H * Dh * e.vt_ld_self,
+                           e.vt_ld_self, ctx, d, g.nb, H, N, N, scale, nullptr, false, g.s);
+        } else {
+            launch_attention_bf16(q, q + d, q + 2 * d, ctx, AttnShape{g.nb, H, N, N, Dh, 3 * d, 3 * d, d, scale},
+                                  nullptr, false, g.s, nullptr, e.vt_op.bf(), e.vt_op_elems);
+        }
+    };
+    // 1c-3. the gated out-projection, the cross-attention block and the feed-forward block
+    auto rest = [&](int64_t l, const Rows& g) {
+        const bh_dit_block_weights& bw = e.blocks[l];
+        const int64_t rows = g.nb * N, o = g.b0 * N * d;
+        bf16_t* x = e.x.bf() + o;
+        bf16_t* ctx = e.ctx.bf() + o;
+        const bf16_t* ch = e.chunks.bf() + l * 6 * B * d + g.b0 * d;   // [6][B][d], this group's rows
         {
             GemmEpilogue ep;
             ep.round_mid = true;
-            ep.residual = e.x.bf();
-            ep.gate = gate_msa;
+            ep.residual = x;
+            ep.gate = ch + 2 * B * d;
             ep.gate_rows = N;
-            gemm(e.ctx.bf(), bw.attn1_o_w, bw.attn1_o_b, e.x.bf(), M, d, d, ep, s);
+            gemm(ctx, bw.attn1_o_w, bw.attn1_o_b, x, rows, d, d, ep, g.s);
         }
         // 2. cross-attention (no norm before it: pixart_dit.cpp:251-253)
-        gemm(e.x.bf(), bw.attn2_q_w, bw.attn2_q_b, e.q2.bf(), M, d, d, plain, s);
+        bf16_t* q2 = e.q2.bf() + o;
+        gemm(x, bw.attn2_q_w, bw.attn2_q_b, q2, rows, d, d, plain, g.s);
+        const bf16_t* kv = e.kv_all.bf() + g.b0 * e.cap_len * L * 2 * d + l * 2 * d;
+        const void* m = static_cast<const char*>(mask) + g.b0 * e.cap_len * mask_elem;
         if (e.vt72) {
-            launch_flash72(e.q2.bf(), d, e.kv_all.bf() + l * 2 * d, L * 2 * d,
-                           e.vt_cross.bf() + l * B * H * Dh * e.vt_ld_cross, e.vt_ld_cross,
-                           e.ctx.bf(), d, B, H, N, e.cap_len, scale, mask, mask_f32, s);
+            launch_flash72(q2, d, kv, L * 2 * d,
+                           e.vt_cross.bf() + (l * B + g.b0) * H * Dh * e.vt_ld_cross, e.vt_ld_cross,
+                           ctx, d, g.nb, H, N, e.cap_len, scale, m, mask_f32, g.s);
         } else {
-            launch_attention_bf16(e.q2.bf(), e.kv_all.bf() + l * 2 * d,
-                                  e.kv_all.bf() + l * 2 * d + d, e.ctx.bf(),
-                                  AttnShape{B, H, N, e.cap_len, Dh, d, L * 2 * d, d, scale}, mask,
-                                  mask_f32, s, nullptr, e.vt_op.bf(), e.vt_op_elems);
+            launch_attention_bf16(q2, kv, kv + d, ctx, AttnShape{g.nb, H, N, e.cap_len, Dh, d, L * 2 * d, d, scale},
+                                  m, mask_f32, g.s, nullptr, e.vt_op.bf(), e.vt_op_elems);
         }
         {
             GemmEpilogue ep;
             ep.round_mid = true;
-            ep.residual = e.x.bf();
-            gemm(e.ctx.bf(), bw.attn2_o_w, bw.attn2_o_b, e.x.bf(), M, d, d, ep, s);
+            ep.residual = x;
+            gemm(ctx, bw.attn2_o_w, bw.attn2_o_b, x, rows, d, d, ep, g.s);
         }
         // 3. feed-forward
-        {
-            ProfileScope ps(K_NORM, s, 4.0 * M * d);
-            if (e.chunks_f32.p)
-                launch_norm_modulate_f32(e.x.bf(), chf + 3 * B * d, chf + 4 * B * d, e.modded.bf(), B,
-                                         N, d, eps, s);
-            else
-                launch_norm_modulate_pre(e.x.bf(), shift_mlp, scale_mlp, e.modded.bf(), B, N, d, eps, s);
-        }
+        norm(l, 3, g);
+        bf16_t* ff0 = e.ff0.bf() + g.b0 * N * e.dff;
         {
             SubclassScope sc(K_GEMM_FF0);
             GemmEpilogue gelu;
             gelu.act = 1;
-            gemm(e.modded.bf(), bw.ff0_w, bw.ff0_b, e.ff0.bf(), M, e.dff, d, gelu, s);
+            gemm(e.modded.bf() + o, bw.ff0_w, bw.ff0_b, ff0, rows, e.dff, d, gelu, g.s);
         }
         {
             SubclassScope sc(K_GEMM_FF2);
             GemmEpilogue ep;
             ep.round_mid = true;
-            ep.residual = e.x.bf();
-            ep.gate = gate_mlp;
+            ep.residual = x;
+            ep.gate = ch + 5 * B * d;
             ep.gate_rows = N;
-            gemm(e.ff0.bf(), bw.ff2_w, bw.ff2_b, e.x.bf(), M, d, e.dff, ep, s);
+            gemm(ff0, bw.ff2_w, bw.ff2_b, x, rows, d, e.dff, ep, g.s);
         }
+    };
+
+    auto blocks = [&](const Rows& g) {
+        for (int64_t l = 0; l < L; ++l) {
+            qkv(l, g);
+            self_attention(g);
+            rest(l, g);
+        }
+    };
+    if (B < 2 || e.row_split == BH_DIT_ROWS_JOINED) {
+        blocks(Rows{0, B, s});
+    } else {
+        // The second group waits for everything before the block loop (on s); s waits for the
+        // second group's last launch before the output head.
+        hip_check(hipEventRecord(e.fork_ev, s), "hipEventRecord");
+        hip_check(hipStreamWaitEvent(e.s2, e.fork_ev, 0), "hipStreamWaitEvent");
+        blocks(Rows{0, (B + 1) / 2, s});
+        blocks(Rows{(B + 1) / 2, B / 2, e.s2});
+        hip_check(hipEventRecord(e.join_ev, e.s2), "hipEventRecord");
+        hip_check(hipStreamWaitEvent(s, e.join_ev, 0), "hipStreamWaitEvent");
     }
 
     // output head: shift = emb_t + table[0], scale = emb_t + table[1] (pixart_dit.cpp:287-294)
@@ -550,6 +597,11 @@ int bh_dit_create(const bh_dit_config* cfg, const bh_dit_weights* w, int64_t bat
             hip_check(hipMemcpy(e->tables_dev.p, tables.data(), sizeof(void*) * L,
                                 hipMemcpyHostToDevice),
                       "hipMemcpy");
+            if (batch >= 2) {   // the row-split schedule's second stream (default priority)
+                hip_check(hipStreamCreateWithFlags(&e->s2, hipStreamNonBlocking), "hipStreamCreate");
+                hip_check(hipEventCreateWithFlags(&e->fork_ev, hipEventDisableTiming), "hipEventCreate");
+                hip_check(hipEventCreateWithFlags(&e->join_ev, hipEventDisableTiming), "hipEventCreate");
+            }
         }
         hip_check(hipDeviceSynchronize(), "hipDeviceSynchronize");
         *out = e.release();
@@ -594,6 +646,17 @@ int bh_dit_position_table(const bh_dit* e, void* out, void* stream) {
         require(e != nullptr, "dit_position_table: null engine");
         require_device_ptr(out, "dit_position_table", "out");
         d2d(out, e->pos_table.p, e->pos_table.bytes, static_cast<hipStream_t>(stream));
+    });
+}
+
+int bh_dit_set_rows(bh_dit* e, int rows) {
+    return guarded([&] {
+        require(e != nullptr, "dit_set_rows: null engine");
+        require(rows == BH_DIT_ROWS_JOINED || rows == BH_DIT_ROWS_SPLIT,
+                "dit_set_rows: unknown row schedule " + std::to_string(rows));
+        require(rows == BH_DIT_ROWS_JOINED || e->mode == BH_DIT_FUSED,
+                "dit_set_rows: the op-by-op plan runs the reference graph on the caller's stream only");
+        e->row_split = rows;
     });
 }
 

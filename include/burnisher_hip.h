@@ -287,6 +287,24 @@ int64_t bh_dit_workspace_bytes(const bh_dit* e);
  * src/models/pixart_dit.cpp:53-105: fp64 on the host, interpolation scale 2, base
  * sample_size / patch_size, stored bf16), [grid*grid, hidden], into the device buffer `out`. */
 int bh_dit_position_table(const bh_dit* e, void* out, void* stream);
+
+/* How the fused plan schedules the batch rows (the CFG pair). No counterpart in the reference,
+ * whose graph runs the whole batch through each op in turn; the result is bit-identical under
+ * every schedule (rows never mix). */
+typedef enum {
+    /* The whole batch through each launch, on the caller's stream (the default). */
+    BH_DIT_ROWS_JOINED = 0,
+    /* The rows in two groups, each on its own stream from the block loop's start to the output
+     * head: one group's launch tails and epilogues overlap the other group's work (measured
+     * 1.1% faster at 1024px, 1.4% at 2048px). The second stream is the engine's own (default
+     * priority); it joins the caller's stream by events, so a forward on a capturing stream is
+     * captured whole. Each launch then covers half the batch and runs beside the other half's,
+     * so per-launch kernel timings no longer describe a kernel alone. */
+    BH_DIT_ROWS_SPLIT = 1
+} bh_dit_rows;
+/* Selects the row schedule of a fused engine (an op-by-op engine refuses any but JOINED). With a
+ * batch of one every schedule runs as JOINED. */
+int bh_dit_set_rows(bh_dit* e, int rows);
 void bh_dit_destroy(bh_dit* e);
 
 /* ---- the denoise loop around the dit-step (pipeline.cpp:104-131) -------------------------- */

@@ -99,6 +99,47 @@ def test_fused_plan_equals_opwise_plan(hip):
         b.close()
 
 
+@pytest.mark.parametrize("cfg,batch,hw,cap,layers", [
+    (PIXART_SIGMA, 2, 64, 300, 2),   # the CFG pair at 512px: one row per stream, head_dim 72
+    (SMALL, 3, 8, 5, None),          # groups of two rows and one, the generic attention
+], ids=["512px_b2", "small_b3"])
+def test_row_schedules_are_bit_identical(hip, cfg, batch, hw, cap, layers):
+    # Rows never mix, so running the two row groups on two streams changes no bit of the output,
+    # forward after forward.
+    import burnisher_amd as bh
+    wl = make_workload(cfg, batch=batch, latent_hw=hw, caption_len=cap, layers=layers)
+    e = Engine(wl, 0)
+    try:
+        joined = e.forward()
+        bh.call("bh_dit_set_rows", e.handle, bh.ROWS_SPLIT)
+        print(f"split rows, batch {batch}", flush=True)
+        for rep in range(2):
+            assert np.array_equal(e.forward(), joined), f"split rows, forward {rep}"
+        # the caption is read per row group too: a new mask reaches the output under the split
+        import torch
+        bh.call("bh_dit_set_rows", e.handle, bh.ROWS_JOINED)
+        want = e.forward(mask=torch.ones_like(e.mask))
+        bh.call("bh_dit_set_rows", e.handle, bh.ROWS_SPLIT)
+        assert np.array_equal(e.forward(mask=torch.ones_like(e.mask)), want)
+    finally:
+        e.close()
+
+
+def test_row_schedule_refusals(hip):
+    import burnisher_amd as bh
+    wl = make_workload(SMALL, batch=2, latent_hw=8, caption_len=5)
+    fused, opwise = Engine(wl, 0), Engine(wl, 1)
+    try:
+        with pytest.raises(bh.BurnisherError, match="unknown row schedule"):
+            bh.call("bh_dit_set_rows", fused.handle, 2)
+        with pytest.raises(bh.BurnisherError, match="op-by-op"):
+            bh.call("bh_dit_set_rows", opwise.handle, bh.ROWS_SPLIT)
+        bh.call("bh_dit_set_rows", opwise.handle, bh.ROWS_JOINED)
+    finally:
+        fused.close()
+        opwise.close()
+
+
 def test_two_blocks_512px_matches_oracle(hip):
     wl = make_workload(PIXART_SIGMA, batch=2, latent_hw=64, caption_len=300, layers=2)
     e = Engine(wl, 0)
