@@ -27,11 +27,14 @@
 // the end of their matrix phases (the shorter ones).
 //
 // Softmax: scores stay fp32; exp2(s * scale * log2e - m) with the running maximum m kept in those
-// units. The first block sets m; a later block moves it (and rescales O by exp2(m_old - m_new))
-// only when one of its scores exceeds it by more than 8: any fixed m gives the same normalised
-// result, and the threshold bounds every P by 2^8, far from fp32 range. The common path then
-// needs no maximum per query at all -- one per lane and a wave vote decide -- which matters
-// because this kernel's vector phase, not its MFMAs, sets the pace.
+// units. Q is multiplied by c = scale * log2e once, as it is loaded (one extra bf16 rounding of
+// q c), and the score MFMAs of a block start from the accumulator value -m, so the matrix cores
+// deliver s c - m and the vector phase spends no operation per score on it. The first block
+// sets m (its scores are formed against 0); a later block moves it (and rescales O by
+// exp2(m_old - m_new)) only when one of its scores exceeds it by more than 8: any fixed m gives
+// the same normalised result, and the threshold bounds every P by 2^8, far from fp32 range. The
+// common path then needs no maximum per query at all -- one per lane and a wave vote decide --
+// which matters because this kernel's vector phase is as long as its matrix phase.
 //
 // Numerics against the reference oracle (ops_cpu.cpp:84-131): a masked key scores exactly -1e9
 // there, so with any unmasked key in the row its weight exp(-1e9 - max) is exactly 0 -- here it
@@ -235,13 +238,13 @@ struct WaveState {
 template <bool OUT, bool SCORES>
 __device__ __forceinline__ void matrix_phase(WaveState& w, const char* vstage, const int (&vbase)[2],
                                              const char* kstage, int kbase) {
-    constexpr int kVF = 10;   // V^T fragments (e, cc)
+    constexpr int kVF = 10;        // V^T fragments (e, cc)
+    constexpr int kKF = 3 * kKT;   // K fragments in MFMA order: p = 4 ks + t
     bf16x8_t vf[kVF];
-    bf16x8_t kf[kKT][3];
+    bf16x8_t kf[kKF];
     auto read_v = [&](int i) { vf[i] = ld_frag(vstage + vbase[i & 1] + (i >> 1) * 16 * 128); };
-    auto read_k = [&](int t) {
-#pragma unroll
-        for (int ks = 0; ks < 3; ++ks) kf[t][ks] = ld_frag(kstage + kbase + t * 16 * kKRow + ks * 64);
+    auto read_k = [&](int p) {
+        kf[p] = ld_frag(kstage + kbase + (p % kKT) * 16 * kKRow + (p / kKT) * 64);
     };
     if (OUT) {
         read_v(0);
@@ -253,22 +256,27 @@ __device__ __forceinline__ void matrix_phase(WaveState& w, const char* vstage, c
             for (int u = 0; u < kQT; ++u)
                 w.o[i >> 1][u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf[i], w.pf[u][i & 1], w.o[i >> 1][u], 0, 0, 0);
             if (i + 3 < kVF) read_v(i + 3);
-            else if (SCORES && i + 3 - kVF < 2) read_k(i + 3 - kVF);
+            else if (SCORES && i >= kVF - 2) read_k(i - (kVF - 2));
         }
     } else if (SCORES) {
         read_k(0);
         read_k(1);
     }
     if (SCORES) {
+        // The first K step accumulates onto -m, so the scores come out as s c - m (Q holds c).
+        // Step-outer, so -m is live for the first step only; each K fragment is read two
+        // fragments (eight MFMAs) ahead of its use.
+        f32x4_t negm[kQT];
 #pragma unroll
-        for (int t = 0; t < kKT; ++t) {
+        for (int u = 0; u < kQT; ++u) negm[u] = f32x4_t{-w.mc[u], -w.mc[u], -w.mc[u], -w.mc[u]};
 #pragma unroll
-            for (int ks = 0; ks < 3; ++ks)
+        for (int p = 0; p < kKF; ++p) {
+            const int t = p % kKT, ks = p / kKT;
 #pragma unroll
-                for (int u = 0; u < kQT; ++u)
-                    w.s[t][u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                        kf[t][ks], w.qf[u][ks], ks == 0 ? f32x4_t{0.f, 0.f, 0.f, 0.f} : w.s[t][u], 0, 0, 0);
-            if (t + 2 < kKT) read_k(t + 2);
+            for (int u = 0; u < kQT; ++u)
+                w.s[t][u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                    kf[p], w.qf[u][ks], ks == 0 ? negm[u] : w.s[t][u], 0, 0, 0);
+            if (p + 2 < kKF) read_k(p + 2);
         }
     }
     // the issue order
@@ -277,24 +285,16 @@ __device__ __forceinline__ void matrix_phase(WaveState& w, const char* vstage, c
 #pragma unroll
         for (int i = 0; i < kVF; ++i) {
             __builtin_amdgcn_sched_group_barrier(0x008, kQT, 0);
-            if (i + 3 < kVF) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-            else if (SCORES && i + 3 - kVF < 2) __builtin_amdgcn_sched_group_barrier(0x100, 3, 0);
+            if (i + 3 < kVF || (SCORES && i >= kVF - 2)) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
         }
     } else if (SCORES) {
-        __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
     }
     if (SCORES) {
 #pragma unroll
-        for (int t = 0; t < kKT; ++t) {
-            if (t + 2 < kKT) {
-#pragma unroll
-                for (int ks = 0; ks < 3; ++ks) {
-                    __builtin_amdgcn_sched_group_barrier(0x008, kQT, 0);
-                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-                }
-            } else {
-                __builtin_amdgcn_sched_group_barrier(0x008, 3 * kQT, 0);
-            }
+        for (int p = 0; p < kKF; ++p) {
+            __builtin_amdgcn_sched_group_barrier(0x008, kQT, 0);
+            if (p + 2 < kKF) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
         }
     }
 }
@@ -309,10 +309,10 @@ __device__ __forceinline__ float lane_max2(float m, bool swap32) {
 // Softmax of the block whose scores are in w.s: masking, the block maximum (the 64 keys of a
 // query sit in lanes lr, lr+16, lr+32, lr+48), the lazy rescale, P = exp2(s c - m) in bf16,
 // regrouped into w.pf.
-template <bool MASKED>
+template <bool MASKED, bool FIRST>
 __device__ __forceinline__ void softmax(WaveState& w, const Flash72Args& a, int blk,
-                                        unsigned long long bits_all, bool all_masked, int g,
-                                        bool first) {
+                                        unsigned long long bits_all, bool all_masked, int g) {
+    constexpr bool first = FIRST;   // a compile-time branch: a run-time one keeps both forms of S live
     if (MASKED) {
         const unsigned long long bits = bits_all >> (4 * g);
         const unsigned long long inrange =
@@ -344,16 +344,17 @@ __device__ __forceinline__ void softmax(WaveState& w, const Flash72Args& a, int 
             m = fmaxf(m, w.s[3][u][3]);
             m = lane_max2(m, true);
             m = lane_max2(m, false);
-            w.mc[u] = m * a.c;
+            w.mc[u] = m;
         }
+        // x = s c - m in place (the first block's scores were formed against m = 0); later
+        // blocks' scores arrive as s c - m from the matrix cores
+#pragma unroll
+        for (int t = 0; t < kKT; ++t)
+#pragma unroll
+            for (int u = 0; u < kQT; ++u)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) w.s[t][u][r] -= w.mc[u];
     }
-    // x = s c - m in place, in the units of the running maximum
-#pragma unroll
-    for (int t = 0; t < kKT; ++t)
-#pragma unroll
-        for (int u = 0; u < kQT; ++u)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) w.s[t][u][r] = __builtin_fmaf(w.s[t][u][r], a.c, -w.mc[u]);
     if (!first) {
         // Later blocks move the maximum only when one of their scores exceeds it by more than
         // the threshold: one maximum over this lane's 64 values and a wave vote decide; the exact
@@ -510,11 +511,20 @@ __global__ void __launch_bounds__(kThreads, 1) k_flash72(Flash72Args a) {
 #pragma unroll
         for (int u = 0; u < kQT; ++u) w.o[e][u] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int u = 0; u < kQT; ++u) w.mc[u] = -INFINITY;
+    for (int u = 0; u < kQT; ++u) w.mc[u] = 0.0f;   // the first block's scores are formed against 0
 
     // The Q loads are drained here, where the compiler sees it: otherwise it waits for them
     // (vmcnt(0), which also drains the DMA in flight) at their first use in every phase.
     s_waitcnt<0, 15>();
+    // Q carries the score scale in log2 units, c = scale log2(e), rounded to bf16 once here, so
+    // the matrix cores deliver s c - m and the softmax spends no multiply-add per score.
+#pragma unroll
+    for (int u = 0; u < kQT; ++u)
+#pragma unroll
+        for (int ks = 0; ks < 3; ++ks)
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                w.qf[u][ks][e] = static_cast<__bf16>(static_cast<float>(w.qf[u][ks][e]) * a.c);
 
     // ---- the phases ----
     // Phase p is bracketed by workgroup barriers. Block j (position j of the live list) sits in
@@ -542,10 +552,10 @@ __global__ void __launch_bounds__(kThreads, 1) k_flash72(Flash72Args a) {
         wait_and_join<0>();
         auto res_stage = [&](int j) -> char* { return smem + j * kStage; };
         matrix_phase<false, true>(w, nullptr, vbase, res_stage(0), kbase);
-        softmax<MASKED>(w, a, live[0], bits_of(0), all_masked, g, true);
+        softmax<MASKED, true>(w, a, live[0], bits_of(0), all_masked, g);
         for (int j = 1; j < n; ++j) {
             matrix_phase<true, true>(w, res_stage(j - 1), vbase, res_stage(j), kbase);
-            softmax<MASKED>(w, a, live[j], bits_of(j), all_masked, g, false);
+            softmax<MASKED, false>(w, a, live[j], bits_of(j), all_masked, g);
         }
         matrix_phase<true, false>(w, res_stage(n - 1), vbase, nullptr, kbase);
     } else {
@@ -565,15 +575,25 @@ __global__ void __launch_bounds__(kThreads, 1) k_flash72(Flash72Args a) {
         wait_and_join<kDmaPerWave>();                            // phase 0: block 0 has landed
         matrix_phase<false, true>(w, nullptr, vbase, stage_of(0), kbase);
         issue(2);
-        for (int j = 1; j < n; ++j) {
-            wait_and_join<63>();                                 // phase 2j-1
-            softmax<MASKED>(w, a, live[j - 1], bits_of(j - 1), all_masked, g, j == 1);
-            wait_and_join<kDmaPerWave>();                        // phase 2j: block j has landed
-            matrix_phase<true, true>(w, stage_of(j - 1), vbase, stage_of(j), kbase);
-            issue(j + 2);
+        if (n > 1) {   // block 0's softmax peeled off, so FIRST is known at compile time
+            wait_and_join<63>();                                 // phase 1
+            softmax<MASKED, true>(w, a, live[0], bits_of(0), all_masked, g);
+            wait_and_join<kDmaPerWave>();                        // phase 2: block 1 has landed
+            matrix_phase<true, true>(w, stage_of(0), vbase, stage_of(1), kbase);
+            issue(3);
+            for (int j = 2; j < n; ++j) {
+                wait_and_join<63>();                             // phase 2j-1
+                softmax<MASKED, false>(w, a, live[j - 1], bits_of(j - 1), all_masked, g);
+                wait_and_join<kDmaPerWave>();                    // phase 2j: block j has landed
+                matrix_phase<true, true>(w, stage_of(j - 1), vbase, stage_of(j), kbase);
+                issue(j + 2);
+            }
+            wait_and_join<63>();                                 // phase 2n-1
+            softmax<MASKED, false>(w, a, live[n - 1], bits_of(n - 1), all_masked, g);
+        } else {
+            wait_and_join<63>();                                 // phase 1
+            softmax<MASKED, true>(w, a, live[0], bits_of(0), all_masked, g);
         }
-        wait_and_join<63>();                                     // phase 2n-1
-        softmax<MASKED>(w, a, live[n - 1], bits_of(n - 1), all_masked, g, n == 1);
         wait_and_join<63>();                                     // phase 2n
         matrix_phase<true, false>(w, stage_of(n - 1), vbase, nullptr, kbase);
         wait_and_join<63>();                                     // phase 2n+1
@@ -583,12 +603,12 @@ __global__ void __launch_bounds__(kThreads, 1) k_flash72(Flash72Args a) {
         wait_and_join<63>();                                     // phase 1
         matrix_phase<false, true>(w, nullptr, vbase, stage_of(0), kbase);
         wait_and_join<63>();                                     // phase 2
-        softmax<MASKED>(w, a, live[0], bits_of(0), all_masked, g, true);
+        softmax<MASKED, true>(w, a, live[0], bits_of(0), all_masked, g);
         for (int j = 1; j < n; ++j) {
             wait_and_join<63>();                                 // phase 2j+1
             matrix_phase<true, true>(w, stage_of(j - 1), vbase, stage_of(j), kbase);
             wait_and_join<63>();                                 // phase 2j+2
-            softmax<MASKED>(w, a, live[j], bits_of(j), all_masked, g, false);
+            softmax<MASKED, false>(w, a, live[j], bits_of(j), all_masked, g);
         }
         wait_and_join<63>();                                     // phase 2n+1
         matrix_phase<true, false>(w, stage_of(n - 1), vbase, nullptr, kbase);
