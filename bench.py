@@ -832,6 +832,22 @@ def main() -> int:
                               "mfma_frac": round(of["total"] / (o_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
                               "finite": bool(np.all(np.isfinite(fo)))}
         log(f"{res}px: {o_ms:.3f} ms/step")
+    # one block at 512px, batch 1, a 120-token caption (block 0's weights)
+    cwl = make_workload(PIXART_SIGMA, batch=1, latent_hw=64, caption_len=120, layers=0)
+    cwl.cfg["num_layers"] = 1
+    ce = Engine(cwl, top, blocks[:1], bh.DIT_FUSED, stream)
+    with torch.cuda.stream(stream):
+        ce.step()
+    c_ms = timed_steps(ce.step, stream, 20)
+    c_med = synced_median(ce.step, stream, 20)
+    cf = dit_step_flops(cwl.cfg, batch=1, latent_hw=64, caption_len=120)
+    cres = ce.output()
+    ce.close()
+    others["config0_block_512px_b1_cap120"] = {
+        "ms_per_step": round(c_ms, 4), "sync_median_ms": round(c_med, 4), "flop": cf["total"],
+        "mfma_frac": round(cf["total"] / (c_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+        "finite": bool(np.all(np.isfinite((cres.astype(np.uint32) << 16).view(np.float32))))}
+    log(f"configs[0] (one block, 512px, B=1, caption 120): {c_ms:.3f} ms, median {c_med:.3f} ms")
     line["other_configs"] = others
     del top, blocks
     torch.cuda.empty_cache()
