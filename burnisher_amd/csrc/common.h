@@ -222,6 +222,13 @@ struct GemmEpilogue {
     bf16_t* vt = nullptr;
     int64_t vt_period = 0, vt_col0 = 0, vt_seq = 0, vt_ld = 0;
     int vt_heads = 0, vt_dim = 72;
+    // Split-K (GEMMs with too few output tiles to fill the CUs): 0 lets the shape decide
+    // (gemm_splits), 1 never splits, n >= 2 sums exactly n K slices. The fp32 partials go to
+    // `splitk_ws` (splitk_ws_floats floats, at least splits * m * n) or, when it is null, to a
+    // per-device library buffer grown on demand (calls that overlap on one device share it).
+    int splitk = 0;
+    float* splitk_ws = nullptr;
+    int64_t splitk_ws_floats = 0;
 };
 
 // A 3x3, stride-1, pad-1 convolution read as a GEMM (batch 1, NHWC): out[H*W, c_out] =
@@ -296,6 +303,11 @@ void launch_gemm_bf16(const bf16_t* a, const bf16_t* b, const bf16_t* bias, bf16
 // Split-K for GEMMs with too few output tiles to fill the CUs: the number of K slices (1: none)
 // that keeps every slice's workgroups resident at once.
 int gemm_splitk_choice(int64_t m, int64_t n, int64_t k);
+// The K slices launch_gemm_bf16 uses for this shape and epilogue when ep.splitk is 0 (1: none):
+// gemm_splitk_choice when K holds at least 48 k-tiles, at most half the CUs would hold a tile, the
+// MFMA kernel applies and the epilogue is a plain, residual or gated store (no row add, no
+// transposed V).
+int gemm_splits(int64_t m, int64_t n, int64_t k, const GemmEpilogue& ep);
 // out = bf16(residual + bf16(A . B^T)) through `splits` fp32 partials (partial holds
 // splits * m * n floats) summed in slice order; out may alias residual.
 void launch_gemm_splitk_residual(const bf16_t* a, const bf16_t* b, float* partial, int splits,

@@ -126,6 +126,8 @@ struct bh_dit {
     int row_split = BH_DIT_ROWS_JOINED;
     hipStream_t s2 = nullptr;
     hipEvent_t fork_ev = nullptr, join_ev = nullptr;
+    DevBuf splitk;                    // fp32 split-K partials of the fused plan's long-K GEMMs
+    int64_t splitk_floats = 0;
 
     ~bh_dit() {
         if (fork_ev) (void)hipEventDestroy(fork_ev);
@@ -260,10 +262,22 @@ struct SubclassScope {
     ~SubclassScope() { set_gemm_subclass(-1); }
 };
 
-void gemm(const bf16_t* a, const void* w, const void* b, bf16_t* out, int64_t m, int64_t n,
-          int64_t k, const GemmEpilogue& ep, hipStream_t s) {
+// Every engine GEMM decides its K split (gemm_splits) on the full batch, so a row group sums
+// exactly the slices the whole batch would, and keeps its fp32 partials in the engine's own buffer
+// at its rows, so a captured forward holds no library-owned pointer and row groups never share.
+void gemm(bh_dit& e, const bf16_t* a, const void* w, const void* b, bf16_t* out, int64_t m,
+          int64_t n, int64_t k, const GemmEpilogue& ep, hipStream_t s, int64_t row0 = 0,
+          int64_t rows_full = -1) {
+    GemmEpilogue g = ep;
+    g.splitk = gemm_splits(rows_full < 0 ? m : rows_full, n, k, ep);
+    if (g.splitk > 1) {
+        require(e.splitk.p != nullptr && g.splitk * (row0 + m) * n <= e.splitk_floats,
+                "dit: the engine's split-K partial buffer is smaller than this GEMM needs");
+        g.splitk_ws = static_cast<float*>(e.splitk.p) + g.splitk * row0 * n;
+        g.splitk_ws_floats = g.splitk * m * n;
+    }
     launch_gemm_bf16(a, static_cast<const bf16_t*>(w), static_cast<const bf16_t*>(b), out, m, n, k,
-                     ep, s);
+                     g, s);
 }
 
 // The MI355X plan.
@@ -287,7 +301,7 @@ void forward_fused(bh_dit& e, const void* latent, double t, const void* caption,
         ep.round_mid = true;
         ep.row_add = e.pos_table.bf();
         ep.row_add_period = N;
-        gemm(e.patches.bf(), e.w.pos_embed_w, e.w.pos_embed_b, e.x.bf(), M, d, e.patch_in, ep, s);
+        gemm(e, e.patches.bf(), e.w.pos_embed_w, e.w.pos_embed_b, e.x.bf(), M, d, e.patch_in, ep, s);
     }
     {   // adaLN-single: one modulation vector per step
         {
@@ -296,20 +310,20 @@ void forward_fused(bh_dit& e, const void* latent, double t, const void* caption,
         }
         GemmEpilogue silu;
         silu.act = 2;
-        gemm(e.temb.bf(), e.w.t_emb1_w, e.w.t_emb1_b, e.h_t.bf(), B, d, 256, silu, s);
-        gemm(e.h_t.bf(), e.w.t_emb2_w, e.w.t_emb2_b, e.emb_t.bf(), B, d, d, plain, s);
+        gemm(e, e.temb.bf(), e.w.t_emb1_w, e.w.t_emb1_b, e.h_t.bf(), B, d, 256, silu, s);
+        gemm(e, e.h_t.bf(), e.w.t_emb2_w, e.w.t_emb2_b, e.emb_t.bf(), B, d, d, plain, s);
         {
             ProfileScope ps(K_ELEMENTWISE, s, 4.0 * B * d);
             launch_activation(e.emb_t.p, e.silu_t.p, B * d, 2, nullptr, false, s);
         }
-        gemm(e.silu_t.bf(), e.w.adaln_w, e.w.adaln_b, e.modulation.bf(), B, 6 * d, d, plain, s);
+        gemm(e, e.silu_t.bf(), e.w.adaln_w, e.w.adaln_b, e.modulation.bf(), B, 6 * d, d, plain, s);
     }
     if (!caption_ready) {   // caption projection, then every layer's cross-attention K and V
         GemmEpilogue gelu;
         gelu.act = 1;
-        gemm(static_cast<const bf16_t*>(caption), e.w.cap1_w, e.w.cap1_b, e.cap_h.bf(), e.Mcap, d,
+        gemm(e, static_cast<const bf16_t*>(caption), e.w.cap1_w, e.w.cap1_b, e.cap_h.bf(), e.Mcap, d,
              c.caption_channels, gelu, s);
-        gemm(e.cap_h.bf(), e.w.cap2_w, e.w.cap2_b, e.cap.bf(), e.Mcap, d, d, plain, s);
+        gemm(e, e.cap_h.bf(), e.w.cap2_w, e.w.cap2_b, e.cap.bf(), e.Mcap, d, d, plain, s);
         GemmEpilogue kv;   // every layer's K into kv_all; V into V^T at head_dim 72
         if (e.vt72) {
             kv.vt = e.vt_cross.bf();
@@ -320,7 +334,7 @@ void forward_fused(bh_dit& e, const void* latent, double t, const void* caption,
             kv.vt_heads = c.num_heads;
             kv.vt_dim = c.head_dim;
         }
-        gemm(e.cap.bf(), e.w_kv.p, e.b_kv.p, e.kv_all.bf(), e.Mcap, L * 2 * d, d, kv, s);
+        gemm(e, e.cap.bf(), e.w_kv.p, e.b_kv.p, e.kv_all.bf(), e.Mcap, L * 2 * d, d, kv, s);
     }
     {
         ProfileScope ps(K_ELEMENTWISE, s, 2.0 * (B * 6 * d + L * 6 * d + L * 6 * B * d));
@@ -367,8 +381,8 @@ void forward_fused(bh_dit& e, const void* latent, double t, const void* caption,
             ep.vt_heads = static_cast<int>(H);
             ep.vt_dim = static_cast<int>(Dh);
         }
-        gemm(e.modded.bf() + g.b0 * N * d, e.w_qkv.bf() + l * 3 * d * d, e.b_qkv.bf() + l * 3 * d,
-             e.qkv.bf() + g.b0 * N * 3 * d, g.nb * N, 3 * d, d, ep, g.s);
+        gemm(e, e.modded.bf() + g.b0 * N * d, e.w_qkv.bf() + l * 3 * d * d, e.b_qkv.bf() + l * 3 * d,
+             e.qkv.bf() + g.b0 * N * 3 * d, g.nb * N, 3 * d, d, ep, g.s, g.b0 * N, M);
     };
     // 1b. self-attention into ctx
     auto self_attention = [&](const Rows& g) {
@@ -395,11 +409,11 @@ void forward_fused(bh_dit& e, const void* latent, double t, const void* caption,
             ep.residual = x;
             ep.gate = ch + 2 * B * d;
             ep.gate_rows = N;
-            gemm(ctx, bw.attn1_o_w, bw.attn1_o_b, x, rows, d, d, ep, g.s);
+            gemm(e, ctx, bw.attn1_o_w, bw.attn1_o_b, x, rows, d, d, ep, g.s, g.b0 * N, M);
         }
         // 2. cross-attention (no norm before it: pixart_dit.cpp:251-253)
         bf16_t* q2 = e.q2.bf() + o;
-        gemm(x, bw.attn2_q_w, bw.attn2_q_b, q2, rows, d, d, plain, g.s);
+        gemm(e, x, bw.attn2_q_w, bw.attn2_q_b, q2, rows, d, d, plain, g.s, g.b0 * N, M);
         const bf16_t* kv = e.kv_all.bf() + g.b0 * e.cap_len * L * 2 * d + l * 2 * d;
         const void* m = static_cast<const char*>(mask) + g.b0 * e.cap_len * mask_elem;
         if (e.vt72) {
@@ -414,7 +428,7 @@ void forward_fused(bh_dit& e, const void* latent, double t, const void* caption,
             GemmEpilogue ep;
             ep.round_mid = true;
             ep.residual = x;
-            gemm(ctx, bw.attn2_o_w, bw.attn2_o_b, x, rows, d, d, ep, g.s);
+            gemm(e, ctx, bw.attn2_o_w, bw.attn2_o_b, x, rows, d, d, ep, g.s, g.b0 * N, M);
         }
         // 3. feed-forward
         norm(l, 3, g);
@@ -423,7 +437,7 @@ void forward_fused(bh_dit& e, const void* latent, double t, const void* caption,
             SubclassScope sc(K_GEMM_FF0);
             GemmEpilogue gelu;
             gelu.act = 1;
-            gemm(e.modded.bf() + o, bw.ff0_w, bw.ff0_b, ff0, rows, e.dff, d, gelu, g.s);
+            gemm(e, e.modded.bf() + o, bw.ff0_w, bw.ff0_b, ff0, rows, e.dff, d, gelu, g.s, g.b0 * N, M);
         }
         {
             SubclassScope sc(K_GEMM_FF2);
@@ -432,7 +446,7 @@ void forward_fused(bh_dit& e, const void* latent, double t, const void* caption,
             ep.residual = x;
             ep.gate = ch + 5 * B * d;
             ep.gate_rows = N;
-            gemm(ff0, bw.ff2_w, bw.ff2_b, x, rows, d, e.dff, ep, g.s);
+            gemm(e, ff0, bw.ff2_w, bw.ff2_b, x, rows, d, e.dff, ep, g.s, g.b0 * N, M);
         }
     };
 
@@ -466,7 +480,7 @@ void forward_fused(bh_dit& e, const void* latent, double t, const void* caption,
         ProfileScope ps(K_NORM, s, 4.0 * M * d);
         launch_norm_modulate_pre(e.x.bf(), e.shift.bf(), e.scale.bf(), e.modded.bf(), B, N, d, eps, s);
     }
-    gemm(e.modded.bf(), e.w.proj_out_w, e.w.proj_out_b, e.tokens.bf(), M, e.patch_out, d, plain, s);
+    gemm(e, e.modded.bf(), e.w.proj_out_w, e.w.proj_out_b, e.tokens.bf(), M, e.patch_out, d, plain, s);
     {
         ProfileScope ps(K_ELEMENTWISE, s, 4.0 * M * e.patch_out);
         launch_patch(e.tokens.p, out, B, c.out_channels, e.grid, P, true, false, s);
@@ -597,6 +611,19 @@ int bh_dit_create(const bh_dit_config* cfg, const bh_dit_weights* w, int64_t bat
             hip_check(hipMemcpy(e->tables_dev.p, tables.data(), sizeof(void*) * L,
                                 hipMemcpyHostToDevice),
                       "hipMemcpy");
+            {   // the largest split-K partial set of any GEMM of the fused plan (full batch)
+                GemmEpilogue plain, vt_ep;
+                vt_ep.vt = e->vt72 ? e->vt_self.bf() : nullptr;
+                const int64_t Mcap = e->Mcap, dff = e->dff;
+                const int64_t shapes[][4] = {{Mcap, d, c.caption_channels, 0}, {Mcap, d, d, 0},
+                                             {Mcap, L * 2 * d, d, 1}, {M, 3 * d, d, 1}, {M, d, d, 0},
+                                             {M, dff, d, 0}, {M, d, dff, 0}, {M, e->patch_out, d, 0}};
+                for (const auto& sh : shapes) {
+                    const int sp = gemm_splits(sh[0], sh[1], sh[2], sh[3] ? vt_ep : plain);
+                    if (sp > 1) e->splitk_floats = std::max(e->splitk_floats, sp * sh[0] * sh[1]);
+                }
+                if (e->splitk_floats > 0) e->splitk = e->make_f32(e->splitk_floats);
+            }
             if (batch >= 2) {   // the row-split schedule's second stream (default priority)
                 hip_check(hipStreamCreateWithFlags(&e->s2, hipStreamNonBlocking), "hipStreamCreate");
                 hip_check(hipEventCreateWithFlags(&e->fork_ev, hipEventDisableTiming), "hipEventCreate");

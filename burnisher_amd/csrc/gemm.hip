@@ -33,7 +33,10 @@
 // accumulation rounding before the single bf16 rounding at the store.
 #include "common.h"
 
+#include <algorithm>
 #include <atomic>
+#include <mutex>
+#include <string>
 
 namespace bh {
 namespace {
@@ -1070,6 +1073,86 @@ __global__ void __launch_bounds__(256) k_splitk_residual(const float* __restrict
     }
 }
 
+// The split-K epilogue: out[m, n8..n8+7] from the slices summed in order, then exactly the MFMA
+// kernel's epilogue (chunk_store): bias, activation, the mid rounding, residual or gated residual,
+// one rounding at the store. out may alias the residual (each element is read before written).
+template <int ACT, int MODE>
+__global__ void __launch_bounds__(256) k_splitk_epi(const float* __restrict__ partial, int splits,
+                                                    int64_t M, int64_t N, Epi e, bf16_t* out) {
+    const int64_t per_row = N / 8;
+    const int64_t groups = M * per_row;
+    const int64_t mn = M * N;
+    for (int64_t g = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; g < groups;
+         g += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+        const int64_t m = g / per_row, n = (g - m * per_row) * 8;
+        const float* p = partial + m * N + n;
+        f32x4_t lo = *reinterpret_cast<const f32x4_t*>(p), hi = *reinterpret_cast<const f32x4_t*>(p + 4);
+        for (int sp = 1; sp < splits; ++sp) {
+            const f32x4_t a = *reinterpret_cast<const f32x4_t*>(p + sp * mn);
+            const f32x4_t b = *reinterpret_cast<const f32x4_t*>(p + sp * mn + 4);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                lo[q] = __fadd_rn(lo[q], a[q]);
+                hi[q] = __fadd_rn(hi[q], b[q]);
+            }
+        }
+        float x[8], bias[8], t[8];
+        if (e.bias) unpack8(*reinterpret_cast<const uint4*>(e.bias + n), bias);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            const float v = q < 4 ? lo[q] : hi[q - 4];
+            x[q] = act_fast<ACT>(e.bias ? __fadd_rn(v, bias[q]) : v);
+        }
+        if (MODE != EPI_STORE && e.round_mid)
+#pragma unroll
+            for (int q = 0; q < 8; ++q) x[q] = round_bf16(x[q]);
+        if (MODE == EPI_RESIDUAL) {
+            unpack8(*reinterpret_cast<const uint4*>(e.residual + m * e.ld_out + n), t);
+#pragma unroll
+            for (int q = 0; q < 8; ++q) x[q] = __fadd_rn(t[q], x[q]);
+        }
+        if (MODE == EPI_GATED) {
+            float gq[8];
+            unpack8(*reinterpret_cast<const uint4*>(e.gate + (m / e.gate_rows) * N + n), gq);
+            unpack8(*reinterpret_cast<const uint4*>(e.residual + m * e.ld_out + n), t);
+#pragma unroll
+            for (int q = 0; q < 8; ++q) x[q] = __fadd_rn(__fmul_rn(x[q], gq[q]), t[q]);
+        }
+        *reinterpret_cast<uint4*>(out + m * e.ld_out + n) = pack8(x);
+    }
+}
+
+// Per-device fp32 partials for split-K calls that bring no buffer of their own, grown on demand.
+float* splitk_workspace(int64_t floats) {
+    static std::mutex mu;
+    static void* ptr[64] = {};
+    static int64_t cap[64] = {};
+    int dev = 0;
+    hip_check(hipGetDevice(&dev), "hipGetDevice");
+    require(dev >= 0 && dev < 64, "gemm: device index out of range");
+    std::lock_guard<std::mutex> lock(mu);
+    if (cap[dev] < floats) {
+        if (ptr[dev]) hip_check(hipFree(ptr[dev]), "hipFree");
+        ptr[dev] = nullptr;
+        cap[dev] = 0;
+        hip_check(hipMalloc(&ptr[dev], static_cast<size_t>(floats) * sizeof(float)), "hipMalloc (split-K partials)");
+        cap[dev] = floats;
+    }
+    return static_cast<float*>(ptr[dev]);
+}
+
+template <int ACT>
+void launch_splitk_epi(int mode, const float* partial, int splits, int64_t m, int64_t n, const Epi& e,
+                       bf16_t* out, hipStream_t s) {
+    const int64_t groups = m * (n / 8);
+    const int blocks = static_cast<int>(std::min<int64_t>((groups + 255) / 256, 8192));
+    switch (mode) {
+        case EPI_STORE: k_splitk_epi<ACT, EPI_STORE><<<blocks, 256, 0, s>>>(partial, splits, m, n, e, out); break;
+        case EPI_RESIDUAL: k_splitk_epi<ACT, EPI_RESIDUAL><<<blocks, 256, 0, s>>>(partial, splits, m, n, e, out); break;
+        default: k_splitk_epi<ACT, EPI_GATED><<<blocks, 256, 0, s>>>(partial, splits, m, n, e, out); break;
+    }
+}
+
 template <int ACT>
 void launch_tn_mode(int mode, const bf16_t* a, const bf16_t* b, bf16_t* out, int64_t m, int64_t n,
                     int64_t k, const Epi& e, hipStream_t s) {
@@ -1153,6 +1236,31 @@ void launch_gemm_bf16(const bf16_t* a, const bf16_t* b, const bf16_t* bias, bf16
         launch_check("gemm (reference order, fused epilogue)");
         return;
     }
+    const int splits = ep.splitk > 0 ? ep.splitk : gemm_splits(m, n, k, ep);
+    if (splits > 1) {
+        require(k % (BK * splits) == 0 && !ep.vt && mode != EPI_ROW_ADD && splits <= 16,
+                "gemm split-K: " + std::to_string(splits) + " slices of K = " + std::to_string(k) +
+                    " (whole 64-wide k-tiles, plain, residual or gated store only)");
+        const int64_t floats = static_cast<int64_t>(splits) * m * n;
+        float* partial = ep.splitk_ws;
+        if (partial) {
+            require(ep.splitk_ws_floats >= floats && aligned(partial, 16),
+                    "gemm split-K: the partial buffer holds " + std::to_string(ep.splitk_ws_floats) +
+                        " floats, this call needs " + std::to_string(floats));
+        } else {
+            partial = splitk_workspace(floats);
+        }
+        ProfileScope ps(K_GEMM, s, flops, gemm_subclass());
+        launch_tn_splitk(a, b, partial, m, n, k, splits, s);
+        launch_check("gemm (split-K partials)");
+        switch (ep.act) {
+            case 1: launch_splitk_epi<1>(mode, partial, splits, m, n, e, out, s); break;
+            case 2: launch_splitk_epi<2>(mode, partial, splits, m, n, e, out, s); break;
+            default: launch_splitk_epi<0>(mode, partial, splits, m, n, e, out, s); break;
+        }
+        launch_check("gemm (split-K epilogue)");
+        return;
+    }
     ProfileScope ps(K_GEMM, s, flops, gemm_subclass());
     switch (ep.act) {
         case 1: launch_tn_mode<1>(mode, a, b, out, m, n, k, e, s); break;
@@ -1191,9 +1299,24 @@ int gemm_splitk_choice(int64_t m, int64_t n, int64_t k) {
     const int64_t tiles = ((m + BM - 1) / BM) * ((n + BN - 1) / BN);
     const int cus = device_cus();
     int best = 1;
-    for (int sp = 2; sp <= 4; ++sp)
+    for (int sp = 2; sp <= 8; ++sp)
         if (tiles * sp <= cus && k % (BK * sp) == 0 && k / sp >= 4 * BK) best = sp;
     return best;
+}
+
+// Automatic split-K only for long K (>= 48 k-tiles: the 4608-deep ff2 and the 4096-wide caption
+// projection). Slices of a 1152-deep GEMM carry more fp32 partial traffic than they save, and
+// leaving them whole keeps the fused QKV projection summing exactly like the separate Q, K and V
+// projections of the op-by-op graph.
+constexpr int kSplitKMinKTiles = 48;
+
+int gemm_splits(int64_t m, int64_t n, int64_t k, const GemmEpilogue& ep) {
+    if (ep.splitk > 0) return ep.splitk;
+    if (ep.vt || ep.row_add || m <= kGemvMaxM || k % BK != 0 || n % 8 != 0) return 1;
+    if (k / BK < kSplitKMinKTiles) return 1;
+    const int64_t tiles = ((m + BM - 1) / BM) * ((n + BN - 1) / BN);
+    if (tiles * 2 > device_cus()) return 1;
+    return gemm_splitk_choice(m, n, k);
 }
 
 void launch_gemm_splitk_residual(const bf16_t* a, const bf16_t* b, float* partial, int splits,

@@ -142,6 +142,51 @@ def test_gemm_fused_epilogues(hip):
     assert s1["mismatch_frac"] < 0.01
 
 
+def test_gemm_split_k_epilogues(hip):
+    # A long-K GEMM with few output tiles (the 512px ff2 shape at 300 tokens per row: 24 tiles of
+    # 256 x 144, 72 k-tiles) runs as K slices whose fp32 partials are summed in slice order by the
+    # epilogue kernel: gated residual, residual and GELU store against the oracle, byte-identical
+    # across calls, and a larger then a smaller call through the library's partial buffer.
+    import burnisher_amd as bh
+    import ctypes
+    B, N_tok, d, K = 2, 300, 1152, 4608
+    M = B * N_tok
+    a, w, bias = randn_bf16(RNG, (M, K)), randn_bf16(RNG, (d, K), 0.02), randn_bf16(RNG, (d,), 0.02)
+    x, gate = randn_bf16(RNG, (M, d)), randn_bf16(RNG, (B, d), 0.5)
+    zero = np.zeros((B, d), np.uint16)
+    proj = np.zeros((M, d), np.uint16)
+    st("stock_gemm", addr(a), addr(w), addr(bias), addr(proj), M, d, K, 1, 0, BF16, 0)
+    want_gated = x.copy()
+    st("stock_modulate", addr(proj), addr(zero), addr(zero), addr(want_gated), B, N_tok, d,
+       addr(want_gated), addr(gate), BF16)
+    want_add = x.copy()
+    st("stock_add", addr(want_add), addr(proj), addr(want_add), M, d, 1.0, 0, BF16)
+    da, dw, db, dgate = dev(a), dev(w), dev(bias), dev(gate)
+    for rep in range(2):
+        print(f"split-K gated / residual, call {rep}", flush=True)
+        dx = dev(x)
+        f = bh.GemmFused(epilogue=0, round_mid=1, residual=P(dx), gate=P(dgate), gate_rows=N_tok, ld_out=d)
+        call("bh_gemm_fused_run", P(da), P(dw), P(db), P(dx), M, d, K, ctypes.byref(f), None)
+        g = host(dx, want_gated)
+        assert_within(from_bf16(g), from_bf16(want_gated), "gemm_fused", f"split-K gated residual {rep}")
+        if rep == 0:
+            first = g
+        else:
+            assert np.array_equal(g, first), "split-K gated residual not byte-identical"
+        dx2 = dev(x)
+        f = bh.GemmFused(epilogue=0, round_mid=1, residual=P(dx2), ld_out=d)
+        call("bh_gemm_fused_run", P(da), P(dw), P(db), P(dx2), M, d, K, ctypes.byref(f), None)
+        assert_within(from_bf16(host(dx2, want_add)), from_bf16(want_add), "gemm_fused",
+                      f"split-K residual {rep}")
+    # GELU store, then a smaller long-K call (one row block) through the same partial buffer
+    for m in (M, 40):
+        want = np.zeros((m, d), np.uint16)
+        st("stock_gemm", addr(a[:m]), addr(w), addr(bias), addr(want), m, d, K, 1, 1, BF16, 0)
+        got = empty((m, d))
+        call("bh_gemm", P(dev(a[:m])), P(dw), P(db), P(got), m, d, K, 1, 1, BF16, None)
+        assert_within(from_bf16(host(got, want)), from_bf16(want), "gemm", f"split-K GELU M={m}")
+
+
 # ---- attention ----------------------------------------------------------------------------
 
 def attention_case(B, S, KV, H, D, mask=None, scale=0.0, strided=False, inputs=None):
