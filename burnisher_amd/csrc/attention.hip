@@ -353,13 +353,14 @@ __global__ void __launch_bounds__(kThreads, 1) k_flash(AttnArgs a) {
         const int64_t qrow = q0 + u * 16 + c16;
         if (qrow >= a.Sq) continue;
         bf16_t* dst = a.out + (b * a.Sq + qrow) * a.ld_o + h * D;
+        const float rl = __frcp_rn(l);   // one reciprocal per query, a multiply per output
 #pragma unroll
         for (int e = 0; e < DT; ++e) {
             const int d = e * 16 + g * 4;
             if (d >= D) continue;
             float v[4];
 #pragma unroll
-            for (int r = 0; r < 4; ++r) v[r] = __fdiv_rn(o[e][u][r], l);
+            for (int r = 0; r < 4; ++r) v[r] = o[e][u][r] * rl;
             if (VEC) {
                 uint2 w;
                 w.x = static_cast<uint32_t>(f2bf(v[0])) | (static_cast<uint32_t>(f2bf(v[1])) << 16);

@@ -41,7 +41,7 @@
 // is -inf, weight 0, and key blocks that are wholly masked are skipped. A row whose keys are ALL
 // masked is uniform over V in the oracle; here all its scores are set equal, which is the same
 // uniform average. P is rounded to bf16 for the MFMA (the oracle keeps it fp32) and the
-// normalisation divides by the sum of those rounded weights.
+// normalisation multiplies by the reciprocal of the sum of those rounded weights.
 #include "common.h"
 
 #include <cmath>
@@ -618,7 +618,10 @@ __global__ void __launch_bounds__(kThreads, 1) k_flash72(Flash72Args a) {
     // ---- normalise and store: lane holds out[q][d..d+3], d = 16e + 4g; O^T row 72 is the sum ----
 #pragma unroll
     for (int u = 0; u < kQT; ++u) {
-        const float l = __shfl(w.o[4][u][0], 32 + lr, 64);
+        // One correctly rounded reciprocal per query, then a multiply per output (within one fp32
+        // ulp of the quotient before the bf16 rounding): an IEEE division per output was ~10
+        // instructions, 72 of them per lane.
+        const float rl = __frcp_rn(__shfl(w.o[4][u][0], 32 + lr, 64));
         const int q = q_base + u * 16 + lr;
         if (q >= a.Sq) continue;
         bf16_t* dst = a.out + (static_cast<int64_t>(b) * a.Sq + q) * a.ld_o + h * D;
@@ -627,10 +630,10 @@ __global__ void __launch_bounds__(kThreads, 1) k_flash72(Flash72Args a) {
             const int d = e * 16 + g * 4;
             if (d >= D) continue;
             uint2 x;
-            x.x = static_cast<uint32_t>(f2bf(__fdiv_rn(w.o[e][u][0], l))) |
-                  (static_cast<uint32_t>(f2bf(__fdiv_rn(w.o[e][u][1], l))) << 16);
-            x.y = static_cast<uint32_t>(f2bf(__fdiv_rn(w.o[e][u][2], l))) |
-                  (static_cast<uint32_t>(f2bf(__fdiv_rn(w.o[e][u][3], l))) << 16);
+            x.x = static_cast<uint32_t>(f2bf(w.o[e][u][0] * rl)) |
+                  (static_cast<uint32_t>(f2bf(w.o[e][u][1] * rl)) << 16);
+            x.y = static_cast<uint32_t>(f2bf(w.o[e][u][2] * rl)) |
+                  (static_cast<uint32_t>(f2bf(w.o[e][u][3] * rl)) << 16);
             *reinterpret_cast<uint2*>(dst + d) = x;
         }
     }

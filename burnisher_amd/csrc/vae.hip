@@ -416,10 +416,11 @@ __global__ void __launch_bounds__(256, 1) k_flash512(A5Args a) {
     l = a5_pair(l, false, false);
     if (q >= a.S) return;
     bf16_t* orow = a.out + static_cast<int64_t>(q) * kA5D + 4 * hi;
+    const float rl = __frcp_rn(l);   // one reciprocal per query, a multiply per output
 #pragma unroll
     for (int dt = 0; dt < 32; ++dt) {
-        const uint32_t lo = static_cast<uint32_t>(f2bf(o[dt][0] / l)) | (static_cast<uint32_t>(f2bf(o[dt][1] / l)) << 16);
-        const uint32_t hi2 = static_cast<uint32_t>(f2bf(o[dt][2] / l)) | (static_cast<uint32_t>(f2bf(o[dt][3] / l)) << 16);
+        const uint32_t lo = static_cast<uint32_t>(f2bf(o[dt][0] * rl)) | (static_cast<uint32_t>(f2bf(o[dt][1] * rl)) << 16);
+        const uint32_t hi2 = static_cast<uint32_t>(f2bf(o[dt][2] * rl)) | (static_cast<uint32_t>(f2bf(o[dt][3] * rl)) << 16);
         *reinterpret_cast<uint2*>(orow + 16 * dt) = make_uint2(lo, hi2);
     }
 }
