@@ -271,16 +271,24 @@ int attention_impl(const void* q, int64_t ld_q, const void* k, const void* v, in
             launch_attention_bf16(qb, kb, vb, ob, sh, key_mask, mask_f32, as_stream(stream), bb);
             return;
         }
-        // V^T into the fixed per-device scratch: nothing is allocated, so the call is refused
-        // when the transposed V would not fit.
+        // V^T and the key-split partials (the same splits bh_attention takes, so both give the
+        // same bits) into the fixed per-device scratch: nothing is allocated, so the call is
+        // refused when they would not fit.
         const int64_t need = attention_vt_elems(qb, kb, vb, ob, sh, key_mask, bb);
-        const int64_t cap = kNoAllocScratchBytes / static_cast<int64_t>(sizeof(bf16_t));
-        require(need <= cap, "attention_noalloc: V^T needs " + std::to_string(need * 2) +
-                                 " bytes of scratch, above the fixed maximum of " +
-                                 std::to_string(kNoAllocScratchBytes) +
-                                 " bytes (use bh_attention, which grows its workspace)");
+        const int64_t part_floats = attention_part_floats(qb, kb, vb, ob, sh, key_mask, bb);
+        const int64_t vt_bytes = (need * 2 + 255) / 256 * 256;
+        const int64_t total = vt_bytes + part_floats * 4;
+        require(total <= kNoAllocScratchBytes,
+                "attention_noalloc: V^T and the key-split partials need " + std::to_string(total) +
+                    " bytes of scratch, above the fixed maximum of " +
+                    std::to_string(kNoAllocScratchBytes) +
+                    " bytes (use bh_attention, which grows its workspace)");
+        bf16_t* base = total > 0 ? noalloc_scratch() : nullptr;
+        float* part = part_floats > 0 ? reinterpret_cast<float*>(reinterpret_cast<char*>(base) + vt_bytes)
+                                      : nullptr;
         launch_attention_bf16(qb, kb, vb, ob, sh, key_mask, mask_f32, as_stream(stream), bb,
-                              need > 0 ? noalloc_scratch() : nullptr, cap);
+                              need > 0 ? base : nullptr, vt_bytes / 2, part_floats > 0 ? 0 : 1, part,
+                              part_floats);
     });
 }
 }  // namespace

@@ -327,24 +327,43 @@ struct AttnShape {
 // The head_dim-72 and -512 kernels read V transposed: into `vt_buf` (vt_buf_elems elements, at
 // least attention_vt_elems of the call, else an error) when given, else into a per-device
 // workspace that grows on demand and that calls overlapping on one device share.
+// `splits`, `part`, `part_floats`: the head_dim-72 kernel's key splits and their fp32 partials,
+// as launch_flash72 takes them (other kernels ignore them).
 void launch_attention_bf16(const bf16_t* q, const bf16_t* k, const bf16_t* v, bf16_t* out,
                            const AttnShape& sh, const void* key_mask, bool mask_f32,
                            hipStream_t s, const bf16_t* bias = nullptr, bf16_t* vt_buf = nullptr,
-                           int64_t vt_buf_elems = 0);
+                           int64_t vt_buf_elems = 0, int splits = 0, float* part = nullptr,
+                           int64_t part_floats = 0);
 // The V^T elements launch_attention_bf16 needs for these operands (0: the kernel reads V as is).
 int64_t attention_vt_elems(const bf16_t* q, const bf16_t* k, const bf16_t* v, const bf16_t* out,
                            const AttnShape& sh, const void* key_mask, const bf16_t* bias);
+// The fp32 key-split partials launch_attention_bf16 needs for these operands with splits = 0
+// (0: the call does not split).
+int64_t attention_part_floats(const bf16_t* q, const bf16_t* k, const bf16_t* v, const bf16_t* out,
+                              const AttnShape& sh, const void* key_mask, const bf16_t* bias);
 // The allocation-free attention's scratch: a fixed device array of kNoAllocScratchBytes per device,
-// its address looked up (hipGetSymbolAddress) on the first call with that device current.
-constexpr int64_t kNoAllocScratchBytes = int64_t{32} << 20;
+// its address looked up (hipGetSymbolAddress) on the first call with that device current. It holds
+// V^T and, after it at a 256-byte boundary, the key-split partials.
+constexpr int64_t kNoAllocScratchBytes = int64_t{64} << 20;
 bf16_t* noalloc_scratch();
 // Flash attention at head_dim 72 with V supplied transposed (flash72.hip): vt holds, for each
 // (b, h, d), a row of vt_ld >= flash72_vt_ld(kv_len) keys, zero past kv_len.
 int64_t flash72_vt_ld(int64_t kv_len);
+// `splits`: key splits (0: flash72_splits decides, 1: none). A split launch writes fp32
+// partials to `part` (part_floats floats, at least flash72_part_floats) or, when it is null, to a
+// per-device library buffer grown on demand, and a second kernel combines them into `out`.
 void launch_flash72(const bf16_t* q, int64_t ld_q, const bf16_t* k, int64_t ld_k,
                     const bf16_t* vt, int64_t vt_ld, bf16_t* out, int64_t ld_o, int64_t batch,
                     int64_t heads, int64_t q_len, int64_t kv_len, float scale,
-                    const void* key_mask, bool mask_f32, hipStream_t s);
+                    const void* key_mask, bool mask_f32, hipStream_t s, int splits = 0,
+                    float* part = nullptr, int64_t part_floats = 0);
+// Key splits for a head_dim-72 attention whose workgroups (512 queries of one batch row and head
+// each) would fill at most half the CUs: as many as still fit at once, at least two key blocks
+// each; 1 for the resident (kv_len <= 448) kernel and for an output whose rows are not 16-byte
+// aligned.
+int flash72_splits(int64_t batch, int64_t heads, int64_t q_len, int64_t kv_len,
+                   const void* out = nullptr, int64_t ld_o = 8);
+int64_t flash72_part_floats(int64_t batch, int64_t heads, int64_t q_len, int splits);
 // V [batch, kv_len, ld_v] (head-last, head_dim 72) -> the V^T rows launch_flash72 reads.
 void launch_transpose_v72(const bf16_t* v, int64_t ld_v, int64_t batch, int64_t heads,
                           int64_t kv_len, bf16_t* vt, int64_t vt_ld, hipStream_t s);

@@ -44,7 +44,10 @@
 // normalisation multiplies by the reciprocal of the sum of those rounded weights.
 #include "common.h"
 
+#include <algorithm>
 #include <cmath>
+#include <mutex>
+#include <string>
 
 namespace bh {
 namespace {
@@ -81,6 +84,13 @@ struct Flash72Args {
     int mask_f32;
     int qblocks;
     float c;   // scale * log2(e)
+    // Split over keys (low-occupancy shapes): workgroup (b, h, query block, split) takes key
+    // blocks [split * nblk / splits, (split + 1) * nblk / splits) and, when `part` is set,
+    // writes its unnormalised partial instead of the output:
+    // part[((split * B + b) * H + h) * Sq + q][0..79] = O over dims 0..71, the row sum at 72, the
+    // running maximum (log2 units) at 73.
+    int splits = 1;
+    float* part = nullptr;
 };
 
 #pragma clang diagnostic push
@@ -423,26 +433,32 @@ __device__ __forceinline__ void softmax(WaveState& w, const Flash72Args& a, int 
 // RESIDENT (kv_len <= 448): every key block is loaded once, up front, into a stage of its own;
 // after one barrier each wave runs its blocks through without further synchronisation (the two
 // waves of a SIMD drift apart, so one's softmax overlaps the other's MFMAs).
-template <bool MASKED, bool RESIDENT>
+// SPLIT (never with RESIDENT): a key split of a.splits, written as an fp32 partial to a.part.
+template <bool MASKED, bool RESIDENT, bool SPLIT>
 __global__ void __launch_bounds__(kThreads, 1) k_flash72(Flash72Args a) {
     constexpr int kNumStages = RESIDENT ? kResidentBlocks : kStages;
     __shared__ __attribute__((aligned(1024))) char smem[kNumStages * kStage];
     __shared__ unsigned long long blk_bits[kMaxBlocks];
     __shared__ int live[kMaxBlocks];
-    __shared__ int nlive_s, all_masked_s;
+    __shared__ int nlive_s, all_masked_s, empty_s;
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lr = lane & 15, g = lane >> 4;
 
-    // ---- which (b, h, query block): the blocks of one (b, h) stay on one XCD ----
-    const int T = a.B * a.H * a.qblocks;
+    // ---- which (b, h, query block, key split): the blocks of one (b, h) stay on one XCD ----
+    const int splits = SPLIT ? a.splits : 1;
+    const int T = a.B * a.H * a.qblocks * splits;
     int bid = blockIdx.x;
     if ((T & 7) == 0) bid = (bid & 7) * (T >> 3) + (bid >> 3);
+    const int split = SPLIT ? bid % splits : 0;
+    if (SPLIT) bid /= splits;
     const int bh = bid / a.qblocks;
     const int b = bh / a.H, h = bh - b * a.H;
     const int q_base = (bid - bh * a.qblocks) * kQPerWg + wave * kQPerWave;
     const int nblk = (a.Skv + kKV - 1) / kKV;
+    const int kb0 = SPLIT ? split * nblk / splits : 0;
+    const int kb1 = SPLIT ? (split + 1) * nblk / splits : nblk;
 
     WaveState w;
     // Q fragments first, so their latency overlaps the set-up below
@@ -488,9 +504,15 @@ __global__ void __launch_bounds__(kThreads, 1) k_flash72(Flash72Args a) {
         unsigned long long any = MASKED ? 0ull : 1ull;
         if (MASKED)
             for (int blk = 0; blk < nblk; ++blk) any |= blk_bits[blk];
-        const bool all_masked = any == 0ull;
-        for (int blk = 0; blk < nblk; ++blk)
+        const bool all_masked = any == 0ull;   // over the whole row, whatever this split's range
+        for (int blk = kb0; blk < kb1; ++blk)
             if (!MASKED || all_masked || blk_bits[blk] != 0ull) live[n++] = blk;
+        // A key split whose blocks are all masked still runs its first block (every score -inf)
+        // and then writes an empty partial: the pipeline needs at least one block.
+        if (SPLIT) {
+            empty_s = n == 0 ? 1 : 0;
+            if (n == 0) live[n++] = kb0;
+        }
         nlive_s = n;
         all_masked_s = all_masked ? 1 : 0;
     }
@@ -615,6 +637,29 @@ __global__ void __launch_bounds__(kThreads, 1) k_flash72(Flash72Args a) {
     }
     }
 
+    // ---- a key split's partial: O unnormalised, the row sum and the running maximum ----
+    if constexpr (SPLIT) {
+        const bool empty = empty_s != 0;
+#pragma unroll
+        for (int u = 0; u < kQT; ++u) {
+            const int q = q_base + u * 16 + lr;
+            if (q >= a.Sq) continue;
+            float* dst = a.part + ((static_cast<int64_t>(split) * a.B + b) * a.H + h) * a.Sq * 80 +
+                         static_cast<int64_t>(q) * 80;
+#pragma unroll
+            for (int e = 0; e < 5; ++e) {
+                const int d = e * 16 + g * 4;
+                if (d < D) {
+                    *reinterpret_cast<f32x4_t*>(dst + d) = empty ? f32x4_t{0.f, 0.f, 0.f, 0.f} : w.o[e][u];
+                } else if (d == D) {   // row 72 is the sum; an empty split contributes nothing
+                    *reinterpret_cast<f32x4_t*>(dst + d) =
+                        empty ? f32x4_t{0.f, -INFINITY, 0.f, 0.f} : f32x4_t{w.o[e][u][0], w.mc[u], 0.f, 0.f};
+                }
+            }
+        }
+        return;
+    }
+
     // ---- normalise and store: lane holds out[q][d..d+3], d = 16e + 4g; O^T row 72 is the sum ----
 #pragma unroll
     for (int u = 0; u < kQT; ++u) {
@@ -662,9 +707,92 @@ __global__ void __launch_bounds__(256) k_transpose_v72(const bf16_t* __restrict_
     }
 }
 
+// The key splits' partials into the output: per (b, h, q), M = the largest running maximum,
+// out = sum_s O_s 2^(m_s - M) / sum_s l_s 2^(m_s - M), in split order. One thread per 8 dims.
+__global__ void __launch_bounds__(256) k_flash72_combine(const float* __restrict__ part, int splits,
+                                                         int B, int H, int Sq, bf16_t* out,
+                                                         int64_t ld_o) {
+    constexpr int kChunks = D / 8;   // 9
+    const int64_t rows = static_cast<int64_t>(B) * H * Sq;
+    const int64_t split_stride = rows * 80;
+    for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < rows * kChunks;
+         i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+        const int64_t row = i / kChunks;   // ((b * H + h) * Sq + q)
+        const int c = static_cast<int>(i - row * kChunks);
+        const float* p = part + row * 80;
+        float mx = -INFINITY;
+        for (int sp = 0; sp < splits; ++sp) mx = fmaxf(mx, p[sp * split_stride + 73]);
+        float l = 0.f, o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        for (int sp = 0; sp < splits; ++sp) {
+            const float* ps = p + sp * split_stride;
+            const float wgt = __builtin_amdgcn_exp2f(ps[73] - mx);   // 0 for an empty split
+            l = __fmaf_rn(ps[72], wgt, l);
+            const f32x4_t lo = *reinterpret_cast<const f32x4_t*>(ps + c * 8);
+            const f32x4_t hi = *reinterpret_cast<const f32x4_t*>(ps + c * 8 + 4);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                o[r] = __fmaf_rn(lo[r], wgt, o[r]);
+                o[4 + r] = __fmaf_rn(hi[r], wgt, o[4 + r]);
+            }
+        }
+        const float rl = __frcp_rn(l);
+        float v[8];
+#pragma unroll
+        for (int r = 0; r < 8; ++r) v[r] = o[r] * rl;
+        const int64_t q = row % Sq, bh = row / Sq;
+        const int64_t b = bh / H, h = bh - b * H;
+        uint32_t wv[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            wv[r] = static_cast<uint32_t>(f2bf(v[2 * r])) | (static_cast<uint32_t>(f2bf(v[2 * r + 1])) << 16);
+        *reinterpret_cast<uint4*>(out + (b * Sq + q) * ld_o + h * D + c * 8) = make_uint4(wv[0], wv[1], wv[2], wv[3]);
+    }
+}
+
+// Per-device partials for split calls that bring no buffer of their own, grown on demand.
+float* flash72_part_workspace(int64_t floats) {
+    static std::mutex mu;
+    static void* ptr[64] = {};
+    static int64_t cap[64] = {};
+    int dev = 0;
+    hip_check(hipGetDevice(&dev), "hipGetDevice");
+    require(dev >= 0 && dev < 64, "attention: device index out of range");
+    std::lock_guard<std::mutex> lock(mu);
+    if (cap[dev] < floats) {
+        if (ptr[dev]) hip_check(hipFree(ptr[dev]), "hipFree");
+        ptr[dev] = nullptr;
+        cap[dev] = 0;
+        hip_check(hipMalloc(&ptr[dev], static_cast<size_t>(floats) * sizeof(float)),
+                  "hipMalloc (attention partials)");
+        cap[dev] = floats;
+    }
+    return static_cast<float*>(ptr[dev]);
+}
+
 }  // namespace
 
 int64_t flash72_vt_ld(int64_t kv_len) { return (kv_len + kKV - 1) / kKV * kKV; }
+
+int flash72_splits(int64_t batch, int64_t heads, int64_t q_len, int64_t kv_len, const void* out,
+                   int64_t ld_o) {
+    const int64_t nblk = (kv_len + kKV - 1) / kKV;
+    if (kv_len <= kResidentBlocks * kKV) return 1;   // the resident kernel does not split
+    // the combine stores 8 outputs at a time
+    if (ld_o % 8 != 0 || reinterpret_cast<uintptr_t>(out) % 16 != 0) return 1;
+    const int64_t wgs = batch * heads * ((q_len + kQPerWg - 1) / kQPerWg);
+    int cus = 0, dev = 0;
+    hip_check(hipGetDevice(&dev), "hipGetDevice");
+    hip_check(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev), "hipDeviceGetAttribute");
+    if (wgs * 2 > cus) return 1;
+    int best = 1;
+    for (int sp = 2; sp <= 8; ++sp)
+        if (wgs * sp <= cus && nblk >= 2 * sp) best = sp;
+    return best;
+}
+
+int64_t flash72_part_floats(int64_t batch, int64_t heads, int64_t q_len, int splits) {
+    return splits > 1 ? static_cast<int64_t>(splits) * batch * heads * q_len * 80 : 0;
+}
 
 void launch_transpose_v72(const bf16_t* v, int64_t ld_v, int64_t batch, int64_t heads,
                           int64_t kv_len, bf16_t* vt, int64_t vt_ld, hipStream_t s) {
@@ -678,7 +806,8 @@ void launch_transpose_v72(const bf16_t* v, int64_t ld_v, int64_t batch, int64_t 
 void launch_flash72(const bf16_t* q, int64_t ld_q, const bf16_t* k, int64_t ld_k,
                     const bf16_t* vt, int64_t vt_ld, bf16_t* out, int64_t ld_o, int64_t batch,
                     int64_t heads, int64_t q_len, int64_t kv_len, float scale,
-                    const void* key_mask, bool mask_f32, hipStream_t s) {
+                    const void* key_mask, bool mask_f32, hipStream_t s, int splits,
+                    float* part, int64_t part_floats) {
     if (batch * heads * q_len == 0) return;
     require(kv_len > 0, "attention: kv_len must be positive");
     require(kv_len <= kMaxBlocks * kKV, "attention (head_dim 72): kv_len above 16384");
@@ -702,16 +831,43 @@ void launch_flash72(const bf16_t* q, int64_t ld_q, const bf16_t* k, int64_t ld_k
     a.mask_f32 = mask_f32 ? 1 : 0;
     a.qblocks = static_cast<int>((q_len + kQPerWg - 1) / kQPerWg);
     a.c = scale * 1.4426950408889634f;
-    const int grid = a.B * a.H * a.qblocks;
-    const double flops = 4.0 * batch * heads * static_cast<double>(q_len) * kv_len * D;
-    ProfileScope ps(q_len == kv_len ? K_ATTN_SELF : K_ATTN_CROSS, s, flops);
     const bool masked = key_mask || kv_len % kKV != 0;
     const bool resident = kv_len <= kResidentBlocks * kKV;
-    if (masked && resident) k_flash72<true, true><<<grid, kThreads, 0, s>>>(a);
-    else if (masked) k_flash72<true, false><<<grid, kThreads, 0, s>>>(a);
-    else if (resident) k_flash72<false, true><<<grid, kThreads, 0, s>>>(a);
-    else k_flash72<false, false><<<grid, kThreads, 0, s>>>(a);
+    if (splits <= 0) splits = flash72_splits(batch, heads, q_len, kv_len, out, ld_o);
+    const int64_t nblk = (kv_len + kKV - 1) / kKV;
+    require(splits >= 1 && splits <= 8 && (splits == 1 || (!resident && nblk >= splits)),
+            "attention (head_dim 72): " + std::to_string(splits) + " key splits of " +
+                std::to_string(nblk) + " key blocks");
+    if (splits > 1) {
+        const int64_t floats = flash72_part_floats(batch, heads, q_len, splits);
+        if (part) {
+            require(part_floats >= floats && reinterpret_cast<uintptr_t>(part) % 16 == 0,
+                    "attention (head_dim 72): the partial buffer holds " + std::to_string(part_floats) +
+                        " floats, this call needs " + std::to_string(floats));
+        } else {
+            part = flash72_part_workspace(floats);
+        }
+        require(ld_o % 8 == 0 && reinterpret_cast<uintptr_t>(out) % 16 == 0,
+                "attention (head_dim 72): a key-split output needs 16-byte rows");
+        a.splits = splits;
+        a.part = part;
+    }
+    const int grid = a.B * a.H * a.qblocks * a.splits;
+    const double flops = 4.0 * batch * heads * static_cast<double>(q_len) * kv_len * D;
+    ProfileScope ps(q_len == kv_len ? K_ATTN_SELF : K_ATTN_CROSS, s, flops);
+    if (a.splits > 1 && masked) k_flash72<true, false, true><<<grid, kThreads, 0, s>>>(a);
+    else if (a.splits > 1) k_flash72<false, false, true><<<grid, kThreads, 0, s>>>(a);
+    else if (masked && resident) k_flash72<true, true, false><<<grid, kThreads, 0, s>>>(a);
+    else if (masked) k_flash72<true, false, false><<<grid, kThreads, 0, s>>>(a);
+    else if (resident) k_flash72<false, true, false><<<grid, kThreads, 0, s>>>(a);
+    else k_flash72<false, false, false><<<grid, kThreads, 0, s>>>(a);
     launch_check("attention (flash, head_dim 72)");
+    if (a.splits > 1) {
+        const int64_t threads = batch * heads * q_len * (D / 8);
+        k_flash72_combine<<<static_cast<int>(std::min<int64_t>((threads + 255) / 256, 8192)), 256, 0, s>>>(
+            a.part, a.splits, a.B, a.H, a.Sq, out, ld_o);
+        launch_check("attention (head_dim 72, key-split combine)");
+    }
 }
 
 }  // namespace bh

@@ -89,10 +89,12 @@ int bh_attention(const void* q, const void* k, const void* v, void* out, int64_t
 /* bh_attention without any allocation, for callers that cannot allocate: code under HIP graph
  * capture, tight serving loops, harnesses that forbid hipMalloc. It has no counterpart in the
  * reference. Same arguments, kernels and results as bh_attention; where bh_attention transposes V
- * into a workspace it grows on demand (head_dim 72 and the single-head head_dim-512 kernel), this
- * one uses a fixed array in the library's device memory of 32 MiB per device (V^T of
- * batch x heads x 72 x kv_len rounded up to 64 keys, or 512 x kv_len rounded up to 32, bf16), and a
- * call that needs more is refused with an error. The array's address is looked up by bh_init (or
+ * into a workspace it grows on demand (head_dim 72 and the single-head head_dim-512 kernel) and,
+ * at head_dim 72 with few queries, splits the keys with fp32 partials in another, this one uses a
+ * fixed array in the library's device memory of 64 MiB per device (V^T of
+ * batch x heads x 72 x kv_len rounded up to 64 keys, or 512 x kv_len rounded up to 32, bf16; then
+ * splits x batch x heads x q_len x 320 bytes of partials), and a call that needs more is refused
+ * with an error. The array's address is looked up by bh_init (or
  * by the first call on a device). Every call on one device shares that array and each call
  * rewrites all of it that it reads, so nothing carries over between calls; calls that overlap on
  * one device (two streams, or two threads) race on it and must be ordered by the caller. */

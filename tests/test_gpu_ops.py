@@ -247,6 +247,25 @@ def test_attention_masks(hip):
     assert np.all(np.isfinite(from_bf16(g)))
 
 
+def test_attention_key_splits_masked(hip):
+    # 16 workgroups of 512 queries over 16 key blocks: the head_dim-72 kernel splits the keys 8
+    # ways (two blocks each) and combines the fp32 partials. Row 0 has live keys in the first split
+    # only, row 1 none at all (the plain mean of V over every split), row 2 a hole covering whole
+    # splits in the middle and a ragged last block.
+    B, S, KV, H, D = 3, 600, 1000, 4, 72
+    mask = np.zeros((B, KV), np.float32)
+    mask[0, :40] = 1.0
+    mask[2, :] = 1.0
+    mask[2, 200:700] = 0.0
+    mask[2, 990:] = 0.0
+    g, want = attention_case(B, S, KV, H, D, mask=mask)
+    assert_within(from_bf16(g), from_bf16(want), "attention", "key splits, masked")
+    assert np.all(np.isfinite(from_bf16(g)))
+    # unmasked, with a key count that is not a multiple of the 64-key block
+    g, want = attention_case(1, 1000, 1000, 4, D)
+    assert_within(from_bf16(g), from_bf16(want), "attention", "key splits, ragged")
+
+
 def test_attention_masked_values_do_not_leak(hip):
     B, S, KV, H, D = 2, 64, 150, 2, 72
     q, k, v = (randn_bf16(RNG, s) for s in ((B, S, H, D), (B, KV, H, D), (B, KV, H, D)))

@@ -1,8 +1,9 @@
-"""bh_attention_noalloc, the allocation-free variant of bh_attention (its V^T scratch is a fixed
-32 MiB device array per GPU), through the C ABI against bh_attention on the same operands: the
-same kernels, so the outputs are equal bit for bit. Two calls in a row, the second smaller (the
-scratch keeps the first call's contents), the head_dim-512 path, a head_dim with no scratch at
-all, and a call whose V^T would not fit, which is refused before any launch."""
+"""bh_attention_noalloc, the allocation-free variant of bh_attention (its V^T and key-split
+partials live in a fixed 64 MiB device array per GPU), through the C ABI against bh_attention on
+the same operands: the same kernels and the same key splits, so the outputs are equal bit for bit.
+Two calls in a row, the second smaller (the scratch keeps the first call's contents), a masked
+call split over the keys, the head_dim-512 path, a head_dim with no scratch at all, and a call
+whose V^T would not fit, which is refused before any launch."""
 import numpy as np
 import pytest
 
@@ -53,6 +54,8 @@ def both(batch, heads, sq, skv, dh, seed=0, masked=False):
 
 def test_noalloc_equals_attention_two_calls_second_smaller(hip):
     import torch
+    # 128 workgroups of 512 queries: both entry points split the keys in two (fp32 partials in
+    # the scratch after V^T for the allocation-free one)
     a, b, f0, f1 = both(2, 16, 2048, 2048, 72, seed=1)
     assert torch.equal(a, b), "head_dim 72 self-attention differs from bh_attention"
     assert f1 == f0, f"the call changed free device memory by {f0 - f1} bytes"
@@ -62,6 +65,14 @@ def test_noalloc_equals_attention_two_calls_second_smaller(hip):
     # and a third at the first size again: nothing left from the smaller call leaks in
     a, b, _, _ = both(2, 16, 2048, 2048, 72, seed=3)
     assert torch.equal(a, b)
+
+
+def test_noalloc_key_split_masked(hip):
+    import torch
+    # 16 workgroups over 16 key blocks, a ragged last block and a caption-style mask: 8 key splits,
+    # and the second batch row's mask leaves some splits with no live key
+    a, b, f0, f1 = both(2, 4, 600, 1000, 72, seed=7, masked=True)
+    assert torch.equal(a, b) and f1 == f0
 
 
 def test_noalloc_head_dim_512_and_no_scratch_paths(hip):
@@ -75,12 +86,12 @@ def test_noalloc_head_dim_512_and_no_scratch_paths(hip):
 def test_noalloc_refuses_what_does_not_fit(hip):
     import torch
     import burnisher_amd as bh
-    # V^T of 2 x 16 x 72 x 8192 bf16 = 37.7 MB > 32 MiB
-    q, k, v, _ = tensors(2, 16, 64, 8192, 72, seed=6, masked=False)
+    # V^T of 2 x 16 x 72 x 16384 bf16 = 75.5 MB > 64 MiB
+    q, k, v, _ = tensors(2, 16, 64, 16384, 72, seed=6, masked=False)
     out = torch.zeros_like(q)
     with pytest.raises(bh.BurnisherError, match="above the fixed maximum"):
         bh.call("bh_attention_noalloc", q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), 2, 16, 64,
-                8192, 72, 0.0, None, None, F32, BF16, None)
+                16384, 72, 0.0, None, None, F32, BF16, None)
     torch.cuda.synchronize()
     assert not out.any(), "a refused call wrote the output"
     host = np.zeros(16, np.uint16)
