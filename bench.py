@@ -14,8 +14,9 @@ device synchronisation.
 
 The JSON line also carries:
   roofline      the dominant kernel (largest share of step time): algorithmic FLOP per launch
-                over its average launch duration, timed live with HIP events around each of its
-                launches in the timed region, against the 2.5166 PFLOP/s dense bf16 MFMA peak;
+                over its average launch duration, timed live with HIP events around one of its
+                launches per step in the timed region (every 29th launch: the sampled layer
+                moves by one each step), against the 2.5166 PFLOP/s dense bf16 MFMA peak;
                 `traffic` is its HBM bytes per launch from the committed rocprofv3 counter
                 summary (profiles/flash72_self_1024_traffic.md);
   step          the whole step's algorithmic FLOP (the reference's accounting,
@@ -703,12 +704,17 @@ def main() -> int:
     dominant = max((c for c in exclusive if c in breakdown), key=lambda c: breakdown[c]["ms"])
     log(f"profiled step: {json.dumps(breakdown)}; dominant kernel {dominant}")
 
-    # the timed region: K steps, HIP events around the dominant kernel's launches
+    # the timed region: K steps, HIP events around one launch of the dominant kernel per step.
+    # Every (layers + 1)-th launch is bracketed, so the sampled layer moves by one each step and
+    # the other launches run with no event beside them.
+    sample_every = wl.cfg["num_layers"] + 1
+    bh.call("bh_profile_sample", sample_every)
     bh.call("bh_profile_enable", 1 << classes[dominant])
     ms_per_step = timed_steps(eng.step, stream, args.steps)
     dms, dn, dwork = ctypes.c_double(), ctypes.c_int64(), ctypes.c_double()
     bh.call("bh_profile_read", classes[dominant], ctypes.byref(dms), ctypes.byref(dn), ctypes.byref(dwork))
     bh.call("bh_profile_enable", 0)
+    bh.call("bh_profile_sample", 1)
     avg_launch_ms = dms.value / max(1, dn.value)
     work_per_launch = dwork.value / max(1, dn.value)
     achieved = work_per_launch / (avg_launch_ms * 1e-3) / 1e12
@@ -759,9 +765,10 @@ def main() -> int:
                    "ms_per_step_rows_split": None if split_ms is None else round(split_ms, 4),
                    "rows_split_output_identical": split_equal,
                    "basis": "value: K back-to-back steps between HIP events on the engine's stream, "
-                            "with HIP events also around each launch of the dominant kernel (the "
-                            "roofline's live measurement); profiler_off: the same with no event "
-                            "inside a step; sync_median: the reference's method, each step timed "
+                            "with HIP events also around one launch of the dominant kernel per step "
+                            f"(every {sample_every}th launch, so the sampled layer moves by one each "
+                            "step: the roofline's live measurement); profiler_off: the same with no "
+                            "event inside a step; sync_median: the reference's method, each step timed "
                             "on the host clock from launch to device synchronisation, median; "
                             "rows_split: the same engine with its two CFG rows on two streams "
                             "(BH_DIT_ROWS_SPLIT), profiler off -- not the value, whose per-launch "
@@ -777,6 +784,7 @@ def main() -> int:
                                       "WRITE_SIZE (x1.000), each scaled by a 256 MiB copy; "
                                       "profiles/flash72_self_1024_traffic.md",
                      "avg_launch_us": round(avg_launch_ms * 1e3, 2), "launches": dn.value,
+                     "launch_sample": f"1 in {sample_every} launches of the timed region",
                      "flop_per_launch": work_per_launch},
         "step": {"flop": flops["total"], "tflops": round(step_tflops, 2),
                  "mfma_frac": round(step_tflops / PEAK_BF16_TFLOPS, 4),

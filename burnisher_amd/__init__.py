@@ -139,6 +139,7 @@ SIGNATURES = {
     "bh_probe_device": ([_V, _V, _I64, ctypes.POINTER(ProbeResult)], _I),
     "bh_dit_destroy": ([_V], None),
     "bh_profile_enable": ([_I], _I),
+    "bh_profile_sample": ([_I], _I),
     "bh_profile_read": ([_I, ctypes.POINTER(_D), ctypes.POINTER(_I64), ctypes.POINTER(_D)], _I),
     "bh_fill_normal_bf16": ([_V, _I64, ctypes.c_uint64, ctypes.c_char_p, _F], _I),
     "bh_repeat": ([_V, _V, _I64, _I64, _I, _V], _I),

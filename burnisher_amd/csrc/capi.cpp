@@ -46,6 +46,8 @@ struct Record {
 struct Profiler {
     std::mutex mu;
     int mask = 0;
+    int every = 1;                  // bracket every `every`-th launch of a class
+    int64_t seen[K_COUNT] = {};     // launches of each enabled class since enable
     std::vector<hipEvent_t> free_events;
     std::vector<Record> pending;
     double total_ms[K_COUNT] = {};
@@ -100,6 +102,7 @@ ProfileScope::ProfileScope(int cls, hipStream_t stream, double work, int also)
     const bool want = (p.mask >> cls) & 1 || (also >= 0 && ((p.mask >> also) & 1));
     if (!want) return;
     std::lock_guard<std::mutex> lock(p.mu);
+    if (p.seen[cls]++ % p.every != 0) return;
     if (p.pending.size() >= 16384) p.settle(8192);
     Record r{(p.mask >> cls) & 1 ? cls : -1, (also >= 0 && ((p.mask >> also) & 1)) ? also : -1,
              p.take(), p.take(), work};
@@ -516,9 +519,19 @@ int bh_profile_enable(int mask) {
         std::lock_guard<std::mutex> lock(p.mu);
         p.settle(p.pending.size());
         p.mask = mask & ((1 << K_COUNT) - 1);
+        std::fill(std::begin(p.seen), std::end(p.seen), 0);
         std::fill(std::begin(p.total_ms), std::end(p.total_ms), 0.0);
         std::fill(std::begin(p.launches), std::end(p.launches), 0);
         std::fill(std::begin(p.work), std::end(p.work), 0.0);
+    });
+}
+
+int bh_profile_sample(int every) {
+    return guarded([&] {
+        require(every >= 1, "profile_sample: every must be at least 1");
+        Profiler& p = profiler();
+        std::lock_guard<std::mutex> lock(p.mu);
+        p.every = every;
     });
 }
 

@@ -425,6 +425,11 @@ typedef enum bh_kernel_class {
  * time is accumulated per class. Enabling resets the counters. Costs a little per launch;
  * off by default. */
 int bh_profile_enable(int class_mask);
+/* Bracket only the first of every `every` launches of each enabled class (counted per class from
+ * bh_profile_enable; 1, the default, brackets every launch). A sampled profile perturbs the
+ * stream it measures less: the launches between samples run with no event around them. It has no
+ * counterpart in the reference, whose timer brackets whole iterations. */
+int bh_profile_sample(int every);
 /* Sums since enable, synchronising on the recorded events: total ms, launches and algorithmic
  * FLOP (or bytes, for the bandwidth classes) per class. */
 int bh_profile_read(int kernel_class, double* total_ms, int64_t* launches, double* work);

@@ -266,6 +266,25 @@ def test_attention_key_splits_masked(hip):
     assert_within(from_bf16(g), from_bf16(want), "attention", "key splits, ragged")
 
 
+def test_launch_profiler_sampling(hip):
+    import ctypes
+    # bh_profile_sample(3) brackets launches 0, 3 and 6 of seven; every launch after sample(1)
+    B, S, H, D = 1, 256, 2, 72
+    q, k, v = (dev(randn_bf16(RNG, (B, S, H, D))) for _ in range(3))
+    out = empty((B, S, H, D))
+    ms, n, work = ctypes.c_double(), ctypes.c_int64(), ctypes.c_double()
+    for every, want in ((3, 3), (1, 7)):
+        call("bh_profile_sample", every)
+        call("bh_profile_enable", 1 << 2)   # BH_K_ATTN_SELF
+        for _ in range(7):
+            call("bh_attention", P(q), P(k), P(v), P(out), B, H, S, S, D, 0.0, None, None, F32, BF16, None)
+        call("bh_profile_read", 2, ctypes.byref(ms), ctypes.byref(n), ctypes.byref(work))
+        call("bh_profile_enable", 0)
+        assert n.value == want, (every, n.value)
+        assert ms.value > 0 and work.value == want * 4.0 * B * H * S * S * D
+    call("bh_profile_sample", 1)
+
+
 def test_attention_masked_values_do_not_leak(hip):
     B, S, KV, H, D = 2, 64, 150, 2, 72
     q, k, v = (randn_bf16(RNG, s) for s in ((B, S, H, D), (B, KV, H, D), (B, KV, H, D)))

@@ -59,6 +59,10 @@ def test_arguments_refused_before_any_device_work():
     assert lib.bh_last_error() == b""
     with pytest.raises(bh.BurnisherError):
         bh.call("bh_attention", None, None, None, None, 1, 1, 4, 0, 8, 0.0, None, None, 0, 1, None)
+    # the launch profiler's sampling stride is at least one launch
+    assert lib.bh_profile_sample(0) != 0
+    assert b"at least 1" in lib.bh_last_error()
+    assert lib.bh_profile_sample(1) == 0
 
 
 def test_fill_normal_is_seeded_by_name_and_split_free():
