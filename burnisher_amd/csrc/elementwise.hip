@@ -17,7 +17,16 @@
 namespace bh {
 namespace {
 
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));   // two bf16 from one conversion
+
 constexpr int kWave = 64;
+
+// The wave's index in its workgroup through readfirstlane: the compiler then knows it is uniform
+// and keeps a one-row-per-wave kernel's row, batch index and row addresses in scalar registers
+// instead of redoing that arithmetic (a 64-bit division among it) in every lane.
+__device__ __forceinline__ int wave_index() {
+    return __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
+}
 
 template <typename T> struct Io;
 template <> struct Io<float> {
@@ -100,7 +109,7 @@ __global__ void __launch_bounds__(256) k_norm(const T* __restrict__ x, const T* 
                                               const T* __restrict__ b, T* __restrict__ out,
                                               int64_t rows, int64_t cols, float eps, bool rms) {
     const int lane = threadIdx.x % kWave;
-    const int64_t row = static_cast<int64_t>(blockIdx.x) * (blockDim.x / kWave) + threadIdx.x / kWave;
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * (blockDim.x / kWave) + wave_index();
     if (row >= rows) return;
     const T* xr = x + row * cols;
     double mean = 0.0;
@@ -136,7 +145,7 @@ __global__ void __launch_bounds__(256) k_norm_rows(const bf16_t* __restrict__ x,
                                                    bf16_t* __restrict__ out, int64_t rows,
                                                    int64_t cols, float eps, bool rms) {
     const int lane = threadIdx.x % kWave;
-    const int64_t row = static_cast<int64_t>(blockIdx.x) * (blockDim.x / kWave) + threadIdx.x / kWave;
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * (blockDim.x / kWave) + wave_index();
     if (row >= rows) return;
     const int nvec = static_cast<int>(cols / 8);
     const bf16_t* xr = x + row * cols;
@@ -230,7 +239,7 @@ __global__ void __launch_bounds__(256) k_norm_modulate(
     const bf16_t* __restrict__ shift_tab, const bf16_t* __restrict__ scale_tab,
     bf16_t* __restrict__ out, int64_t rows, int64_t tokens, int64_t cols, float eps) {
     const int lane = threadIdx.x % kWave;
-    const int64_t row = static_cast<int64_t>(blockIdx.x) * (blockDim.x / kWave) + threadIdx.x / kWave;
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * (blockDim.x / kWave) + wave_index();
     if (row >= rows) return;
     const int nvec = static_cast<int>(cols / 8);
     const bf16_t* xr = x + row * cols;
@@ -242,7 +251,7 @@ __global__ void __launch_bounds__(256) k_norm_modulate(
         const int vi = lane + j * kWave;
         xv[j] = vi < nvec ? *reinterpret_cast<const uint4*>(xr + vi * 8) : make_uint4(0, 0, 0, 0);
     }
-    const int64_t b = row / tokens;
+    const int64_t b = static_cast<int>(row) / static_cast<int>(tokens);   // rows < 2^31
     // precomputed shift and scale are loaded before the statistics, so their latency overlaps
     uint4 shr[NV], scr[NV];
     if (PRE) {
@@ -330,12 +339,12 @@ __global__ void __launch_bounds__(256) k_norm_mod_dense(
     constexpr int kE = Row::kE;
     constexpr int pair0 = NV * 8 * kWave;   // first channel of the pairs
     const int lane = threadIdx.x % kWave;
-    const int64_t row = static_cast<int64_t>(blockIdx.x) * (blockDim.x / kWave) + threadIdx.x / kWave;
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * (blockDim.x / kWave) + wave_index();
     if (row >= rows) return;
     Row cur;
     cur.load(x + row * cols, lane);
     {
-        const int64_t b = row / tokens;
+        const int64_t b = static_cast<int>(row) / static_cast<int>(tokens);   // rows < 2^31
         float sh[kE], sc[kE];
 #pragma unroll
         for (int j = 0; j < NV; ++j) {
@@ -381,15 +390,17 @@ __global__ void __launch_bounds__(256) k_norm_mod_dense(
         uint32_t o[kE / 2];
 #pragma unroll
         for (int i = 0; i < kE / 2; ++i) {
-            float r[2];
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                const int e = 2 * i + h;
-                // normed is stored (rounded) by the norm op before modulate reads it
-                const float nrm = round_bf16(__fmul_rn(__fsub_rn(v[e], fmean), inv));
-                r[h] = __fadd_rn(__fmul_rn(nrm, sc[e]), sh[e]);
-            }
-            o[i] = static_cast<uint32_t>(f2bf(r[0])) | (static_cast<uint32_t>(f2bf(r[1])) << 16);
+            // normed is stored (rounded) by the norm op before modulate reads it: both values of
+            // the pair rounded by one conversion, then widened back
+            bf16x2_t nb;
+            nb[0] = static_cast<__bf16>(__fmul_rn(__fsub_rn(v[2 * i], fmean), inv));
+            nb[1] = static_cast<__bf16>(__fmul_rn(__fsub_rn(v[2 * i + 1], fmean), inv));
+            const uint32_t nw = __builtin_bit_cast(uint32_t, nb);
+            const float n0 = __uint_as_float(nw << 16), n1 = __uint_as_float(nw & 0xffff0000u);
+            bf16x2_t rb;
+            rb[0] = static_cast<__bf16>(__fadd_rn(__fmul_rn(n0, sc[2 * i]), sh[2 * i]));
+            rb[1] = static_cast<__bf16>(__fadd_rn(__fmul_rn(n1, sc[2 * i + 1]), sh[2 * i + 1]));
+            o[i] = __builtin_bit_cast(uint32_t, rb);
         }
         bf16_t* orow = out + row * cols;
 #pragma unroll
@@ -658,6 +669,7 @@ void dispatch_norm_modulate(const bf16_t* x, const bf16_t* mod, int64_t mod_stri
     require(aligned16(x) && aligned16(out) && aligned16(mod) && aligned16(shift_src) &&
                 aligned16(scale_src) && aligned16(shift_tab) && aligned16(scale_tab),
             "norm_modulate: every operand must be 16-byte aligned");
+    require(rows < (int64_t{1} << 31), "norm_modulate: 2^31 rows or more");
     const int nv = static_cast<int>((cols / 8 + kWave - 1) / kWave);
     const int grid = static_cast<int>((rows + 3) / 4);
 #define BH_NM(NV)                                                                             \
@@ -707,6 +719,7 @@ void launch_norm_modulate_f32(const bf16_t* x, const float* shift, const float* 
             "norm_modulate_f32: channels must be a multiple of 128 and at most 4096");
     require(aligned16(x) && aligned16(out) && aligned16(shift) && aligned16(scale1),
             "norm_modulate_f32: every operand must be 16-byte aligned");
+    require(rows < (int64_t{1} << 31), "norm_modulate_f32: 2^31 rows or more");
     const int nv = static_cast<int>(channels / 512), np = static_cast<int>(channels % 512 / 128);
     const int grid = static_cast<int>((rows + 3) / 4);
     const int c = static_cast<int>(channels);
