@@ -50,6 +50,14 @@ constexpr int kBBytes = BN * kRowBytes;           // 18 KiB
 // and the loop body has no per-wave branch.
 constexpr int kStageBytes = kABytes + kBBytes + 1024;   // 51 KiB
 constexpr int kMT = 4, kNT = 9;                   // 16x16 tiles per wave
+// The bias row of a tile (BN bf16) is loaded into LDS by the producers with the tile's first
+// k-tile, into one of three slots (tile index % 3), so the epilogue reads it from LDS. A global
+// load there would be issued after the previous chunk's stores, and waiting for it (vmcnt counts
+// loads and stores in issue order) would wait for those stores to be acknowledged.
+constexpr int kBiasSlots = 3, kBiasSlotBytes = 512;
+constexpr int kBiasOff = 3 * kStageBytes;
+constexpr int kSmemBytes = kBiasOff + kBiasSlots * kBiasSlotBytes;
+static_assert(BN * 2 <= kBiasSlotBytes, "bias row must fit its slot");
 
 // Epilogue modes. v = act(acc + bias), then:
 enum EpiMode {
@@ -212,7 +220,21 @@ struct Operands {
     int64_t M, N, K;
     ConvGeom cv;   // cv.in != null: A is the implicit im2col of a 3x3 convolution (see below)
     int64_t ldk;   // row stride of A and B (K, or the full K of a split-K slice)
+    const bf16_t* bias;   // [N] or null: copied to the LDS bias slot of each tile
 };
+
+__device__ __forceinline__ const bf16_t* bias_slot(const char* smem, int tile) {
+    return reinterpret_cast<const bf16_t*>(smem + kBiasOff + (tile % kBiasSlots) * kBiasSlotBytes);
+}
+
+// The bias row of the tile at n0 into its LDS slot: 18 lanes of producer wave 0, 16 bytes each.
+// Columns past N re-read the last 8 valid ones (never stored; N % 8 == 0 on this kernel's path).
+__device__ __forceinline__ void dma_bias(char* smem, const Operands& o, int64_t n0, int tile, int lane) {
+    if (lane < BN / 8) {
+        const int64_t n = min(n0 + lane * 8, o.N - 8);
+        dma16(o.bias + n, const_cast<char*>(reinterpret_cast<const char*>(bias_slot(smem, tile))));
+    }
+}
 
 // This lane's source address (at k = 0) for each of the wave's 13 DMA items of a tile: items
 // r < 8 are A row blocks 4r + wave, r >= 8 are B row blocks 4(r-8) + wave; the one B block that
@@ -365,6 +387,7 @@ __device__ __forceinline__ void produce(char* smem, const Operands& o, int KT, i
     const int total = my_tiles * KT;
     const bf16_t* src[kDmaItems];
     int it = 0, kt = 0;   // the next k-tile to issue
+    bool fresh = true;    // k-tile kt is the first of tile it, whose bias row is not loaded yet
     int64_t m0, n0;
     tile_origin(blockIdx.x, tiles_m, tiles_n, group_m, m0, n0);
     dma_sources(src, o, m0, n0, wave, lane);
@@ -372,6 +395,7 @@ __device__ __forceinline__ void produce(char* smem, const Operands& o, int KT, i
         if (++kt == KT) {
             kt = 0;
             ++it;
+            fresh = true;
             tile_origin(blockIdx.x + it * gridDim.x, tiles_m, tiles_n, group_m, m0, n0);
             dma_sources(src, o, m0, n0, wave, lane);
         }
@@ -388,7 +412,15 @@ __device__ __forceinline__ void produce(char* smem, const Operands& o, int KT, i
             px[r] = p - py[r] * o.cv.W;
         }
     };
+    // The bias DMA goes out before its k-tile's 13, so the producers' wait for that k-tile
+    // (at most 13 outstanding) also covers it, and the consumers see it from that barrier on.
+    // Slot it % 3 was last read in the epilogue of tile it - 3, which every consumer finished
+    // before the barrier at which this k-tile is issued (two k-tiles ahead of the consumers).
     auto issue = [&](char* stage_ptr) {
+        if (fresh) {
+            if (o.bias && wave == 0) dma_bias(smem, o, n0, it, lane);
+            fresh = false;
+        }
         if (conv) dma_tile_conv(stage_ptr, src, o, py, px, kt, wave, lane);
         else dma_tile(stage_ptr, src, static_cast<int64_t>(kt) * BK, wave);
     };
@@ -466,11 +498,11 @@ struct ChunkIn {
 template <int MODE, int P>
 __device__ __forceinline__ void chunk_load(ChunkIn<MODE, kW<P>>& in, const Epi& e, int64_t M,
                                            int64_t N, int64_t mb, int64_t n0, int hi,
-                                           bool gate_uniform) {
+                                           bool gate_uniform, const bf16_t* bias_lds) {
     constexpr int W = kW<P>;
     const int64_t n = n0 + chunk_col<P>(hi);
     if (n >= N) return;
-    if (e.bias) in.bias = ld_raw<W>(e.bias + n);
+    if (e.bias) in.bias = ld_raw<W>(bias_lds + chunk_col<P>(hi));
     if (MODE == EPI_GATED && gate_uniform) in.gate = ld_raw<W>(e.gate + (mb / e.gate_rows) * N + n);
 #pragma unroll
     for (int i = 0; i < kMT; ++i) {
@@ -552,12 +584,13 @@ __device__ __forceinline__ void chunk_store(const f32x4_t (&acc)[kMT][kNT],
 // and the 16 lanes of a column group write 128 contiguous bytes of one V^T row.
 template <int ACT, int P>
 __device__ __forceinline__ void vt_chunk(const f32x4_t (&acc)[kMT][kNT], const Epi& e, int64_t M,
-                                         int64_t N, int64_t mb, int64_t n0, int hi) {
+                                         int64_t N, int64_t mb, int64_t n0, int hi,
+                                         const bf16_t* bias_lds) {
     constexpr int W = kW<P>;
     const int col = chunk_col<P>(hi);
     if (n0 + col >= N) return;
     float b[W];
-    if (e.bias) unpack(ld_raw<W>(e.bias + n0 + col), b);
+    if (e.bias) unpack(ld_raw<W>(bias_lds + col), b);
     const int64_t batches = M / e.vt_seq;
     const int64_t bt = mb / e.vt_seq, tok = mb - bt * e.vt_seq;
     const bool whole = tok + kMT <= e.vt_seq && mb + kMT <= M;
@@ -593,15 +626,15 @@ __device__ __forceinline__ void vt_chunk(const f32x4_t (&acc)[kMT][kNT], const E
 template <int ACT, int MODE>
 __device__ __forceinline__ void epilogue(const f32x4_t (&acc)[kMT][kNT], const Epi& e,
                                          bf16_t* out, int64_t M, int64_t N, int64_t m0,
-                                         int64_t n0, int wave, int lane) {
+                                         int64_t n0, int wave, int lane, const bf16_t* bl) {
     const int lr = lane & 15, hi = lane >> 4;
     const int64_t mb = m0 + wave * 64 + lr * 4;   // this lane's rows: mb .. mb+3
     if (MODE == EPI_STORE && e.vt && n0 % e.vt_period >= e.vt_col0) {
-        vt_chunk<ACT, 0>(acc, e, M, N, mb, n0, hi);
-        vt_chunk<ACT, 1>(acc, e, M, N, mb, n0, hi);
-        vt_chunk<ACT, 2>(acc, e, M, N, mb, n0, hi);
-        vt_chunk<ACT, 3>(acc, e, M, N, mb, n0, hi);
-        vt_chunk<ACT, 4>(acc, e, M, N, mb, n0, hi);
+        vt_chunk<ACT, 0>(acc, e, M, N, mb, n0, hi, bl);
+        vt_chunk<ACT, 1>(acc, e, M, N, mb, n0, hi, bl);
+        vt_chunk<ACT, 2>(acc, e, M, N, mb, n0, hi, bl);
+        vt_chunk<ACT, 3>(acc, e, M, N, mb, n0, hi, bl);
+        vt_chunk<ACT, 4>(acc, e, M, N, mb, n0, hi, bl);
         return;
     }
     // gate rows are whole batches of tokens: one gate row per tile unless the tile straddles two
@@ -609,14 +642,14 @@ __device__ __forceinline__ void epilogue(const f32x4_t (&acc)[kMT][kNT], const E
     const bool gu = MODE == EPI_GATED && m0 / e.gate_rows == m_last / e.gate_rows;
     ChunkIn<MODE, 8> c0, c1, c2, c3;
     ChunkIn<MODE, 4> c4;
-    chunk_load<MODE, 0>(c0, e, M, N, mb, n0, hi, gu);
-    chunk_load<MODE, 1>(c1, e, M, N, mb, n0, hi, gu);
+    chunk_load<MODE, 0>(c0, e, M, N, mb, n0, hi, gu, bl);
+    chunk_load<MODE, 1>(c1, e, M, N, mb, n0, hi, gu, bl);
     chunk_store<ACT, MODE, 0>(acc, c0, e, out, M, N, mb, n0, hi, gu);
-    chunk_load<MODE, 2>(c2, e, M, N, mb, n0, hi, gu);
+    chunk_load<MODE, 2>(c2, e, M, N, mb, n0, hi, gu, bl);
     chunk_store<ACT, MODE, 1>(acc, c1, e, out, M, N, mb, n0, hi, gu);
-    chunk_load<MODE, 3>(c3, e, M, N, mb, n0, hi, gu);
+    chunk_load<MODE, 3>(c3, e, M, N, mb, n0, hi, gu, bl);
     chunk_store<ACT, MODE, 2>(acc, c2, e, out, M, N, mb, n0, hi, gu);
-    chunk_load<MODE, 4>(c4, e, M, N, mb, n0, hi, gu);
+    chunk_load<MODE, 4>(c4, e, M, N, mb, n0, hi, gu, bl);
     chunk_store<ACT, MODE, 3>(acc, c3, e, out, M, N, mb, n0, hi, gu);
     chunk_store<ACT, MODE, 4>(acc, c4, e, out, M, N, mb, n0, hi, gu);
 }
@@ -651,7 +684,8 @@ __device__ __forceinline__ void park_tile(const f32x4_t (&acc)[kMT][kNT], char* 
 
 template <int ACT, int MODE>
 __device__ __forceinline__ void store_staged(const char* smem, const Epi& e, bf16_t* out,
-                                             int64_t M, int64_t N, int64_t m0, int64_t n0) {
+                                             int64_t M, int64_t N, int64_t m0, int64_t n0,
+                                             const bf16_t* bias_lds) {
     const float* ctile = reinterpret_cast<const float*>(smem);
     if (MODE == EPI_STORE && e.vt && n0 % e.vt_period >= e.vt_col0) {
         // V columns: 8 consecutive tokens of one column per 16-byte store, consecutive threads
@@ -670,7 +704,7 @@ __device__ __forceinline__ void store_staged(const char* smem, const Epi& e, bf1
             if (n0 + col >= N) break;
             const int vc = vbase + col;
             const int h = vc / 72, dd = vc - h * 72;   // the vt store is built for head_dim 72
-            const float bias = e.bias ? bf2f(e.bias[n0 + col]) : 0.f;
+            const float bias = e.bias ? bf2f(bias_lds[col]) : 0.f;
             float v[8];
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
@@ -704,7 +738,7 @@ __device__ __forceinline__ void store_staged(const char* smem, const Epi& e, bf1
     const int64_t n = n0 + ch * 8;
     if (r0 >= kRowStep || n >= N) return;
     float bias[8];
-    if (e.bias) unpack8(*reinterpret_cast<const uint4*>(e.bias + n), bias);
+    if (e.bias) unpack8(*reinterpret_cast<const uint4*>(bias_lds + ch * 8), bias);
     else
 #pragma unroll
         for (int q = 0; q < 8; ++q) bias[q] = 0.f;
@@ -799,7 +833,7 @@ __device__ __forceinline__ void consume(char* smem, const Epi& e, bf16_t* out, i
         if (it + 1 < my_tiles) {
             int64_t m0, n0;
             tile_origin(blockIdx.x + it * gridDim.x, tiles_m, tiles_n, group_m, m0, n0);
-            epilogue<ACT, MODE>(acc, e, out, M, N, m0, n0, wave, lane);
+            epilogue<ACT, MODE>(acc, e, out, M, N, m0, n0, wave, lane, bias_slot(smem, it));
         } else {
             wait_and_join<63>();   // the producers' trailing copies have landed
             park_tile(acc, smem, wave, lane);
@@ -811,7 +845,7 @@ template <int ACT, int MODE, bool CONV>
 __global__ void __launch_bounds__(kWgThreads, 1)
 k_gemm_tn(const bf16_t* __restrict__ A, const bf16_t* __restrict__ B, bf16_t* out, int64_t M,
           int64_t N, int64_t K, Epi e, int tiles_m, int tiles_n, int group_m, ConvGeom cv) {
-    __shared__ __attribute__((aligned(1024))) char smem[3 * kStageBytes];
+    __shared__ __attribute__((aligned(1024))) char smem[kSmemBytes];
     const int T = tiles_m * tiles_n;
     const int my_tiles = (T - static_cast<int>(blockIdx.x) + static_cast<int>(gridDim.x) - 1) /
                          static_cast<int>(gridDim.x);
@@ -827,15 +861,15 @@ k_gemm_tn(const bf16_t* __restrict__ A, const bf16_t* __restrict__ B, bf16_t* ou
         out += static_cast<int64_t>(blockIdx.y) * M * e.ld_out * 2;   // float elements
     }
     if (wave >= kConsumers) {
-        produce<CONV>(smem, Operands{A, B, M, N, K, cv, ldk}, KT, my_tiles, tiles_m, tiles_n, group_m,
-                      wave - kConsumers, lane);
+        produce<CONV>(smem, Operands{A, B, M, N, K, cv, ldk, e.bias}, KT, my_tiles, tiles_m, tiles_n,
+                      group_m, wave - kConsumers, lane);
     } else {
         consume<ACT, MODE>(smem, e, out, M, N, KT, my_tiles, tiles_m, tiles_n, group_m, wave, lane);
     }
     wait_and_join<63>();   // the parked tile is complete and visible
     int64_t m0, n0;
     tile_origin(blockIdx.x + (my_tiles - 1) * gridDim.x, tiles_m, tiles_n, group_m, m0, n0);
-    store_staged<ACT, MODE>(smem, e, out, M, N, m0, n0);
+    store_staged<ACT, MODE>(smem, e, out, M, N, m0, n0, bias_slot(smem, my_tiles - 1));
 }
 
 // ---- small M: one wave per output column, both operands read with 16-byte loads ----
