@@ -95,12 +95,16 @@ __device__ __forceinline__ float gelu_tanh(float x) {
 }
 __device__ __forceinline__ float silu(float x) { return __fdiv_rn(x, __fadd_rn(1.0f, expf(-x))); }
 
-// The MFMA epilogue's GELU: 0.5 x (1 + tanh u) = x / (1 + exp(-2u)), with the hardware exp2 and
-// reciprocal. Its fp32 error (a few ulp) is far below the bf16 ulp it is rounded to, so it moves a
-// stored value by at most one bf16 ulp, the same bound the summation order already takes.
+// The MFMA epilogue's GELU: 0.5 x (1 + tanh u) = x / (1 + exp(-2u)), u = c (x + 0.044715 x^3),
+// with exp(-2u) = exp2(x (k0 + k1 x^2)), k0 = -2 c log2(e), k1 = 0.044715 k0: three VALU
+// operations before the hardware exp2 and reciprocal. Its fp32 error (under 1e-6 relative) is far
+// below the bf16 ulp it is rounded to, so it moves a stored value by at most one bf16 ulp, the
+// same bound the summation order already takes. Large |x| saturate cleanly: exp2 gives 0 (x) or
+// +inf (reciprocal 0, so -0).
 __device__ __forceinline__ float gelu_tanh_fast(float x) {
-    const float u = 0.7978845608028654f * (x + 0.044715f * x * x * x);
-    const float e = __builtin_amdgcn_exp2f(-2.8853900817779268f * u);   // exp(-2u)
+    constexpr float k0 = -2.0f * 0.7978845608028654f * 1.4426950408889634f;
+    constexpr float k1 = k0 * 0.044715f;
+    const float e = __builtin_amdgcn_exp2f(x * __builtin_fmaf(x * x, k1, k0));
     return x * __builtin_amdgcn_rcpf(1.0f + e);
 }
 __device__ __forceinline__ float silu_fast(float x) {
@@ -489,6 +493,18 @@ __device__ __forceinline__ float acc_at(const f32x4_t (&acc)[kMT][kNT], int i, i
 // IS the output in the engine's in-place updates). Stores start as early as they can: at the end
 // of a tile every CU stores at once and the epilogue runs at the memory's write rate, so a later
 // first store (all loads first) measured slower.
+// The bias values of a chunk, or -0.0 when there is no bias: v + (-0.0) is v exactly for every v
+// (signed zeros included), so the epilogue adds unconditionally instead of selecting per value.
+template <typename R, int W>
+__device__ __forceinline__ void bias_or_neg_zero(const Epi& e, const R& raw, float (&b)[W]) {
+    if (e.bias) {
+        unpack(raw, b);
+    } else {
+#pragma unroll
+        for (int q = 0; q < W; ++q) b[q] = -0.0f;
+    }
+}
+
 template <int MODE, int W>
 struct ChunkIn {
     Raw<W> bias, gate;
@@ -536,7 +552,7 @@ __device__ __forceinline__ void chunk_store(const f32x4_t (&acc)[kMT][kNT],
         return;
     }
     float b[W], gt[W];
-    if (e.bias) unpack(in.bias, b);
+    bias_or_neg_zero(e, in.bias, b);
     if (MODE == EPI_GATED && gate_uniform) unpack(in.gate, gt);
 #pragma unroll
     for (int i = 0; i < kMT; ++i) {
@@ -544,10 +560,7 @@ __device__ __forceinline__ void chunk_store(const f32x4_t (&acc)[kMT][kNT],
         if (m >= M) continue;
         float x[W], t[W];
 #pragma unroll
-        for (int q = 0; q < W; ++q) {
-            const float v = acc_at<P>(acc, i, q);
-            x[q] = act_fast<ACT>(e.bias ? __fadd_rn(v, b[q]) : v);
-        }
+        for (int q = 0; q < W; ++q) x[q] = act_fast<ACT>(__fadd_rn(acc_at<P>(acc, i, q), b[q]));
         if (MODE != EPI_STORE && e.round_mid)
 #pragma unroll
             for (int q = 0; q < W; ++q) x[q] = round_bf16(x[q]);
@@ -590,7 +603,7 @@ __device__ __forceinline__ void vt_chunk(const f32x4_t (&acc)[kMT][kNT], const E
     const int col = chunk_col<P>(hi);
     if (n0 + col >= N) return;
     float b[W];
-    if (e.bias) unpack(ld_raw<W>(bias_lds + col), b);
+    bias_or_neg_zero(e, e.bias ? ld_raw<W>(bias_lds + col) : Raw<W>{}, b);
     const int64_t batches = M / e.vt_seq;
     const int64_t bt = mb / e.vt_seq, tok = mb - bt * e.vt_seq;
     const bool whole = tok + kMT <= e.vt_seq && mb + kMT <= M;
@@ -602,10 +615,7 @@ __device__ __forceinline__ void vt_chunk(const f32x4_t (&acc)[kMT][kNT], const E
         const int h = vc / 72, dd = vc - h * 72;   // the vt store is built for head_dim 72
         float v[kMT];
 #pragma unroll
-        for (int i = 0; i < kMT; ++i) {
-            const float a = acc_at<P>(acc, i, q);
-            v[i] = act_fast<ACT>(e.bias ? __fadd_rn(a, b[q]) : a);
-        }
+        for (int i = 0; i < kMT; ++i) v[i] = act_fast<ACT>(__fadd_rn(acc_at<P>(acc, i, q), b[q]));
         if (whole) {
             uint2 r;
             pack(v, r);
@@ -704,13 +714,10 @@ __device__ __forceinline__ void store_staged(const char* smem, const Epi& e, bf1
             if (n0 + col >= N) break;
             const int vc = vbase + col;
             const int h = vc / 72, dd = vc - h * 72;   // the vt store is built for head_dim 72
-            const float bias = e.bias ? bf2f(bias_lds[col]) : 0.f;
+            const float bias = e.bias ? bf2f(bias_lds[col]) : -0.0f;
             float v[8];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const float a = ctile[ctile_at(rg * 8 + j, col)];
-                v[j] = act_fast<ACT>(e.bias ? __fadd_rn(a, bias) : a);
-            }
+            for (int j = 0; j < 8; ++j) v[j] = act_fast<ACT>(__fadd_rn(ctile[ctile_at(rg * 8 + j, col)], bias));
             const int64_t hrow = ((blk * batches + b) * e.vt_heads + h) * 72 + dd;
             if (whole) {   // two runs of four keys (vt_pos keeps runs of four together)
                 const uint4 p8 = pack8(v);
@@ -738,10 +745,7 @@ __device__ __forceinline__ void store_staged(const char* smem, const Epi& e, bf1
     const int64_t n = n0 + ch * 8;
     if (r0 >= kRowStep || n >= N) return;
     float bias[8];
-    if (e.bias) unpack8(*reinterpret_cast<const uint4*>(bias_lds + ch * 8), bias);
-    else
-#pragma unroll
-        for (int q = 0; q < 8; ++q) bias[q] = 0.f;
+    bias_or_neg_zero(e, e.bias ? *reinterpret_cast<const uint4*>(bias_lds + ch * 8) : uint4{}, bias);
     // gate rows are whole batches of tokens: one gate row per tile unless the tile straddles two
     const int64_t m_last = min(m0 + BM, M) - 1;
     const bool gate_uniform = MODE == EPI_GATED && m0 / e.gate_rows == m_last / e.gate_rows;
@@ -781,7 +785,7 @@ __device__ __forceinline__ void store_staged(const char* smem, const Epi& e, bf1
             }
             float x[8], t[8];
 #pragma unroll
-            for (int q = 0; q < 8; ++q) x[q] = act_fast<ACT>(e.bias ? __fadd_rn(v[i][q], bias[q]) : v[i][q]);
+            for (int q = 0; q < 8; ++q) x[q] = act_fast<ACT>(__fadd_rn(v[i][q], bias[q]));
             if (MODE != EPI_STORE && e.round_mid)
 #pragma unroll
                 for (int q = 0; q < 8; ++q) x[q] = round_bf16(x[q]);
@@ -1131,12 +1135,9 @@ __global__ void __launch_bounds__(256) k_splitk_epi(const float* __restrict__ pa
             }
         }
         float x[8], bias[8], t[8];
-        if (e.bias) unpack8(*reinterpret_cast<const uint4*>(e.bias + n), bias);
+        bias_or_neg_zero(e, e.bias ? *reinterpret_cast<const uint4*>(e.bias + n) : uint4{}, bias);
 #pragma unroll
-        for (int q = 0; q < 8; ++q) {
-            const float v = q < 4 ? lo[q] : hi[q - 4];
-            x[q] = act_fast<ACT>(e.bias ? __fadd_rn(v, bias[q]) : v);
-        }
+        for (int q = 0; q < 8; ++q) x[q] = act_fast<ACT>(__fadd_rn(q < 4 ? lo[q] : hi[q - 4], bias[q]));
         if (MODE != EPI_STORE && e.round_mid)
 #pragma unroll
             for (int q = 0; q < 8; ++q) x[q] = round_bf16(x[q]);
