@@ -41,23 +41,41 @@
 namespace bh {
 namespace {
 
-constexpr int BM = 256, BN = 144, BK = 64;
+constexpr int BN = 144, BK = 64;
 constexpr int kRowBytes = BK * 2;                 // 128
-constexpr int kABytes = BM * kRowBytes;           // 32 KiB
 constexpr int kBBytes = BN * kRowBytes;           // 18 KiB
-// Each stage also has one spare 1 KiB row block: waves 2-3 have one B row block fewer than waves
-// 0-1 and load a duplicate into it, so every wave issues the same 13 DMA instructions per k-tile
-// and the loop body has no per-wave branch.
-constexpr int kStageBytes = kABytes + kBBytes + 1024;   // 51 KiB
-constexpr int kMT = 4, kNT = 9;                   // 16x16 tiles per wave
+constexpr int kNT = 9;                            // 16x16 column tiles per consumer wave
 // The bias row of a tile (BN bf16) is loaded into LDS by the producers with the tile's first
-// k-tile, into one of three slots (tile index % 3), so the epilogue reads it from LDS. A global
-// load there would be issued after the previous chunk's stores, and waiting for it (vmcnt counts
-// loads and stores in issue order) would wait for those stores to be acknowledged.
-constexpr int kBiasSlots = 3, kBiasSlotBytes = 512;
-constexpr int kBiasOff = 3 * kStageBytes;
-constexpr int kSmemBytes = kBiasOff + kBiasSlots * kBiasSlotBytes;
+// k-tile, into one of kStages slots (tile index % kStages), so the epilogue reads it from LDS. A
+// global load there would be issued after the previous chunk's stores, and waiting for it (vmcnt
+// counts loads and stores in issue order) would wait for those stores to be acknowledged.
+constexpr int kBiasSlotBytes = 512;
 static_assert(BN * 2 <= kBiasSlotBytes, "bias row must fit its slot");
+
+// Tile height: each of the four consumer waves owns MT 16-row blocks, so a tile is BM = 64 MT rows
+// (256 for the DiT's 8192-row GEMMs; 128 and 64 for short-M shapes, whose 256-row tiles would fill
+// few CUs). Each stage also has one spare 1 KiB row block: waves 2-3 have one B row block fewer
+// than waves 0-1 and load a duplicate into it, so every wave issues the same number of DMA
+// instructions per k-tile (BM / 32 + 5) and the loop body has no per-wave branch. A shorter tile
+// keeps more k-tiles in flight in the LDS it frees: kStages - 1 of them ahead of the consumers.
+template <int MT>
+struct Geom {
+    static_assert(MT == 1 || MT == 2 || MT == 4, "tile height: 64, 128 or 256 rows");
+    static constexpr int BM = 64 * MT;
+    static constexpr int kABytes = BM * kRowBytes;                    // 32 KiB at MT = 4
+    static constexpr int kStageBytes = kABytes + kBBytes + 1024;      // 51 KiB at MT = 4
+    static constexpr int kStages = MT == 4 ? 3 : MT == 2 ? 4 : 5;
+    static constexpr int kDmaItems = BM / 32 + (BN / 8 + 3) / 4;      // 13 per wave at MT = 4
+    // The slot of tile t is written kStages - 1 k-tiles ahead of the consumers and read in tile
+    // t's epilogue; the next tile to use it starts KT * kBiasSlots k-tiles later, so kStages
+    // slots keep the two apart even at one k-tile per tile.
+    static constexpr int kBiasSlots = kStages;
+    static constexpr int kBiasOff = kStages * kStageBytes;
+    static constexpr int kSmemBytes = kBiasOff + kBiasSlots * kBiasSlotBytes;
+    static_assert(kSmemBytes <= 160 * 1024, "LDS");
+    static_assert((kStages - 2) * kDmaItems + 1 <= 63, "vmcnt");
+};
+constexpr int kMaxMT = 4;   // the DiT's tile (256 rows): split-K, the transposed V store, convs
 
 // Epilogue modes. v = act(acc + bias), then:
 enum EpiMode {
@@ -191,20 +209,21 @@ __device__ __forceinline__ void dma16(const void* src, const char* lds) {
 //    128 + 4hi + t for j = 8. A lane then owns columns 32p + 8hi .. +7 (accumulators j = 2p and
 //    2p+1, p < 4) and 128 + 4hi .. +3 (j = 8) of each of its rows: one 16-byte store per row and
 //    p, and the four lanes of a row cover 64 contiguous bytes.
+template <int MT>
 __device__ __forceinline__ int a_row(int r) {
-    return (r & ~63) | ((r & 15) << 2) | ((r >> 4) & 3);
+    constexpr int W = 16 * MT;   // LDS rows of one consumer wave
+    return (r & ~(W - 1)) | ((r & 15) * MT) | ((r >> 4) & (MT - 1));
 }
 __device__ __forceinline__ int b_col(int n) {
     const int j = n >> 4, hi = (n >> 2) & 3, t = n & 3;
     return j < 8 ? ((j >> 1) << 5) | (hi << 3) | ((j & 1) << 2) | t : 128 + (hi << 2) + t;
 }
 
-constexpr int kDmaItems = BM / 32 + (BN / 8 + 3) / 4;   // 13 per wave per k-tile
-
 // Tile v of the launch -> (tm, tn). Workgroup b runs on XCD b % 8 and, persistent, takes tiles
 // b, b + G, b + 2G, ... (G = grid, a multiple of 8 whenever T is), so tiles are renumbered to
 // give each XCD a contiguous band of the M x N tile grid, walked `group_m` M-tiles at a time,
 // whose A and B panels share that XCD's L2.
+template <int MT>
 __device__ __forceinline__ void tile_origin(int v, int tiles_m, int tiles_n, int group_m,
                                             int64_t& m0, int64_t& n0) {
     const int T = tiles_m * tiles_n;
@@ -214,7 +233,7 @@ __device__ __forceinline__ void tile_origin(int v, int tiles_m, int tiles_n, int
     const int first_m = g * group_m;
     const int gm = min(tiles_m - first_m, group_m);
     const int in_group = v - g * group_size;
-    m0 = static_cast<int64_t>(first_m + in_group % gm) * BM;
+    m0 = static_cast<int64_t>(first_m + in_group % gm) * Geom<MT>::BM;
     n0 = static_cast<int64_t>(in_group / gm) * BN;
 }
 
@@ -227,33 +246,37 @@ struct Operands {
     const bf16_t* bias;   // [N] or null: copied to the LDS bias slot of each tile
 };
 
+template <int MT>
 __device__ __forceinline__ const bf16_t* bias_slot(const char* smem, int tile) {
-    return reinterpret_cast<const bf16_t*>(smem + kBiasOff + (tile % kBiasSlots) * kBiasSlotBytes);
+    return reinterpret_cast<const bf16_t*>(smem + Geom<MT>::kBiasOff + (tile % Geom<MT>::kBiasSlots) * kBiasSlotBytes);
 }
 
 // The bias row of the tile at n0 into its LDS slot: 18 lanes of producer wave 0, 16 bytes each.
 // Columns past N re-read the last 8 valid ones (never stored; N % 8 == 0 on this kernel's path).
+template <int MT>
 __device__ __forceinline__ void dma_bias(char* smem, const Operands& o, int64_t n0, int tile, int lane) {
     if (lane < BN / 8) {
         const int64_t n = min(n0 + lane * 8, o.N - 8);
-        dma16(o.bias + n, const_cast<char*>(reinterpret_cast<const char*>(bias_slot(smem, tile))));
+        dma16(o.bias + n, const_cast<char*>(reinterpret_cast<const char*>(bias_slot<MT>(smem, tile))));
     }
 }
 
-// This lane's source address (at k = 0) for each of the wave's 13 DMA items of a tile: items
-// r < 8 are A row blocks 4r + wave, r >= 8 are B row blocks 4(r-8) + wave; the one B block that
-// does not exist (waves 2-3, r = 12) repeats the last into the stage's spare block. Each lane
+// This lane's source address (at k = 0) for each of the wave's DMA items of a tile (13 at MT = 4):
+// items r < BM/32 are A row blocks 4r + wave, the rest B row blocks 4(r - BM/32) + wave; the one B
+// block that does not exist (waves 2-3, last item) repeats the last into the stage's spare block. Each lane
 // moves 16 bytes: LDS row rb*8 + lane/8, swizzled chunk lane%8. Rows past M or N re-read the
 // last valid row; their results are never stored.
-__device__ __forceinline__ void dma_sources(const bf16_t* (&src)[kDmaItems], const Operands& o,
+template <int MT>
+__device__ __forceinline__ void dma_sources(const bf16_t* (&src)[Geom<MT>::kDmaItems], const Operands& o,
                                             int64_t m0, int64_t n0, int wave, int lane) {
+    constexpr int BM = Geom<MT>::BM;
     const int sub = lane >> 3, slot = lane & 7;
 #pragma unroll
-    for (int r = 0; r < kDmaItems; ++r) {
+    for (int r = 0; r < Geom<MT>::kDmaItems; ++r) {
         if (r < BM / 32) {
             const int row_in = (r * 4 + wave) * 8 + sub;
             const int c = slot ^ ((row_in >> 1) & 7);
-            const int64_t row = min(m0 + a_row(row_in), o.M - 1);
+            const int64_t row = min(m0 + a_row<MT>(row_in), o.M - 1);
             src[r] = o.A + row * o.ldk + c * 8;
         } else {
             const int row_in = min((r - BM / 32) * 4 + wave, BN / 8 - 1) * 8 + sub;
@@ -264,13 +287,15 @@ __device__ __forceinline__ void dma_sources(const bf16_t* (&src)[kDmaItems], con
     }
 }
 
-// The whole k-tile at `k0` into one stage: 13 DMA instructions per producer wave.
-__device__ __forceinline__ void dma_tile(char* stage, const bf16_t* const (&src)[kDmaItems],
+// The whole k-tile at `k0` into one stage: 13 DMA instructions per producer wave at MT = 4.
+template <int MT>
+__device__ __forceinline__ void dma_tile(char* stage, const bf16_t* const (&src)[Geom<MT>::kDmaItems],
                                          int64_t k0, int wave) {
+    constexpr int BM = Geom<MT>::BM;
 #pragma unroll
-    for (int r = 0; r < kDmaItems; ++r) {
+    for (int r = 0; r < Geom<MT>::kDmaItems; ++r) {
         const int rb = r < BM / 32 ? r * 4 + wave : min((r - BM / 32) * 4 + wave, BN / 8);
-        dma16(src[r] + k0, stage + (r < BM / 32 ? 0 : kABytes) + rb * 1024);
+        dma16(src[r] + k0, stage + (r < BM / 32 ? 0 : Geom<MT>::kABytes) + rb * 1024);
     }
 }
 
@@ -279,9 +304,11 @@ __device__ __forceinline__ void dma_tile(char* stage, const bf16_t* const (&src)
 // is 128 contiguous bytes of one input pixel: the output pixel's neighbour (y + ky - 1,
 // x + kx - 1), halved when the input is upsampled 2x on the fly, or the zero row for a tap in the
 // padding. B rows (the weights, repacked [c_out][ky][kx][c_in]) stream as in the plain GEMM.
-__device__ __forceinline__ void dma_tile_conv(char* stage, const bf16_t* const (&src)[kDmaItems],
-                                              const Operands& o, const int (&py)[BM / 32],
-                                              const int (&px)[BM / 32], int kt, int wave, int lane) {
+template <int MT>
+__device__ __forceinline__ void dma_tile_conv(char* stage, const bf16_t* const (&src)[Geom<MT>::kDmaItems],
+                                              const Operands& o, const int (&py)[Geom<MT>::BM / 32],
+                                              const int (&px)[Geom<MT>::BM / 32], int kt, int wave, int lane) {
+    constexpr int BM = Geom<MT>::BM;
     const ConvGeom& c = o.cv;
     const int cb_count = c.c_in >> 6;
     const int tap = kt / cb_count, cb = kt - tap * cb_count;
@@ -304,53 +331,55 @@ __device__ __forceinline__ void dma_tile_conv(char* stage, const bf16_t* const (
     }
     const int64_t k0 = static_cast<int64_t>(kt) * BK;
 #pragma unroll
-    for (int r = BM / 32; r < kDmaItems; ++r) {
+    for (int r = BM / 32; r < Geom<MT>::kDmaItems; ++r) {
         const int rb = min((r - BM / 32) * 4 + wave, BN / 8);
-        dma16(src[r] + k0, stage + kABytes + rb * 1024);
+        dma16(src[r] + k0, stage + Geom<MT>::kABytes + rb * 1024);
     }
 }
 
-// One k-tile of MFMAs for a consumer wave out of `cur`: 4 activation fragments per K=32 half
-// (rows 64w + 16i + lane%16) and 9 weight fragments (rows 16j + lane%16), 72 MFMAs. The second
+// One k-tile of MFMAs for a consumer wave out of `cur`: MT activation fragments per K=32 half
+// (rows 16 MT w + 16i + lane%16) and 9 weight fragments (rows 16j + lane%16), 72 MFMAs at MT = 4
+// (the figures below are for that tile). The second
 // half's weight fragment j is read into the registers of the first half's, right after the four
 // MFMAs that consume it, so only 17 fragments (68 VGPRs) are live: two waves per SIMD fit in the
 // register file with the 144 accumulators. `off0`/`off1` are this lane's byte offsets of its
 // chunk within a 16-row block for the two halves (row lane%16, chunk 4*half + lane/16, swizzled).
 __device__ __forceinline__ bf16x8_t frag(const char* p) { return *reinterpret_cast<const bf16x8_t*>(p); }
 
-__device__ __forceinline__ void consume_tile(f32x4_t (&acc)[kMT][kNT], const char* cur, int wave,
+template <int MT>
+__device__ __forceinline__ void consume_tile(f32x4_t (&acc)[MT][kNT], const char* cur, int wave,
                                              int off0, int off1) {
-    const char* a_rows = cur + wave * 64 * kRowBytes;
-    const char* b_rows = cur + kABytes;
-    bf16x8_t a0[kMT], a1[kMT], b[kNT];
+    const char* a_rows = cur + wave * 16 * MT * kRowBytes;
+    const char* b_rows = cur + Geom<MT>::kABytes;
+    bf16x8_t a0[MT], a1[MT], b[kNT];
 #pragma unroll
-    for (int i = 0; i < kMT; ++i) a0[i] = frag(a_rows + i * 16 * kRowBytes + off0);
+    for (int i = 0; i < MT; ++i) a0[i] = frag(a_rows + i * 16 * kRowBytes + off0);
 #pragma unroll
     for (int j = 0; j < kNT; ++j) b[j] = frag(b_rows + j * 16 * kRowBytes + off0);
 #pragma unroll
-    for (int i = 0; i < kMT; ++i) a1[i] = frag(a_rows + i * 16 * kRowBytes + off1);
+    for (int i = 0; i < MT; ++i) a1[i] = frag(a_rows + i * 16 * kRowBytes + off1);
 #pragma unroll
     for (int j = 0; j < kNT; ++j) {
 #pragma unroll
-        for (int i = 0; i < kMT; ++i)
+        for (int i = 0; i < MT; ++i)
             acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(b[j], a0[i], acc[i][j], 0, 0, 0);
         b[j] = frag(b_rows + j * 16 * kRowBytes + off1);
     }
 #pragma unroll
     for (int j = 0; j < kNT; ++j)
 #pragma unroll
-        for (int i = 0; i < kMT; ++i)
+        for (int i = 0; i < MT; ++i)
             acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(b[j], a1[i], acc[i][j], 0, 0, 0);
     // Keep that order: all 17 first reads up front, each second-half weight read right after its
     // register's last use, then the second half. Left alone, the scheduler sinks every read next
     // to its first use and exposes the LDS latency before each group of four MFMAs.
-    __builtin_amdgcn_sched_group_barrier(0x100, 2 * kMT + kNT, 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, 2 * MT + kNT, 0);
 #pragma unroll
     for (int j = 0; j < kNT; ++j) {
-        __builtin_amdgcn_sched_group_barrier(0x008, kMT, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, MT, 0);
         __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, kMT * kNT, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, MT * kNT, 0);
 }
 
 // Waits until this wave has at most N vector-memory operations outstanding and none of its LDS
@@ -371,37 +400,39 @@ __device__ __forceinline__ void wait_and_join() {
 // MFMAs, here it only delays the producer, and the consumer on the same SIMD keeps the matrix
 // core busy.
 //
-// The workgroup's k-tiles are numbered g = 0 .. total-1 across all its tiles (stage g % 3). Per g,
-// every wave:
-//   producers: wait until k-tile g has landed (g+1 may still be in flight)
+// The workgroup's k-tiles are numbered g = 0 .. total-1 across all its tiles (stage g % S, S =
+// kStages: 3 for the 256-row tile). Per g, every wave:
+//   producers: wait until k-tile g has landed (g+1 .. g+S-2 may still be in flight)
 //   consumers: wait until their LDS reads of the previous stage are done
 //   barrier
-//   producers: DMA k-tile g+2 -> stage (g+2) % 3 (it held g-1, which every consumer finished
+//   producers: DMA k-tile g+S-1 -> stage (g+S-1) % S (it held g-1, which every consumer finished
 //              reading before the barrier)
-//   consumers: multiply stage g % 3; after a tile's last k-tile, its epilogue
-// so while the consumers store one tile, the first two k-tiles of the next are already loading.
-// The last two steps load a copy of the last k-tile into stages nobody reads again, which keeps
+//   consumers: multiply stage g % S; after a tile's last k-tile, its epilogue
+// so while the consumers store one tile, the first S-1 k-tiles of the next are already loading.
+// The last S-1 steps load a copy of the last k-tile into stages nobody reads again, which keeps
 // every step's wait count identical.
 constexpr int kConsumers = 4;
 constexpr int kWgThreads = 2 * kConsumers * 64;   // 512
 
-template <bool CONV>
+template <int MT, bool CONV>
 __device__ __forceinline__ void produce(char* smem, const Operands& o, int KT, int my_tiles,
                                         int tiles_m, int tiles_n, int group_m, int wave, int lane) {
+    using G = Geom<MT>;
+    constexpr int BM = G::BM;
     const int total = my_tiles * KT;
-    const bf16_t* src[kDmaItems];
+    const bf16_t* src[G::kDmaItems];
     int it = 0, kt = 0;   // the next k-tile to issue
     bool fresh = true;    // k-tile kt is the first of tile it, whose bias row is not loaded yet
     int64_t m0, n0;
-    tile_origin(blockIdx.x, tiles_m, tiles_n, group_m, m0, n0);
-    dma_sources(src, o, m0, n0, wave, lane);
+    tile_origin<MT>(blockIdx.x, tiles_m, tiles_n, group_m, m0, n0);
+    dma_sources<MT>(src, o, m0, n0, wave, lane);
     auto advance = [&]() {
         if (++kt == KT) {
             kt = 0;
             ++it;
             fresh = true;
-            tile_origin(blockIdx.x + it * gridDim.x, tiles_m, tiles_n, group_m, m0, n0);
-            dma_sources(src, o, m0, n0, wave, lane);
+            tile_origin<MT>(blockIdx.x + it * gridDim.x, tiles_m, tiles_n, group_m, m0, n0);
+            dma_sources<MT>(src, o, m0, n0, wave, lane);
         }
     };
     // Implicit convolution: the output pixel of each A item of this lane, per tile.
@@ -411,42 +442,47 @@ __device__ __forceinline__ void produce(char* smem, const Operands& o, int KT, i
 #pragma unroll
         for (int r = 0; r < BM / 32; ++r) {
             const int row_in = (r * 4 + wave) * 8 + (lane >> 3);
-            const int p = static_cast<int>(min(m0 + a_row(row_in), o.M - 1));
+            const int p = static_cast<int>(min(m0 + a_row<MT>(row_in), o.M - 1));
             py[r] = p / o.cv.W;
             px[r] = p - py[r] * o.cv.W;
         }
     };
-    // The bias DMA goes out before its k-tile's 13, so the producers' wait for that k-tile
-    // (at most 13 outstanding) also covers it, and the consumers see it from that barrier on.
-    // Slot it % 3 was last read in the epilogue of tile it - 3, which every consumer finished
-    // before the barrier at which this k-tile is issued (two k-tiles ahead of the consumers).
+    // The bias DMA goes out before its k-tile's items, so the producers' wait for that k-tile (at
+    // most one k-tile's items outstanding) also covers it, and the consumers see it from that
+    // barrier on.
+    // Slot it % S was last read in the epilogue of tile it - S, which every consumer finished
+    // before the barrier at which this k-tile is issued (S - 1 k-tiles ahead of the consumers).
     auto issue = [&](char* stage_ptr) {
         if (fresh) {
-            if (o.bias && wave == 0) dma_bias(smem, o, n0, it, lane);
+            if (o.bias && wave == 0) dma_bias<MT>(smem, o, n0, it, lane);
             fresh = false;
         }
-        if (conv) dma_tile_conv(stage_ptr, src, o, py, px, kt, wave, lane);
-        else dma_tile(stage_ptr, src, static_cast<int64_t>(kt) * BK, wave);
+        if (conv) dma_tile_conv<MT>(stage_ptr, src, o, py, px, kt, wave, lane);
+        else dma_tile<MT>(stage_ptr, src, static_cast<int64_t>(kt) * BK, wave);
     };
+    constexpr int S = G::kStages;
     if (conv) conv_rows();
-    issue(smem);
-    if (total > 1) {
-        const int it0 = it;
-        advance();
-        if (conv && it != it0) conv_rows();
-    }
-    issue(smem + kStageBytes);
-    int stage = 0;
-    for (int g = 0; g < total; ++g) {
-        wait_and_join<kDmaItems>();
-        if (g + 2 < total) {
+    issue(smem);   // k-tiles 0 .. S-2 into stages 0 .. S-2 (past the last k-tile, copies of it)
+#pragma unroll
+    for (int q = 1; q < S - 1; ++q) {
+        if (q < total) {
             const int it0 = it;
             advance();
             if (conv && it != it0) conv_rows();
         }
-        const int s2 = stage == 0 ? 2 : stage - 1;   // (g + 2) % 3
-        issue(smem + s2 * kStageBytes);
-        stage = stage == 2 ? 0 : stage + 1;
+        issue(smem + q * G::kStageBytes);
+    }
+    int stage = 0;   // the stage of k-tile g
+    for (int g = 0; g < total; ++g) {
+        wait_and_join<(S - 2) * G::kDmaItems>();
+        if (g + S - 1 < total) {
+            const int it0 = it;
+            advance();
+            if (conv && it != it0) conv_rows();
+        }
+        const int sf = stage == 0 ? S - 1 : stage - 1;   // (g + S - 1) % S, k-tile g - 1's stage
+        issue(smem + sf * G::kStageBytes);
+        stage = stage == S - 1 ? 0 : stage + 1;
     }
     wait_and_join<0>();   // the trailing copies have landed before the LDS holds the output
 }
@@ -482,8 +518,8 @@ __device__ __forceinline__ void pack(const float (&f)[4], uint2& r) {
 template <int P> constexpr int kW = P < 4 ? 8 : 4;
 template <int P>
 __device__ __forceinline__ int chunk_col(int hi) { return P < 4 ? 32 * P + 8 * hi : 128 + 4 * hi; }
-template <int P>
-__device__ __forceinline__ float acc_at(const f32x4_t (&acc)[kMT][kNT], int i, int q) {
+template <int MT, int P>
+__device__ __forceinline__ float acc_at(const f32x4_t (&acc)[MT][kNT], int i, int q) {
     if constexpr (P < 4) return q < 4 ? acc[i][2 * P][q] : acc[i][2 * P + 1][q - 4];
     else return acc[i][8][q];
 }
@@ -505,14 +541,14 @@ __device__ __forceinline__ void bias_or_neg_zero(const Epi& e, const R& raw, flo
     }
 }
 
-template <int MODE, int W>
+template <int MODE, int W, int MT>
 struct ChunkIn {
     Raw<W> bias, gate;
-    Raw<W> row[kMT];    // residual or row_add
+    Raw<W> row[MT];    // residual or row_add
 };
 
-template <int MODE, int P>
-__device__ __forceinline__ void chunk_load(ChunkIn<MODE, kW<P>>& in, const Epi& e, int64_t M,
+template <int MT, int MODE, int P>
+__device__ __forceinline__ void chunk_load(ChunkIn<MODE, kW<P>, MT>& in, const Epi& e, int64_t M,
                                            int64_t N, int64_t mb, int64_t n0, int hi,
                                            bool gate_uniform, const bf16_t* bias_lds) {
     constexpr int W = kW<P>;
@@ -521,7 +557,7 @@ __device__ __forceinline__ void chunk_load(ChunkIn<MODE, kW<P>>& in, const Epi& 
     if (e.bias) in.bias = ld_raw<W>(bias_lds + chunk_col<P>(hi));
     if (MODE == EPI_GATED && gate_uniform) in.gate = ld_raw<W>(e.gate + (mb / e.gate_rows) * N + n);
 #pragma unroll
-    for (int i = 0; i < kMT; ++i) {
+    for (int i = 0; i < MT; ++i) {
         const int64_t m = mb + i;
         if (m >= M) continue;
         if (MODE == EPI_RESIDUAL || MODE == EPI_GATED)
@@ -530,9 +566,9 @@ __device__ __forceinline__ void chunk_load(ChunkIn<MODE, kW<P>>& in, const Epi& 
     }
 }
 
-template <int ACT, int MODE, int P>
-__device__ __forceinline__ void chunk_store(const f32x4_t (&acc)[kMT][kNT],
-                                            const ChunkIn<MODE, kW<P>>& in, const Epi& e,
+template <int MT, int ACT, int MODE, int P>
+__device__ __forceinline__ void chunk_store(const f32x4_t (&acc)[MT][kNT],
+                                            const ChunkIn<MODE, kW<P>, MT>& in, const Epi& e,
                                             bf16_t* out, int64_t M, int64_t N, int64_t mb,
                                             int64_t n0, int hi, bool gate_uniform) {
     constexpr int W = kW<P>;
@@ -540,14 +576,14 @@ __device__ __forceinline__ void chunk_store(const f32x4_t (&acc)[kMT][kNT],
     if (n >= N) return;
     if constexpr (MODE == EPI_F32) {
 #pragma unroll
-        for (int i = 0; i < kMT; ++i) {
+        for (int i = 0; i < MT; ++i) {
             const int64_t m = mb + i;
             if (m >= M) continue;
             float* dst = reinterpret_cast<float*>(out) + m * e.ld_out + n;
 #pragma unroll
             for (int q = 0; q < W; q += 4)
-                *reinterpret_cast<f32x4_t*>(dst + q) = f32x4_t{acc_at<P>(acc, i, q), acc_at<P>(acc, i, q + 1),
-                                                              acc_at<P>(acc, i, q + 2), acc_at<P>(acc, i, q + 3)};
+                *reinterpret_cast<f32x4_t*>(dst + q) = f32x4_t{acc_at<MT, P>(acc, i, q), acc_at<MT, P>(acc, i, q + 1),
+                                                              acc_at<MT, P>(acc, i, q + 2), acc_at<MT, P>(acc, i, q + 3)};
         }
         return;
     }
@@ -555,12 +591,12 @@ __device__ __forceinline__ void chunk_store(const f32x4_t (&acc)[kMT][kNT],
     bias_or_neg_zero(e, in.bias, b);
     if (MODE == EPI_GATED && gate_uniform) unpack(in.gate, gt);
 #pragma unroll
-    for (int i = 0; i < kMT; ++i) {
+    for (int i = 0; i < MT; ++i) {
         const int64_t m = mb + i;
         if (m >= M) continue;
         float x[W], t[W];
 #pragma unroll
-        for (int q = 0; q < W; ++q) x[q] = act_fast<ACT>(__fadd_rn(acc_at<P>(acc, i, q), b[q]));
+        for (int q = 0; q < W; ++q) x[q] = act_fast<ACT>(__fadd_rn(acc_at<MT, P>(acc, i, q), b[q]));
         if (MODE != EPI_STORE && e.round_mid)
 #pragma unroll
             for (int q = 0; q < W; ++q) x[q] = round_bf16(x[q]);
@@ -595,8 +631,8 @@ __device__ __forceinline__ void chunk_store(const f32x4_t (&acc)[kMT][kNT],
 // V columns of the fused QKV projection go to V^T (vt[(blk*B + b)*heads + h)*72 + d][vt_pos(token)]):
 // a lane's four rows are four consecutive tokens, so each of its columns is one 8-byte store,
 // and the 16 lanes of a column group write 128 contiguous bytes of one V^T row.
-template <int ACT, int P>
-__device__ __forceinline__ void vt_chunk(const f32x4_t (&acc)[kMT][kNT], const Epi& e, int64_t M,
+template <int MT, int ACT, int P>
+__device__ __forceinline__ void vt_chunk(const f32x4_t (&acc)[MT][kNT], const Epi& e, int64_t M,
                                          int64_t N, int64_t mb, int64_t n0, int hi,
                                          const bf16_t* bias_lds) {
     constexpr int W = kW<P>;
@@ -606,16 +642,16 @@ __device__ __forceinline__ void vt_chunk(const f32x4_t (&acc)[kMT][kNT], const E
     bias_or_neg_zero(e, e.bias ? ld_raw<W>(bias_lds + col) : Raw<W>{}, b);
     const int64_t batches = M / e.vt_seq;
     const int64_t bt = mb / e.vt_seq, tok = mb - bt * e.vt_seq;
-    const bool whole = tok + kMT <= e.vt_seq && mb + kMT <= M;
+    const bool whole = tok + MT <= e.vt_seq && mb + MT <= M;
     const int vbase = static_cast<int>(n0 % e.vt_period - e.vt_col0) + col;
     const int64_t blk = n0 / e.vt_period;
 #pragma unroll
     for (int q = 0; q < W; ++q) {
         const int vc = vbase + q;
         const int h = vc / 72, dd = vc - h * 72;   // the vt store is built for head_dim 72
-        float v[kMT];
+        float v[MT];
 #pragma unroll
-        for (int i = 0; i < kMT; ++i) v[i] = act_fast<ACT>(__fadd_rn(acc_at<P>(acc, i, q), b[q]));
+        for (int i = 0; i < MT; ++i) v[i] = act_fast<ACT>(__fadd_rn(acc_at<MT, P>(acc, i, q), b[q]));
         if (whole) {
             uint2 r;
             pack(v, r);
@@ -623,7 +659,7 @@ __device__ __forceinline__ void vt_chunk(const f32x4_t (&acc)[kMT][kNT], const E
                                                  e.vt_ld + vt_pos(tok)) = r;
         } else {
 #pragma unroll
-            for (int i = 0; i < kMT; ++i) {
+            for (int i = 0; i < MT; ++i) {
                 const int64_t m = mb + i;
                 if (m >= M) break;
                 const int64_t bj = m / e.vt_seq, tj = m - bj * e.vt_seq;
@@ -633,35 +669,37 @@ __device__ __forceinline__ void vt_chunk(const f32x4_t (&acc)[kMT][kNT], const E
     }
 }
 
-template <int ACT, int MODE>
-__device__ __forceinline__ void epilogue(const f32x4_t (&acc)[kMT][kNT], const Epi& e,
+template <int MT, int ACT, int MODE>
+__device__ __forceinline__ void epilogue(const f32x4_t (&acc)[MT][kNT], const Epi& e,
                                          bf16_t* out, int64_t M, int64_t N, int64_t m0,
                                          int64_t n0, int wave, int lane, const bf16_t* bl) {
     const int lr = lane & 15, hi = lane >> 4;
-    const int64_t mb = m0 + wave * 64 + lr * 4;   // this lane's rows: mb .. mb+3
-    if (MODE == EPI_STORE && e.vt && n0 % e.vt_period >= e.vt_col0) {
-        vt_chunk<ACT, 0>(acc, e, M, N, mb, n0, hi, bl);
-        vt_chunk<ACT, 1>(acc, e, M, N, mb, n0, hi, bl);
-        vt_chunk<ACT, 2>(acc, e, M, N, mb, n0, hi, bl);
-        vt_chunk<ACT, 3>(acc, e, M, N, mb, n0, hi, bl);
-        vt_chunk<ACT, 4>(acc, e, M, N, mb, n0, hi, bl);
-        return;
+    const int64_t mb = m0 + wave * 16 * MT + lr * MT;   // this lane's rows: mb .. mb + MT - 1
+    if constexpr (MODE == EPI_STORE && MT == kMaxMT) {   // the transposed V store needs four rows a lane
+        if (e.vt && n0 % e.vt_period >= e.vt_col0) {
+            vt_chunk<MT, ACT, 0>(acc, e, M, N, mb, n0, hi, bl);
+            vt_chunk<MT, ACT, 1>(acc, e, M, N, mb, n0, hi, bl);
+            vt_chunk<MT, ACT, 2>(acc, e, M, N, mb, n0, hi, bl);
+            vt_chunk<MT, ACT, 3>(acc, e, M, N, mb, n0, hi, bl);
+            vt_chunk<MT, ACT, 4>(acc, e, M, N, mb, n0, hi, bl);
+            return;
+        }
     }
     // gate rows are whole batches of tokens: one gate row per tile unless the tile straddles two
-    const int64_t m_last = min(m0 + BM, M) - 1;
+    const int64_t m_last = min(m0 + Geom<MT>::BM, M) - 1;
     const bool gu = MODE == EPI_GATED && m0 / e.gate_rows == m_last / e.gate_rows;
-    ChunkIn<MODE, 8> c0, c1, c2, c3;
-    ChunkIn<MODE, 4> c4;
-    chunk_load<MODE, 0>(c0, e, M, N, mb, n0, hi, gu, bl);
-    chunk_load<MODE, 1>(c1, e, M, N, mb, n0, hi, gu, bl);
-    chunk_store<ACT, MODE, 0>(acc, c0, e, out, M, N, mb, n0, hi, gu);
-    chunk_load<MODE, 2>(c2, e, M, N, mb, n0, hi, gu, bl);
-    chunk_store<ACT, MODE, 1>(acc, c1, e, out, M, N, mb, n0, hi, gu);
-    chunk_load<MODE, 3>(c3, e, M, N, mb, n0, hi, gu, bl);
-    chunk_store<ACT, MODE, 2>(acc, c2, e, out, M, N, mb, n0, hi, gu);
-    chunk_load<MODE, 4>(c4, e, M, N, mb, n0, hi, gu, bl);
-    chunk_store<ACT, MODE, 3>(acc, c3, e, out, M, N, mb, n0, hi, gu);
-    chunk_store<ACT, MODE, 4>(acc, c4, e, out, M, N, mb, n0, hi, gu);
+    ChunkIn<MODE, 8, MT> c0, c1, c2, c3;
+    ChunkIn<MODE, 4, MT> c4;
+    chunk_load<MT, MODE, 0>(c0, e, M, N, mb, n0, hi, gu, bl);
+    chunk_load<MT, MODE, 1>(c1, e, M, N, mb, n0, hi, gu, bl);
+    chunk_store<MT, ACT, MODE, 0>(acc, c0, e, out, M, N, mb, n0, hi, gu);
+    chunk_load<MT, MODE, 2>(c2, e, M, N, mb, n0, hi, gu, bl);
+    chunk_store<MT, ACT, MODE, 1>(acc, c1, e, out, M, N, mb, n0, hi, gu);
+    chunk_load<MT, MODE, 3>(c3, e, M, N, mb, n0, hi, gu, bl);
+    chunk_store<MT, ACT, MODE, 2>(acc, c2, e, out, M, N, mb, n0, hi, gu);
+    chunk_load<MT, MODE, 4>(c4, e, M, N, mb, n0, hi, gu, bl);
+    chunk_store<MT, ACT, MODE, 3>(acc, c3, e, out, M, N, mb, n0, hi, gu);
+    chunk_store<MT, ACT, MODE, 4>(acc, c4, e, out, M, N, mb, n0, hi, gu);
 }
 
 // ---- the last tile's epilogue, staged through LDS ------------------------------------------------
@@ -673,31 +711,35 @@ __device__ __forceinline__ void epilogue(const f32x4_t (&acc)[kMT][kNT], const E
 // bandwidth. Rows are 148 floats; 4-float groups are XOR-swizzled by row so the consumers'
 // writes (16 rows 4 apart per quarter-wave) land on disjoint banks.
 constexpr int kCRow = BN + 4;
-static_assert(BM * kCRow * 4 <= 3 * kStageBytes, "fp32 output tile must fit in the stages");
+static_assert(Geom<1>::BM * kCRow * 4 <= Geom<1>::kBiasOff && Geom<2>::BM * kCRow * 4 <= Geom<2>::kBiasOff &&
+                  Geom<4>::BM * kCRow * 4 <= Geom<4>::kBiasOff,
+              "fp32 output tile must fit in the stages");
 
 __device__ __forceinline__ int ctile_at(int row, int col) {
     return row * kCRow + (col ^ (((row >> 4) & 3) << 2));
 }
 
-__device__ __forceinline__ void park_tile(const f32x4_t (&acc)[kMT][kNT], char* smem, int wave,
+template <int MT>
+__device__ __forceinline__ void park_tile(const f32x4_t (&acc)[MT][kNT], char* smem, int wave,
                                           int lane) {
     float* ctile = reinterpret_cast<float*>(smem);
     const int lr = lane & 15, hi = lane >> 4;
 #pragma unroll
-    for (int i = 0; i < kMT; ++i)
+    for (int i = 0; i < MT; ++i)
 #pragma unroll
         for (int j = 0; j < kNT; ++j) {
-            const int row = wave * 64 + lr * 4 + i, col = b_col(j * 16 + hi * 4);
+            const int row = wave * 16 * MT + lr * MT + i, col = b_col(j * 16 + hi * 4);
             *reinterpret_cast<f32x4_t*>(ctile + ctile_at(row, col)) = acc[i][j];
         }
 }
 
-template <int ACT, int MODE>
+template <int MT, int ACT, int MODE>
 __device__ __forceinline__ void store_staged(const char* smem, const Epi& e, bf16_t* out,
                                              int64_t M, int64_t N, int64_t m0, int64_t n0,
                                              const bf16_t* bias_lds) {
+    constexpr int BM = Geom<MT>::BM;
     const float* ctile = reinterpret_cast<const float*>(smem);
-    if (MODE == EPI_STORE && e.vt && n0 % e.vt_period >= e.vt_col0) {
+    if (MODE == EPI_STORE && MT == kMaxMT && e.vt && n0 % e.vt_period >= e.vt_col0) {
         // V columns: 8 consecutive tokens of one column per 16-byte store, consecutive threads
         // along the token axis of one V^T row. A thread keeps its 8-row group (512 threads over
         // 32 groups), so its batch and token are worked out once.
@@ -815,7 +857,7 @@ __device__ __forceinline__ void store_staged(const char* smem, const Epi& e, bf1
     }
 }
 
-template <int ACT, int MODE>
+template <int MT, int ACT, int MODE>
 __device__ __forceinline__ void consume(char* smem, const Epi& e, bf16_t* out, int64_t M,
                                         int64_t N, int KT, int my_tiles, int tiles_m, int tiles_n,
                                         int group_m, int wave, int lane) {
@@ -824,32 +866,32 @@ __device__ __forceinline__ void consume(char* smem, const Epi& e, bf16_t* out, i
     const int off1 = lr * kRowBytes + (((4 + hi) ^ sw) * 16);
     int stage = 0;
     for (int it = 0; it < my_tiles; ++it) {
-        f32x4_t acc[kMT][kNT];
+        f32x4_t acc[MT][kNT];
 #pragma unroll
-        for (int i = 0; i < kMT; ++i)
+        for (int i = 0; i < MT; ++i)
 #pragma unroll
             for (int j = 0; j < kNT; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
         for (int kt = 0; kt < KT; ++kt) {
             wait_and_join<63>();   // only this wave's LDS reads (its stores need not wait)
-            consume_tile(acc, smem + stage * kStageBytes, wave, off0, off1);
-            stage = stage == 2 ? 0 : stage + 1;
+            consume_tile<MT>(acc, smem + stage * Geom<MT>::kStageBytes, wave, off0, off1);
+            stage = stage == Geom<MT>::kStages - 1 ? 0 : stage + 1;
         }
         if (it + 1 < my_tiles) {
             int64_t m0, n0;
-            tile_origin(blockIdx.x + it * gridDim.x, tiles_m, tiles_n, group_m, m0, n0);
-            epilogue<ACT, MODE>(acc, e, out, M, N, m0, n0, wave, lane, bias_slot(smem, it));
+            tile_origin<MT>(blockIdx.x + it * gridDim.x, tiles_m, tiles_n, group_m, m0, n0);
+            epilogue<MT, ACT, MODE>(acc, e, out, M, N, m0, n0, wave, lane, bias_slot<MT>(smem, it));
         } else {
             wait_and_join<63>();   // the producers' trailing copies have landed
-            park_tile(acc, smem, wave, lane);
+            park_tile<MT>(acc, smem, wave, lane);
         }
     }
 }
 
-template <int ACT, int MODE, bool CONV>
+template <int ACT, int MODE, bool CONV, int MT = kMaxMT>
 __global__ void __launch_bounds__(kWgThreads, 1)
 k_gemm_tn(const bf16_t* __restrict__ A, const bf16_t* __restrict__ B, bf16_t* out, int64_t M,
           int64_t N, int64_t K, Epi e, int tiles_m, int tiles_n, int group_m, ConvGeom cv) {
-    __shared__ __attribute__((aligned(1024))) char smem[kSmemBytes];
+    __shared__ __attribute__((aligned(1024))) char smem[Geom<MT>::kSmemBytes];
     const int T = tiles_m * tiles_n;
     const int my_tiles = (T - static_cast<int>(blockIdx.x) + static_cast<int>(gridDim.x) - 1) /
                          static_cast<int>(gridDim.x);
@@ -865,15 +907,15 @@ k_gemm_tn(const bf16_t* __restrict__ A, const bf16_t* __restrict__ B, bf16_t* ou
         out += static_cast<int64_t>(blockIdx.y) * M * e.ld_out * 2;   // float elements
     }
     if (wave >= kConsumers) {
-        produce<CONV>(smem, Operands{A, B, M, N, K, cv, ldk, e.bias}, KT, my_tiles, tiles_m, tiles_n,
-                      group_m, wave - kConsumers, lane);
+        produce<MT, CONV>(smem, Operands{A, B, M, N, K, cv, ldk, e.bias}, KT, my_tiles, tiles_m,
+                          tiles_n, group_m, wave - kConsumers, lane);
     } else {
-        consume<ACT, MODE>(smem, e, out, M, N, KT, my_tiles, tiles_m, tiles_n, group_m, wave, lane);
+        consume<MT, ACT, MODE>(smem, e, out, M, N, KT, my_tiles, tiles_m, tiles_n, group_m, wave, lane);
     }
     wait_and_join<63>();   // the parked tile is complete and visible
     int64_t m0, n0;
-    tile_origin(blockIdx.x + (my_tiles - 1) * gridDim.x, tiles_m, tiles_n, group_m, m0, n0);
-    store_staged<ACT, MODE>(smem, e, out, M, N, m0, n0, bias_slot(smem, my_tiles - 1));
+    tile_origin<MT>(blockIdx.x + (my_tiles - 1) * gridDim.x, tiles_m, tiles_n, group_m, m0, n0);
+    store_staged<MT, ACT, MODE>(smem, e, out, M, N, m0, n0, bias_slot<MT>(smem, my_tiles - 1));
 }
 
 // ---- small M: one wave per output column, both operands read with 16-byte loads ----
@@ -1055,23 +1097,50 @@ bool aligned(const void* p, int bytes) {
     return (reinterpret_cast<uintptr_t>(p) % bytes) == 0;
 }
 
-template <int ACT, int MODE, bool CONV = false>
+template <int ACT, int MODE, bool CONV = false, int MT = kMaxMT>
 void launch_tn(const bf16_t* a, const bf16_t* b, bf16_t* out, int64_t m, int64_t n, int64_t k,
                const Epi& e, hipStream_t s, const ConvGeom& cv = ConvGeom{}) {
+    constexpr int BM = Geom<MT>::BM;
     const int tiles_m = static_cast<int>((m + BM - 1) / BM);
     const int tiles_n = static_cast<int>((n + BN - 1) / BN);
     const int tiles = tiles_m * tiles_n;
     // One persistent workgroup per CU (the LDS stages allow no second one); with the tile count
-    // a multiple of 8, so is the grid, which the XCD banding relies on.
+    // a multiple of 8, so is the grid, which the XCD banding relies on. An XCD's band is walked
+    // 256 rows of M-tiles at a time whatever the tile height.
     int grid = min(tiles, device_cus() & ~7);
     if (grid < 8) grid = min(tiles, device_cus());
-    k_gemm_tn<ACT, MODE, CONV><<<grid, kWgThreads, 0, s>>>(a, b, out, m, n, k, e, tiles_m, tiles_n, 4, cv);
+    k_gemm_tn<ACT, MODE, CONV, MT><<<grid, kWgThreads, 0, s>>>(a, b, out, m, n, k, e, tiles_m, tiles_n,
+                                                               16 / MT, cv);
+}
+
+// The tile height of a GEMM that runs whole (no split-K): the one with the least estimated time,
+// rounds x (rows a k-tile loads), where rounds = ceil(tiles / CUs) and a k-tile of a BM-row tile
+// loads BM + 144 rows of 128 bytes. The k-loop runs at the rate its operand stream is delivered,
+// not at the MFMA rate (~2,100 cycles per 256-row k-tile against 1,152 of MFMA issue), so a
+// shorter tile's k-tile is proportionally shorter. Ties keep the taller tile. Every height sums
+// each output's k-tiles in the same order with the same MFMAs, so results do not depend on it.
+int gemm_tile_mt(int64_t m, int64_t n) {
+    const int64_t cus = device_cus();
+    const int64_t tiles_n = (n + BN - 1) / BN;
+    int best = kMaxMT;
+    int64_t best_cost = -1;
+    for (int mt = kMaxMT; mt >= 1; mt /= 2) {
+        const int64_t bm = 64 * mt;
+        const int64_t rounds = (((m + bm - 1) / bm) * tiles_n + cus - 1) / cus;
+        const int64_t cost = rounds * (bm + BN);
+        if (best_cost < 0 || cost < best_cost) {
+            best = mt;
+            best_cost = cost;
+        }
+    }
+    return best;
 }
 
 // Split-K partials: `splits` slices of K in one launch (grid.y = slice), each persistent
 // workgroup set over the same output tiles, slice s writing fp32 partial[s][m][n].
 void launch_tn_splitk(const bf16_t* a, const bf16_t* b, float* partial, int64_t m, int64_t n, int64_t k,
                       int splits, hipStream_t s) {
+    constexpr int BM = Geom<kMaxMT>::BM;
     const int tiles_m = static_cast<int>((m + BM - 1) / BM);
     const int tiles_n = static_cast<int>((n + BN - 1) / BN);
     const int tiles = tiles_m * tiles_n;
@@ -1188,14 +1257,24 @@ void launch_splitk_epi(int mode, const float* partial, int splits, int64_t m, in
     }
 }
 
-template <int ACT>
+template <int ACT, int MT>
 void launch_tn_mode(int mode, const bf16_t* a, const bf16_t* b, bf16_t* out, int64_t m, int64_t n,
                     int64_t k, const Epi& e, hipStream_t s) {
     switch (mode) {
-        case EPI_STORE: launch_tn<ACT, EPI_STORE>(a, b, out, m, n, k, e, s); break;
-        case EPI_ROW_ADD: launch_tn<ACT, EPI_ROW_ADD>(a, b, out, m, n, k, e, s); break;
-        case EPI_RESIDUAL: launch_tn<ACT, EPI_RESIDUAL>(a, b, out, m, n, k, e, s); break;
-        default: launch_tn<ACT, EPI_GATED>(a, b, out, m, n, k, e, s); break;
+        case EPI_STORE: launch_tn<ACT, EPI_STORE, false, MT>(a, b, out, m, n, k, e, s); break;
+        case EPI_ROW_ADD: launch_tn<ACT, EPI_ROW_ADD, false, MT>(a, b, out, m, n, k, e, s); break;
+        case EPI_RESIDUAL: launch_tn<ACT, EPI_RESIDUAL, false, MT>(a, b, out, m, n, k, e, s); break;
+        default: launch_tn<ACT, EPI_GATED, false, MT>(a, b, out, m, n, k, e, s); break;
+    }
+}
+
+template <int ACT>
+void launch_tn_mt(int mt, int mode, const bf16_t* a, const bf16_t* b, bf16_t* out, int64_t m, int64_t n,
+                  int64_t k, const Epi& e, hipStream_t s) {
+    switch (mt) {
+        case 1: launch_tn_mode<ACT, 1>(mode, a, b, out, m, n, k, e, s); break;
+        case 2: launch_tn_mode<ACT, 2>(mode, a, b, out, m, n, k, e, s); break;
+        default: launch_tn_mode<ACT, kMaxMT>(mode, a, b, out, m, n, k, e, s); break;
     }
 }
 
@@ -1297,10 +1376,11 @@ void launch_gemm_bf16(const bf16_t* a, const bf16_t* b, const bf16_t* bias, bf16
         return;
     }
     ProfileScope ps(K_GEMM, s, flops, gemm_subclass());
+    const int mt = ep.vt ? kMaxMT : gemm_tile_mt(m, n);   // the transposed V store: 256-row tiles
     switch (ep.act) {
-        case 1: launch_tn_mode<1>(mode, a, b, out, m, n, k, e, s); break;
-        case 2: launch_tn_mode<2>(mode, a, b, out, m, n, k, e, s); break;
-        default: launch_tn_mode<0>(mode, a, b, out, m, n, k, e, s); break;
+        case 1: launch_tn_mt<1>(mt, mode, a, b, out, m, n, k, e, s); break;
+        case 2: launch_tn_mt<2>(mt, mode, a, b, out, m, n, k, e, s); break;
+        default: launch_tn_mt<0>(mt, mode, a, b, out, m, n, k, e, s); break;
     }
     launch_check("gemm (mfma)");
 }
@@ -1331,7 +1411,7 @@ void launch_conv3x3_bf16(const ConvGeom& cv, const bf16_t* wr, const bf16_t* bia
 
 int gemm_splitk_choice(int64_t m, int64_t n, int64_t k) {
     if (m <= kGemvMaxM || n % 8 != 0 || k % BK != 0) return 1;
-    const int64_t tiles = ((m + BM - 1) / BM) * ((n + BN - 1) / BN);
+    const int64_t tiles = ((m + Geom<kMaxMT>::BM - 1) / Geom<kMaxMT>::BM) * ((n + BN - 1) / BN);
     const int cus = device_cus();
     int best = 1;
     for (int sp = 2; sp <= 8; ++sp)
@@ -1349,7 +1429,7 @@ int gemm_splits(int64_t m, int64_t n, int64_t k, const GemmEpilogue& ep) {
     if (ep.splitk > 0) return ep.splitk;
     if (ep.vt || ep.row_add || m <= kGemvMaxM || k % BK != 0 || n % 8 != 0) return 1;
     if (k / BK < kSplitKMinKTiles) return 1;
-    const int64_t tiles = ((m + BM - 1) / BM) * ((n + BN - 1) / BN);
+    const int64_t tiles = ((m + Geom<kMaxMT>::BM - 1) / Geom<kMaxMT>::BM) * ((n + BN - 1) / BN);
     if (tiles * 2 > device_cus()) return 1;
     return gemm_splitk_choice(m, n, k);
 }

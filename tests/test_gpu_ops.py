@@ -69,7 +69,9 @@ GEMM_SHAPES = [(13, 11, 40), (37, 150, 64), (2, 6912, 1152), (5, 1152, 256), (60
                # the MFMA kernel with ragged M and N tiles, and k-tile counts of 1, 2 and 5
                (37, 152, 128), (777, 296, 320), (300, 1152, 64),
                # more tiles than CUs: the persistent loop, whole and ragged tile grids
-               (3072, 3456, 128), (4100, 2312, 64)]
+               (3072, 3456, 128), (4100, 2312, 64),
+               # tile heights: 128 rows (96 tiles of 256 rows would fill 96 CUs), 64 rows
+               (2048, 1728, 256), (1000, 1160, 192)]
 
 
 @pytest.mark.parametrize("shape", GEMM_SHAPES, ids=lambda s: "x".join(map(str, s)))
