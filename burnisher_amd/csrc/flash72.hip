@@ -434,8 +434,13 @@ __device__ __forceinline__ void softmax(WaveState& w, const Flash72Args& a, int 
 // after one barrier each wave runs its blocks through without further synchronisation (the two
 // waves of a SIMD drift apart, so one's softmax overlaps the other's MFMAs).
 // SPLIT (never with RESIDENT): a key split of a.splits, written as an fp32 partial to a.part.
-template <bool MASKED, bool RESIDENT, bool SPLIT>
-__global__ void __launch_bounds__(kThreads, 1) k_flash72(Flash72Args a) {
+// WAVES: waves per workgroup, 64 queries each. The streaming pipeline needs its two groups of four;
+// the resident variant runs with fewer when a full workgroup would leave CUs idle (short query
+// sequences): its waves run independently after the one barrier.
+template <bool MASKED, bool RESIDENT, bool SPLIT, int WAVES = kWaves>
+__global__ void __launch_bounds__(WAVES * 64, 1) k_flash72(Flash72Args a) {
+    static_assert(WAVES == kWaves || (RESIDENT && (WAVES == 4 || WAVES == 2 || WAVES == 1)),
+                  "fewer waves only for the resident variant");
     constexpr int kNumStages = RESIDENT ? kResidentBlocks : kStages;
     __shared__ __attribute__((aligned(1024))) char smem[kNumStages * kStage];
     __shared__ unsigned long long blk_bits[kMaxBlocks];
@@ -455,7 +460,7 @@ __global__ void __launch_bounds__(kThreads, 1) k_flash72(Flash72Args a) {
     if (SPLIT) bid /= splits;
     const int bh = bid / a.qblocks;
     const int b = bh / a.H, h = bh - b * a.H;
-    const int q_base = (bid - bh * a.qblocks) * kQPerWg + wave * kQPerWave;
+    const int q_base = (bid - bh * a.qblocks) * (WAVES * kQPerWave) + wave * kQPerWave;
     const int nblk = (a.Skv + kKV - 1) / kKV;
     const int kb0 = SPLIT ? split * nblk / splits : 0;
     const int kb1 = SPLIT ? (split + 1) * nblk / splits : nblk;
@@ -479,7 +484,7 @@ __global__ void __launch_bounds__(kThreads, 1) k_flash72(Flash72Args a) {
 
     // ---- key validity per block (bit i = key 64 blk + i is in range and unmasked) ----
     if (MASKED) {
-        for (int blk = wave; blk < nblk; blk += kWaves) {
+        for (int blk = wave; blk < nblk; blk += WAVES) {
             const int key = blk * kKV + lane;
             bool ok = key < a.Skv;
             if (ok && a.mask) {
@@ -492,7 +497,7 @@ __global__ void __launch_bounds__(kThreads, 1) k_flash72(Flash72Args a) {
         }
     }
     // V^T rows 72..79 of every stage: the ones row and zero padding (never written by the DMA)
-    for (int i = threadIdx.x; i < kNumStages * 8 * 128 / 16; i += kThreads) {
+    for (int i = threadIdx.x; i < kNumStages * 8 * 128 / 16; i += WAVES * 64) {
         const int st = i / 64, x = i - st * 64;   // 64 16-byte words per stage
         const uint32_t one = x < 8 ? 0x3f803f80u : 0u;
         *reinterpret_cast<uint4*>(smem + st * kStage + kKBytes + 72 * 128 + x * 16) =
@@ -567,7 +572,7 @@ __global__ void __launch_bounds__(kThreads, 1) k_flash72(Flash72Args a) {
         const int last_full = a.Skv / kKV;
         for (int j = 0; j < n; ++j) {
             const int blk = live[j];
-            for (int item = wave; item < 20; item += kWaves)
+            for (int item = wave; item < 20; item += WAVES)
                 dma_item(smem + j * kStage, a, kbh, vbh, item, lane, blk * kKV,
                          MASKED && blk >= last_full);
         }
@@ -769,6 +774,20 @@ float* flash72_part_workspace(int64_t floats) {
     return static_cast<float*>(ptr[dev]);
 }
 
+template <bool MASKED>
+void launch_resident_m(int waves, int grid, const Flash72Args& a, hipStream_t s) {
+    switch (waves) {
+        case 1: k_flash72<MASKED, true, false, 1><<<grid, 64, 0, s>>>(a); break;
+        case 2: k_flash72<MASKED, true, false, 2><<<grid, 128, 0, s>>>(a); break;
+        case 4: k_flash72<MASKED, true, false, 4><<<grid, 256, 0, s>>>(a); break;
+        default: k_flash72<MASKED, true, false, kWaves><<<grid, kThreads, 0, s>>>(a); break;
+    }
+}
+void launch_resident(bool masked, int waves, int grid, const Flash72Args& a, hipStream_t s) {
+    if (masked) launch_resident_m<true>(waves, grid, a, s);
+    else launch_resident_m<false>(waves, grid, a, s);
+}
+
 }  // namespace
 
 int64_t flash72_vt_ld(int64_t kv_len) { return (kv_len + kKV - 1) / kKV * kKV; }
@@ -829,10 +848,22 @@ void launch_flash72(const bf16_t* q, int64_t ld_q, const bf16_t* k, int64_t ld_k
     a.Sq = static_cast<int>(q_len);
     a.Skv = static_cast<int>(kv_len);
     a.mask_f32 = mask_f32 ? 1 : 0;
-    a.qblocks = static_cast<int>((q_len + kQPerWg - 1) / kQPerWg);
     a.c = scale * 1.4426950408889634f;
     const bool masked = key_mask || kv_len % kKV != 0;
     const bool resident = kv_len <= kResidentBlocks * kKV;
+    // Resident launches take fewer waves per workgroup until the grid covers the CUs (one
+    // workgroup per CU: the resident stages fill the LDS), so a short query sequence runs one
+    // wave per SIMD on more CUs instead of two per SIMD on a few.
+    int waves = kWaves;
+    if (resident) {
+        int cus = 0, dev = 0;
+        hip_check(hipGetDevice(&dev), "hipGetDevice");
+        hip_check(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev),
+                  "hipDeviceGetAttribute");
+        auto wgs = [&](int w) { return batch * heads * ((q_len + w * kQPerWave - 1) / (w * kQPerWave)); };
+        while (waves > 1 && wgs(waves) < cus) waves /= 2;
+    }
+    a.qblocks = static_cast<int>((q_len + waves * kQPerWave - 1) / (waves * kQPerWave));
     if (splits <= 0) splits = flash72_splits(batch, heads, q_len, kv_len, out, ld_o);
     const int64_t nblk = (kv_len + kKV - 1) / kKV;
     require(splits >= 1 && splits <= 8 && (splits == 1 || (!resident && nblk >= splits)),
@@ -857,9 +888,8 @@ void launch_flash72(const bf16_t* q, int64_t ld_q, const bf16_t* k, int64_t ld_k
     ProfileScope ps(q_len == kv_len ? K_ATTN_SELF : K_ATTN_CROSS, s, flops);
     if (a.splits > 1 && masked) k_flash72<true, false, true><<<grid, kThreads, 0, s>>>(a);
     else if (a.splits > 1) k_flash72<false, false, true><<<grid, kThreads, 0, s>>>(a);
-    else if (masked && resident) k_flash72<true, true, false><<<grid, kThreads, 0, s>>>(a);
+    else if (resident) launch_resident(masked, waves, grid, a, s);
     else if (masked) k_flash72<true, false, false><<<grid, kThreads, 0, s>>>(a);
-    else if (resident) k_flash72<false, true, false><<<grid, kThreads, 0, s>>>(a);
     else k_flash72<false, false, false><<<grid, kThreads, 0, s>>>(a);
     launch_check("attention (flash, head_dim 72)");
     if (a.splits > 1) {
