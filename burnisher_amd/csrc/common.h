@@ -82,12 +82,14 @@ __device__ __forceinline__ void s_waitcnt() {
     __builtin_amdgcn_s_waitcnt((VM & 15) | (7 << 4) | (LGKM << 8) | ((VM >> 4) << 14));
 }
 
-// Position of key `kv` in a V^T row as the head_dim-72 attention kernel reads it: within each
-// 32-key chunk, keys 4i..4i+3 sit at 8i..8i+3 and keys 16+4i..16+4i+3 at 8i+4..8i+7 (i < 4), so
-// the 16 bytes at 8i are exactly the keys lane group i of a 16x16 score tile pair holds (the
-// output product then needs no exchange of P across lanes). Runs of four keys stay contiguous.
+// Position of key `kv` in a V^T row as the head_dim-72 attention kernel reads it. Within each
+// 32-key chunk, with key bits b4..b0, the key sits at slot b2 b4 b3 b1 b0: the 16 bytes at slot
+// 8r are the eight keys lane row r (lanes 16r..16r+15) holds after its 32x32 score tile is
+// converted to bf16 and one permlane16 swap pairs up the query halves, so P feeds the output
+// product with no further exchange. Runs of four keys stay contiguous.
 __host__ __device__ inline int64_t vt_pos(int64_t kv) {
-    return (kv & ~int64_t{31}) | (((kv & 15) >> 2) << 3) | (((kv >> 4) & 1) << 2) | (kv & 3);
+    return (kv & ~int64_t{31}) | (((kv >> 2) & 1) << 4) | (((kv >> 4) & 1) << 3) |
+           (((kv >> 3) & 1) << 2) | (kv & 3);
 }
 
 // ---- errors ---------------------------------------------------------------------------------

@@ -4,35 +4,39 @@
 //   V supplied TRANSPOSED: vt[((b * heads + h) * 72 + d) * vt_ld + vt_pos(kv)], zero past
 //   kv_len (vt_pos, common.h: keys permuted within 32-key chunks, runs of four kept).
 //
-// Workgroup: 8 waves, 512 queries of one (batch, head); wave w owns queries 64w..64w+63 as four
-// 16-query tiles. Keys stream in blocks of 64 through FOUR LDS stages filled by direct
-// global->LDS loads (global_load_lds_dwordx4).
+// Workgroup: 8 waves, 512 queries of one (batch, head); wave w owns queries 64w..64w+63. Keys
+// stream in blocks of 64 through FOUR LDS stages filled by direct global->LDS loads
+// (global_load_lds_dwordx4).
 //
-// Both products run on v_mfma_f32_16x16x32_bf16 with the score matrix TRANSPOSED:
-//   S^T[kv, q]  = K[kv, :] . Q[q, :]^T      A = K fragment (LDS), B = Q fragment (registers)
-//   O^T[d, q]  += V^T[d, kv] . P^T[kv, q]   A = V^T fragment (LDS), B = P (registers)
-// The S^T accumulator gives each lane four consecutive keys of one query per 16-key tile; with
-// the two tiles of a 32-key chunk, lane group g holds keys 4g..4g+3 and 16+4g..16+4g+3, which
-// is its B operand of the second product as it stands, because V^T keeps exactly those eight
-// keys together (vt_pos): the matching V^T fragment is one 16-byte LDS read. head_dim 72 is
-// padded to 96 for the score product (Q is zero in the padding, so whatever finite K bytes sit
-// there vanish) and to 80 for the output: V^T rows 72..79 sit in LDS with row 72 all ONES, so O^T
-// row 72 is the softmax denominator sum_kv P[kv], accumulated from the same bf16 P as the
-// numerator.
+// Both products run on the matrix cores with the score matrix TRANSPOSED:
+//   S^T[kv, q]  = K[kv, :] . Q[q, :]^T      v_mfma_f32_32x32x16_bf16: A = K (LDS), B = Q (registers)
+//   O^T[d, q]  += V^T[d, kv] . P^T[kv, q]   v_mfma_f32_16x16x32_bf16: A = V^T (LDS), B = P (registers)
+// The score product runs in 32x32 tiles (two key tiles x two query tiles per block and wave) over
+// K = 80 dims in five steps of 16, so head_dim 72 pads to 80: 20 MFMAs, 640 matrix-core cycles
+// per block and wave, where 16x16x32 tiles would pad it to 96 (48 MFMAs, 768 cycles). Its accumulator gives lane l sixteen keys of
+// query l % 32: 8j + 4h + (0..3), j < 4, h = l / 32. Converted to bf16 pairs and swapped once
+// between the lane rows 16r..16r+15 (v_permlane16_swap, four per tile), those are two B operands
+// of the output product, one per 16-query half, each lane row holding eight keys that V^T keeps
+// together (vt_pos, common.h): the matching V^T fragment is one 16-byte LDS read. The output
+// product pads head_dim to 80: V^T rows 72..79 sit in LDS with row 72 all ONES, so O^T row 72 is
+// the softmax denominator sum_kv P[kv], accumulated from the same bf16 P as the numerator. The
+// score padding carries the running maximum: Q's dim 72 holds -m (dims 73..79 zero) and the
+// upper lanes of the last K step read that ones row instead of K, so the matrix cores deliver
+// s c - m; whatever finite K bytes would sit past dim 71 never enter.
 //
 // Schedule: a wave alternates a matrix phase (the output product of block j-1, then the scores of
-// block j: 88 MFMAs) and a vector phase (softmax of block j: maximum, exp2, conversion to bf16).
+// block j: 40 + 20 MFMAs) and a vector phase (softmax of block j: maximum, exp2, conversion to bf16).
 // Waves 0-3 and 4-7 run one phase apart, separated by a workgroup barrier per phase, so on every
 // SIMD one wave's exponentials overlap the other wave's MFMAs. Waves 0-3 also issue the DMA, at
 // the end of their matrix phases (the shorter ones).
 //
 // Softmax: scores stay fp32; exp2(s * scale * log2e - m) with the running maximum m kept in those
 // units. Q is multiplied by c = scale * log2e once, as it is loaded (one extra bf16 rounding of
-// q c), and the score MFMAs of a block start from the accumulator value -m, so the matrix cores
-// deliver s c - m and the vector phase spends no operation per score on it. The first block
-// sets m (its scores are formed against 0); a later block moves it (and rescales O by
-// exp2(m_old - m_new)) only when one of its scores exceeds it by more than 8: any fixed m gives
-// the same normalised result, and the threshold bounds every P by 2^8, far from fp32 range. The
+// q c), and the score product's dim 72 adds -m, so the matrix cores deliver s c - m and the
+// vector phase spends no operation per score on it. m is kept a bf16 value, so -m in Q is exact.
+// The first block sets m (its scores are formed against 0); a later block moves it (and rescales
+// O by exp2(m_old - m_new)) only when one of its scores exceeds it by more than 8: any fixed m
+// gives the same normalised result, and the threshold bounds every P by about 2^8. The
 // common path then needs no maximum per query at all -- one per lane and a wave vote decide --
 // which matters because this kernel's vector phase is as long as its matrix phase.
 //
@@ -58,12 +62,15 @@ constexpr int kThreads = kWaves * 64;
 constexpr int kQPerWave = 64;
 constexpr int kQPerWg = kWaves * kQPerWave;   // 512
 constexpr int kKV = 64;                       // keys per block
-constexpr int kQT = 4;                        // 16-query tiles per wave
-constexpr int kKT = 4;                        // 16-key tiles per block
+constexpr int kQT = 4;                        // 16-query tiles per wave (output product)
+constexpr int kST = 2;                        // 32-query tiles per wave (score product)
+constexpr int kSK = 2;                        // 32-key tiles per block (score product)
+constexpr int kSSteps = 5;                    // K = 16 steps of the score product: dims 0..79
 constexpr int kKRow = D * 2;                  // 144 bytes per K row in LDS
 constexpr int kKBytes = kKV * kKRow;          // 9216 = 9 DMA blocks
 constexpr int kVRows = 80;                    // 72 dims + the ones row + zero rows
 constexpr int kVBytes = kVRows * 128;         // 128 bytes = 64 keys per V^T row
+constexpr int kOnesOff = kKBytes + D * 128;   // V^T row 72 of a stage: 64 bf16 ones
 constexpr int kSpareBytes = 2 * 1024;
 constexpr int kStage = kKBytes + kVBytes + kSpareBytes;   // 21504
 constexpr int kStages = 4;
@@ -223,38 +230,43 @@ __device__ __forceinline__ bf16x8_t ld_frag(const char* p) {
 
 // Per-wave state of the pipeline.
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16_t;
 
 struct WaveState {
-    bf16x8_t qf[kQT][3];       // Q fragments: tile u, K=32 step ks covers dims 32ks + 8g .. +7
+    bf16x8_t qf[kST][kSSteps]; // Q fragments: query 32 qt + l%32, dims 16 s + 8 h .. +7 (h = l/32);
+                               // lanes h = 1 of step 4 hold (-m, 0, ..., 0) for dims 72..79
     f32x4_t o[5][kQT];         // O^T accumulators: rows 16e + 4g .. +3 (row 72 = denominator)
-    f32x4_t s[kKT][kQT];       // S^T of the current block: key 16t + 4g + r, query 16u + lr
+    f32x16_t s[kSK][kST];      // S^T of the current block: element r is key 32 kt + 8 (r/4) + 4 h + r%4,
+                               // query 32 qt + l%32
     bf16x8_t pf[kQT][2];       // P of the previous block, as the second product's B operand
-    float mc[kQT];             // running maximum (scaled, log2 units), per query of the lane
+    float mc[kST];             // running maximum (scaled, log2 units, a bf16 value) of query 32 qt + l%32
 };
 
-// The matrix phase: O^T += V^T P^T for the block whose P is in w.pf (OUT: 40 MFMAs, V^T from
-// `vstage`), then the scores of the next block (SCORES: 48 MFMAs, K from `kstage`) into w.s.
+// The matrix phase: O^T += V^T P^T for the block whose P is in w.pf (OUT: 40 MFMAs 16x16x32,
+// V^T from `vstage`), then the scores of the next block (SCORES: 20 MFMAs 32x32x16, K from
+// `kstage`) into w.s.
 //   output: for each V^T fragment (row block e, 32-key chunk cc), four MFMAs (query tiles u);
 //           `vbase[cc]`: this lane's byte offset of its V^T chunk at row block 0 (e adds 16 rows).
-//   scores: three K=32 steps over dims 0..95 (Q zero past 71, so whatever finite K bytes sit
-//           there vanish), step-outer so that four independent MFMAs separate the dependent
-//           ones; all three of an accumulator have one shape, which the matrix core forwards
-//           back to back. `kbase`: this lane's byte offset of its K chunk (row lane%16, chunk
-//           lane/16) at key tile 0 (key tile t adds 16 rows, step ks 64 bytes).
-// Fragments are read ahead of their MFMAs: V^T three fragments ahead, K one key tile ahead, the
-// first two K tiles during the last output MFMAs. The sched_group_barrier sequence pins that
-// order (left alone, the scheduler sinks each read next to its first use and the wave waits out
-// the LDS latency in front of every group).
+//   scores: five K=16 steps over dims 0..79, step-outer so that four independent MFMAs separate
+//           the dependent ones. `kb[0]`: this lane's byte offset of its K chunk (row l%32, dims
+//           8h..8h+7) at key tile 0 and step 0 (key tile kt adds 32 rows, step s 32 bytes);
+//           `kb[1 + kt]`: the offset for step 4 -- dims 64..71 of its row for h = 0, the ones row
+//           (kOnesOff) for h = 1, which pairs with -m in Q's dim 72.
+// Fragments are read ahead of their MFMAs: V^T three fragments ahead, K two ahead, the first two
+// K fragments during the last output MFMAs. The sched_group_barrier sequence pins that order (left
+// alone, the scheduler sinks each read next to its first use and the wave waits out the LDS
+// latency in front of every group).
 template <bool OUT, bool SCORES>
 __device__ __forceinline__ void matrix_phase(WaveState& w, const char* vstage, const int (&vbase)[2],
-                                             const char* kstage, int kbase) {
-    constexpr int kVF = 10;        // V^T fragments (e, cc)
-    constexpr int kKF = 3 * kKT;   // K fragments in MFMA order: p = 4 ks + t
+                                             const char* kstage, const int (&kb)[3]) {
+    constexpr int kVF = 10;                // V^T fragments (e, cc)
+    constexpr int kKF = kSSteps * kSK;     // K fragments in MFMA order: p = 2 s + kt
     bf16x8_t vf[kVF];
     bf16x8_t kf[kKF];
     auto read_v = [&](int i) { vf[i] = ld_frag(vstage + vbase[i & 1] + (i >> 1) * 16 * 128); };
     auto read_k = [&](int p) {
-        kf[p] = ld_frag(kstage + kbase + (p % kKT) * 16 * kKRow + (p / kKT) * 64);
+        const int kt = p % kSK, st = p / kSK;
+        kf[p] = ld_frag(kstage + (st < kSSteps - 1 ? kb[0] + kt * 32 * kKRow + st * 32 : kb[1 + kt]));
     };
     if (OUT) {
         read_v(0);
@@ -273,19 +285,14 @@ __device__ __forceinline__ void matrix_phase(WaveState& w, const char* vstage, c
         read_k(1);
     }
     if (SCORES) {
-        // The first K step accumulates onto -m, so the scores come out as s c - m (Q holds c).
-        // Step-outer, so -m is live for the first step only; each K fragment is read two
-        // fragments (eight MFMAs) ahead of its use.
-        f32x4_t negm[kQT];
-#pragma unroll
-        for (int u = 0; u < kQT; ++u) negm[u] = f32x4_t{-w.mc[u], -w.mc[u], -w.mc[u], -w.mc[u]};
+        const f32x16_t zero = {};
 #pragma unroll
         for (int p = 0; p < kKF; ++p) {
-            const int t = p % kKT, ks = p / kKT;
+            const int kt = p % kSK, st = p / kSK;
 #pragma unroll
-            for (int u = 0; u < kQT; ++u)
-                w.s[t][u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                    kf[p], w.qf[u][ks], ks == 0 ? negm[u] : w.s[t][u], 0, 0, 0);
+            for (int qt = 0; qt < kST; ++qt)
+                w.s[kt][qt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                    kf[p], w.qf[qt][st], st == 0 ? zero : w.s[kt][qt], 0, 0, 0);
             if (p + 2 < kKF) read_k(p + 2);
         }
     }
@@ -303,7 +310,7 @@ __device__ __forceinline__ void matrix_phase(WaveState& w, const char* vstage, c
     if (SCORES) {
 #pragma unroll
         for (int p = 0; p < kKF; ++p) {
-            __builtin_amdgcn_sched_group_barrier(0x008, kQT, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, kST, 0);
             if (p + 2 < kKF) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
         }
     }
@@ -316,117 +323,132 @@ __device__ __forceinline__ float lane_max2(float m, bool swap32) {
     return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
+// Maximum of the 32 scores this lane holds for query tile qt (its query's keys 8j + 4h + i of
+// both key tiles).
+__device__ __forceinline__ float tile_max(const WaveState& w, int qt) {
+    float m = max3(w.s[0][qt][0], w.s[0][qt][1], w.s[0][qt][2]);
+#pragma unroll
+    for (int i = 3; i < 15; i += 2) m = max3(m, w.s[0][qt][i], w.s[0][qt][i + 1]);
+    m = max3(m, w.s[0][qt][15], w.s[1][qt][0]);
+#pragma unroll
+    for (int i = 1; i < 15; i += 2) m = max3(m, w.s[1][qt][i], w.s[1][qt][i + 1]);
+    return fmaxf(m, w.s[1][qt][15]);
+}
+
+// Q's dim 72 := -m (lanes h = 1 of the last K step; their dims 73..79 stay zero).
+__device__ __forceinline__ void set_neg_max(WaveState& w, int h) {
+#pragma unroll
+    for (int qt = 0; qt < kST; ++qt) {
+        bf16x8_t f = {};
+        f[0] = static_cast<__bf16>(-w.mc[qt]);   // exact: mc is a bf16 value
+        if (h) w.qf[qt][kSSteps - 1] = f;
+    }
+}
+
+__device__ __forceinline__ float round_bf16(float x) {
+    return static_cast<float>(static_cast<__bf16>(x));
+}
+
 // Softmax of the block whose scores are in w.s: masking, the block maximum (the 64 keys of a
-// query sit in lanes lr, lr+16, lr+32, lr+48), the lazy rescale, P = exp2(s c - m) in bf16,
-// regrouped into w.pf.
+// query sit in lanes l and l ^ 32), the lazy rescale, P = exp2(s c - m) in bf16, regrouped into
+// w.pf.
 template <bool MASKED, bool FIRST>
 __device__ __forceinline__ void softmax(WaveState& w, const Flash72Args& a, int blk,
-                                        unsigned long long bits_all, bool all_masked, int g) {
+                                        unsigned long long bits_all, bool all_masked, int h) {
     constexpr bool first = FIRST;   // a compile-time branch: a run-time one keeps both forms of S live
     if (MASKED) {
-        const unsigned long long bits = bits_all >> (4 * g);
+        const unsigned long long bits = bits_all >> (4 * h);
         const unsigned long long inrange =
-            (blk * kKV + kKV <= a.Skv) ? ~0ull : (((1ull << (a.Skv - blk * kKV)) - 1ull) >> (4 * g));
+            (blk * kKV + kKV <= a.Skv) ? ~0ull : (((1ull << (a.Skv - blk * kKV)) - 1ull) >> (4 * h));
 #pragma unroll
-        for (int t = 0; t < kKT; ++t)
+        for (int kt = 0; kt < kSK; ++kt)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int bit = 16 * t + r;
+            for (int r = 0; r < 16; ++r) {
+                const int bit = 32 * kt + 8 * (r >> 2) + (r & 3);
                 const bool ok = all_masked ? ((inrange >> bit) & 1ull) : ((bits >> bit) & 1ull);
 #pragma unroll
-                for (int u = 0; u < kQT; ++u) {
-                    const float v = all_masked ? 0.0f : w.s[t][u][r];
-                    w.s[t][u][r] = ok ? v : -INFINITY;
+                for (int qt = 0; qt < kST; ++qt) {
+                    const float v = all_masked ? 0.0f : w.s[kt][qt][r];
+                    w.s[kt][qt][r] = ok ? v : -INFINITY;
                 }
             }
     }
     if (first) {
-        // the first block sets the maximum: per query, over its 64 keys (lanes lr + 16 g)
+        // the first block sets the maximum: per query, over its 64 keys (lanes l, l ^ 32), kept
+        // as a bf16 value
 #pragma unroll
-        for (int u = 0; u < kQT; ++u) {
-            float m = max3(w.s[0][u][0], w.s[0][u][1], w.s[0][u][2]);
-            m = max3(m, w.s[0][u][3], w.s[1][u][0]);
-            m = max3(m, w.s[1][u][1], w.s[1][u][2]);
-            m = max3(m, w.s[1][u][3], w.s[2][u][0]);
-            m = max3(m, w.s[2][u][1], w.s[2][u][2]);
-            m = max3(m, w.s[2][u][3], w.s[3][u][0]);
-            m = max3(m, w.s[3][u][1], w.s[3][u][2]);
-            m = fmaxf(m, w.s[3][u][3]);
-            m = lane_max2(m, true);
-            m = lane_max2(m, false);
-            w.mc[u] = m;
-        }
+        for (int qt = 0; qt < kST; ++qt) w.mc[qt] = round_bf16(lane_max2(tile_max(w, qt), true));
         // x = s c - m in place (the first block's scores were formed against m = 0); later
         // blocks' scores arrive as s c - m from the matrix cores
 #pragma unroll
-        for (int t = 0; t < kKT; ++t)
+        for (int kt = 0; kt < kSK; ++kt)
 #pragma unroll
-            for (int u = 0; u < kQT; ++u)
+            for (int qt = 0; qt < kST; ++qt)
 #pragma unroll
-                for (int r = 0; r < 4; ++r) w.s[t][u][r] -= w.mc[u];
+                for (int r = 0; r < 16; ++r) w.s[kt][qt][r] -= w.mc[qt];
+        set_neg_max(w, h);
     }
     if (!first) {
         // Later blocks move the maximum only when one of their scores exceeds it by more than
         // the threshold: one maximum over this lane's 64 values and a wave vote decide; the exact
         // per-query maxima (across lanes) are formed only then.
-        float mx[kKT];
-#pragma unroll
-        for (int t = 0; t < kKT; ++t) {
-            float m = max3(w.s[t][0][0], w.s[t][0][1], w.s[t][0][2]);
-            m = max3(m, w.s[t][0][3], w.s[t][1][0]);
-            m = max3(m, w.s[t][1][1], w.s[t][1][2]);
-            m = max3(m, w.s[t][1][3], w.s[t][2][0]);
-            m = max3(m, w.s[t][2][1], w.s[t][2][2]);
-            m = max3(m, w.s[t][2][3], w.s[t][3][0]);
-            m = max3(m, w.s[t][3][1], w.s[t][3][2]);
-            mx[t] = fmaxf(m, w.s[t][3][3]);
-        }
-        const float m_all = fmaxf(max3(mx[0], mx[1], mx[2]), mx[3]);
+        const float m_all = fmaxf(tile_max(w, 0), tile_max(w, 1));
         if (__any(m_all > kRescaleThreshold)) {
+            const int lr = __lane_id() & 15;
 #pragma unroll
-            for (int u = 0; u < kQT; ++u) {
-                float m = max3(w.s[0][u][0], w.s[0][u][1], w.s[0][u][2]);
-                m = max3(m, w.s[0][u][3], w.s[1][u][0]);
-                m = max3(m, w.s[1][u][1], w.s[1][u][2]);
-                m = max3(m, w.s[1][u][3], w.s[2][u][0]);
-                m = max3(m, w.s[2][u][1], w.s[2][u][2]);
-                m = max3(m, w.s[2][u][3], w.s[3][u][0]);
-                m = max3(m, w.s[3][u][1], w.s[3][u][2]);
-                m = fmaxf(m, w.s[3][u][3]);
-                m = lane_max2(m, true);
-                m = lane_max2(m, false);
-                const float dm = fmaxf(m, 0.0f);   // the query's new maximum is mc + dm
+            for (int qt = 0; qt < kST; ++qt) {
+                const float m = lane_max2(tile_max(w, qt), true);
+                // the query's new maximum, a bf16 value not below the old one
+                const float mnew = round_bf16(w.mc[qt] + fmaxf(m, 0.0f));
+                const float dm = mnew - w.mc[qt];
                 const float alpha = __builtin_amdgcn_exp2f(-dm);
-                w.mc[u] += dm;
+                w.mc[qt] = mnew;
 #pragma unroll
-                for (int e = 0; e < 5; ++e)
+                for (int kt = 0; kt < kSK; ++kt)
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) w.o[e][u][r] *= alpha;
+                    for (int r = 0; r < 16; ++r) w.s[kt][qt][r] -= dm;
+                // O^T tile u = 2 qt + t holds query 32 qt + 16 t + l%16 in every lane row
 #pragma unroll
-                for (int t = 0; t < kKT; ++t)
+                for (int t = 0; t < 2; ++t) {
+                    const float au = __shfl(alpha, 16 * t + lr, 64);
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) w.s[t][u][r] -= dm;
+                    for (int e = 0; e < 5; ++e)
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) w.o[e][2 * qt + t][r] *= au;
+                }
             }
+            set_neg_max(w, h);
         }
     }
+    // P: element r = 4j + i of tile (kt, qt) is key 32 kt + 8j + 4h + i. Pairs pk[2j + v] hold
+    // keys (8j + 4h + 2v, +1). X = pk[0..3] (j = 0, 1) and Y = pk[4..7] (j = 2, 3); swapping X's
+    // odd lane rows with Y's even ones leaves in X queries 32 qt + 0..15 and in Y queries
+    // 32 qt + 16..31, lane row r holding keys 16 (r & 1) + 4 (r >> 1) + {0..3, 8..11}: the eight
+    // keys at V^T slots 8r..8r+7 of the chunk (vt_pos).
 #pragma unroll
-    for (int u = 0; u < kQT; ++u)
+    for (int qt = 0; qt < kST; ++qt)
 #pragma unroll
-        for (int cc = 0; cc < 2; ++cc) {
-            uint32_t x[2], y[2];   // key tiles 2cc and 2cc+1, bf16 pairs of keys (4g, 4g+1), (4g+2, 4g+3)
+        for (int kt = 0; kt < kSK; ++kt) {
+            uint32_t pk[8];
 #pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                bf16x2_t px, py;   // v_cvt_pk_bf16_f32: round to nearest even (P is finite)
-                px[0] = static_cast<__bf16>(__builtin_amdgcn_exp2f(w.s[2 * cc][u][2 * h]));
-                px[1] = static_cast<__bf16>(__builtin_amdgcn_exp2f(w.s[2 * cc][u][2 * h + 1]));
-                py[0] = static_cast<__bf16>(__builtin_amdgcn_exp2f(w.s[2 * cc + 1][u][2 * h]));
-                py[1] = static_cast<__bf16>(__builtin_amdgcn_exp2f(w.s[2 * cc + 1][u][2 * h + 1]));
-                x[h] = __builtin_bit_cast(uint32_t, px);
-                y[h] = __builtin_bit_cast(uint32_t, py);
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int v = 0; v < 2; ++v) {
+                    bf16x2_t p;   // v_cvt_pk_bf16_f32: round to nearest even (P is finite)
+                    p[0] = static_cast<__bf16>(__builtin_amdgcn_exp2f(w.s[kt][qt][4 * j + 2 * v]));
+                    p[1] = static_cast<__bf16>(__builtin_amdgcn_exp2f(w.s[kt][qt][4 * j + 2 * v + 1]));
+                    pk[2 * j + v] = __builtin_bit_cast(uint32_t, p);
+                }
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const auto r = __builtin_amdgcn_permlane16_swap(pk[v], pk[4 + v], false, false);
+                pk[v] = r[0];
+                pk[4 + v] = r[1];
             }
-            // keys 32cc + 4g .. +3 and 32cc + 16 + 4g .. +3: V^T's slots 8g .. 8g+7 of the chunk
-            const uint4 packed = make_uint4(x[0], x[1], y[0], y[1]);
-            w.pf[u][cc] = *reinterpret_cast<const bf16x8_t*>(&packed);
+            const uint4 x = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+            const uint4 y = make_uint4(pk[4], pk[5], pk[6], pk[7]);
+            w.pf[2 * qt][kt] = *reinterpret_cast<const bf16x8_t*>(&x);
+            w.pf[2 * qt + 1][kt] = *reinterpret_cast<const bf16x8_t*>(&y);
         }
 }
 
@@ -467,18 +489,17 @@ __global__ void __launch_bounds__(WAVES * 64, 1) k_flash72(Flash72Args a) {
 
     WaveState w;
     // Q fragments first, so their latency overlaps the set-up below
+    const int lq = lane & 31, hq = lane >> 5;
 #pragma unroll
-    for (int u = 0; u < kQT; ++u) {
-        const int q = q_base + u * 16 + lr;
+    for (int qt = 0; qt < kST; ++qt) {
+        const int q = q_base + qt * 32 + lq;
         const bf16_t* qrow = a.q + (static_cast<int64_t>(b) * a.Sq + q) * a.ld_q + h * D;
 #pragma unroll
-        for (int ks = 0; ks < 3; ++ks) {
-            const int d0 = ks * 32 + g * 8;
-            bf16x8_t f;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) f[e] = static_cast<__bf16>(0.0f);
+        for (int st = 0; st < kSSteps; ++st) {
+            const int d0 = st * 16 + hq * 8;
+            bf16x8_t f = {};
             if (q < a.Sq && d0 < D) f = ld_frag(reinterpret_cast<const char*>(qrow + d0));
-            w.qf[u][ks] = f;
+            w.qf[qt][st] = f;
         }
     }
 
@@ -526,7 +547,10 @@ __global__ void __launch_bounds__(WAVES * 64, 1) k_flash72(Flash72Args a) {
     const bool all_masked = MASKED && all_masked_s != 0;
 
     // fragment byte offsets within a stage
-    const int kbase = lr * kKRow + g * 16;   // K step 2, g >= 1: the next row's finite bytes (Q is 0)
+    int kb[3];
+    kb[0] = lq * kKRow + hq * 16;
+    kb[1] = hq ? kOnesOff : lq * kKRow + 128;
+    kb[2] = hq ? kOnesOff : (32 + lq) * kKRow + 128;
     int vbase[2];
     {
         const int sw = (lr >> 1) & 7;
@@ -538,7 +562,7 @@ __global__ void __launch_bounds__(WAVES * 64, 1) k_flash72(Flash72Args a) {
 #pragma unroll
         for (int u = 0; u < kQT; ++u) w.o[e][u] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int u = 0; u < kQT; ++u) w.mc[u] = 0.0f;   // the first block's scores are formed against 0
+    for (int qt = 0; qt < kST; ++qt) w.mc[qt] = 0.0f;   // the first block's scores are formed against 0
 
     // The Q loads are drained here, where the compiler sees it: otherwise it waits for them
     // (vmcnt(0), which also drains the DMA in flight) at their first use in every phase.
@@ -546,12 +570,12 @@ __global__ void __launch_bounds__(WAVES * 64, 1) k_flash72(Flash72Args a) {
     // Q carries the score scale in log2 units, c = scale log2(e), rounded to bf16 once here, so
     // the matrix cores deliver s c - m and the softmax spends no multiply-add per score.
 #pragma unroll
-    for (int u = 0; u < kQT; ++u)
+    for (int qt = 0; qt < kST; ++qt)
 #pragma unroll
-        for (int ks = 0; ks < 3; ++ks)
+        for (int st = 0; st < kSSteps; ++st)
 #pragma unroll
             for (int e = 0; e < 8; ++e)
-                w.qf[u][ks][e] = static_cast<__bf16>(static_cast<float>(w.qf[u][ks][e]) * a.c);
+                w.qf[qt][st][e] = static_cast<__bf16>(static_cast<float>(w.qf[qt][st][e]) * a.c);
 
     // ---- the phases ----
     // Phase p is bracketed by workgroup barriers. Block j (position j of the live list) sits in
@@ -578,13 +602,13 @@ __global__ void __launch_bounds__(WAVES * 64, 1) k_flash72(Flash72Args a) {
         }
         wait_and_join<0>();
         auto res_stage = [&](int j) -> char* { return smem + j * kStage; };
-        matrix_phase<false, true>(w, nullptr, vbase, res_stage(0), kbase);
-        softmax<MASKED, true>(w, a, live[0], bits_of(0), all_masked, g);
+        matrix_phase<false, true>(w, nullptr, vbase, res_stage(0), kb);
+        softmax<MASKED, true>(w, a, live[0], bits_of(0), all_masked, hq);
         for (int j = 1; j < n; ++j) {
-            matrix_phase<true, true>(w, res_stage(j - 1), vbase, res_stage(j), kbase);
-            softmax<MASKED, false>(w, a, live[j], bits_of(j), all_masked, g);
+            matrix_phase<true, true>(w, res_stage(j - 1), vbase, res_stage(j), kb);
+            softmax<MASKED, false>(w, a, live[j], bits_of(j), all_masked, hq);
         }
-        matrix_phase<true, false>(w, res_stage(n - 1), vbase, nullptr, kbase);
+        matrix_phase<true, false>(w, res_stage(n - 1), vbase, nullptr, kb);
     } else {
     auto stage_of = [&](int j) -> char* { return smem + (j & (kStages - 1)) * kStage; };
     if (wave < kDmaWaves) {
@@ -600,51 +624,54 @@ __global__ void __launch_bounds__(WAVES * 64, 1) k_flash72(Flash72Args a) {
         issue(0);
         issue(1);
         wait_and_join<kDmaPerWave>();                            // phase 0: block 0 has landed
-        matrix_phase<false, true>(w, nullptr, vbase, stage_of(0), kbase);
+        matrix_phase<false, true>(w, nullptr, vbase, stage_of(0), kb);
         issue(2);
         if (n > 1) {   // block 0's softmax peeled off, so FIRST is known at compile time
             wait_and_join<63>();                                 // phase 1
-            softmax<MASKED, true>(w, a, live[0], bits_of(0), all_masked, g);
+            softmax<MASKED, true>(w, a, live[0], bits_of(0), all_masked, hq);
             wait_and_join<kDmaPerWave>();                        // phase 2: block 1 has landed
-            matrix_phase<true, true>(w, stage_of(0), vbase, stage_of(1), kbase);
+            matrix_phase<true, true>(w, stage_of(0), vbase, stage_of(1), kb);
             issue(3);
             for (int j = 2; j < n; ++j) {
                 wait_and_join<63>();                             // phase 2j-1
-                softmax<MASKED, false>(w, a, live[j - 1], bits_of(j - 1), all_masked, g);
+                softmax<MASKED, false>(w, a, live[j - 1], bits_of(j - 1), all_masked, hq);
                 wait_and_join<kDmaPerWave>();                    // phase 2j: block j has landed
-                matrix_phase<true, true>(w, stage_of(j - 1), vbase, stage_of(j), kbase);
+                matrix_phase<true, true>(w, stage_of(j - 1), vbase, stage_of(j), kb);
                 issue(j + 2);
             }
             wait_and_join<63>();                                 // phase 2n-1
-            softmax<MASKED, false>(w, a, live[n - 1], bits_of(n - 1), all_masked, g);
+            softmax<MASKED, false>(w, a, live[n - 1], bits_of(n - 1), all_masked, hq);
         } else {
             wait_and_join<63>();                                 // phase 1
-            softmax<MASKED, true>(w, a, live[0], bits_of(0), all_masked, g);
+            softmax<MASKED, true>(w, a, live[0], bits_of(0), all_masked, hq);
         }
         wait_and_join<63>();                                     // phase 2n
-        matrix_phase<true, false>(w, stage_of(n - 1), vbase, nullptr, kbase);
+        matrix_phase<true, false>(w, stage_of(n - 1), vbase, nullptr, kb);
         wait_and_join<63>();                                     // phase 2n+1
         s_waitcnt<0, 15>();   // the trailing copies
     } else {
         wait_and_join<63>();                                     // phase 0
         wait_and_join<63>();                                     // phase 1
-        matrix_phase<false, true>(w, nullptr, vbase, stage_of(0), kbase);
+        matrix_phase<false, true>(w, nullptr, vbase, stage_of(0), kb);
         wait_and_join<63>();                                     // phase 2
-        softmax<MASKED, true>(w, a, live[0], bits_of(0), all_masked, g);
+        softmax<MASKED, true>(w, a, live[0], bits_of(0), all_masked, hq);
         for (int j = 1; j < n; ++j) {
             wait_and_join<63>();                                 // phase 2j+1
-            matrix_phase<true, true>(w, stage_of(j - 1), vbase, stage_of(j), kbase);
+            matrix_phase<true, true>(w, stage_of(j - 1), vbase, stage_of(j), kb);
             wait_and_join<63>();                                 // phase 2j+2
-            softmax<MASKED, false>(w, a, live[j], bits_of(j), all_masked, g);
+            softmax<MASKED, false>(w, a, live[j], bits_of(j), all_masked, hq);
         }
         wait_and_join<63>();                                     // phase 2n+1
-        matrix_phase<true, false>(w, stage_of(n - 1), vbase, nullptr, kbase);
+        matrix_phase<true, false>(w, stage_of(n - 1), vbase, nullptr, kb);
     }
     }
 
     // ---- a key split's partial: O unnormalised, the row sum and the running maximum ----
     if constexpr (SPLIT) {
         const bool empty = empty_s != 0;
+        float mo[kQT];   // the running maximum of query 16 u + l%16 (held by lane 16 (u & 1) + l%16)
+#pragma unroll
+        for (int u = 0; u < kQT; ++u) mo[u] = __shfl(w.mc[u >> 1], 16 * (u & 1) + lr, 64);
 #pragma unroll
         for (int u = 0; u < kQT; ++u) {
             const int q = q_base + u * 16 + lr;
@@ -658,7 +685,7 @@ __global__ void __launch_bounds__(WAVES * 64, 1) k_flash72(Flash72Args a) {
                     *reinterpret_cast<f32x4_t*>(dst + d) = empty ? f32x4_t{0.f, 0.f, 0.f, 0.f} : w.o[e][u];
                 } else if (d == D) {   // row 72 is the sum; an empty split contributes nothing
                     *reinterpret_cast<f32x4_t*>(dst + d) =
-                        empty ? f32x4_t{0.f, -INFINITY, 0.f, 0.f} : f32x4_t{w.o[e][u][0], w.mc[u], 0.f, 0.f};
+                        empty ? f32x4_t{0.f, -INFINITY, 0.f, 0.f} : f32x4_t{w.o[e][u][0], mo[u], 0.f, 0.f};
                 }
             }
         }

@@ -266,8 +266,9 @@ __global__ void __launch_bounds__(256) k_upsample_nchw(const bf16_t* __restrict_
 // ---- the mid-block attention: one head, head_dim 512 ------------------------------------------
 //
 // softmax(Q K^T / sqrt(512)) V over S tokens, Q, K, O [S, 512] and V given transposed,
-// vt[d][vt_pos(key)] (keys permuted within 32-key chunks as the head_dim-72 kernel has them,
-// zero past S up to a multiple of 32). A workgroup of four waves owns 64 queries, a wave one
+// vt[d][slot(key)] (keys permuted within 32-key chunks so that the eight keys a lane group holds
+// after a pair of 16x16 score tiles are one 16-byte fragment, see k_vt512; zero past S up to a
+// multiple of 32). A workgroup of four waves owns 64 queries, a wave one
 // 16-query tile; keys stream in blocks of 32 through two LDS stages of 64 KiB (the block's K rows
 // and V^T rows), filled by direct global->LDS loads issued by all four waves after the block
 // barrier. Both products run on v_mfma_f32_16x16x32_bf16 with transposed tiles, as in the
@@ -425,7 +426,7 @@ __global__ void __launch_bounds__(256, 1) k_flash512(A5Args a) {
     }
 }
 
-// V [S, 512] -> vt[d][vt_pos(key)], zero for S <= key < vt_ld. A 32-key x 32-dim tile per block.
+// V [S, 512] -> vt[d][slot(key)], zero for S <= key < vt_ld. A 32-key x 32-dim tile per block.
 __global__ void __launch_bounds__(256) k_vt512(const bf16_t* __restrict__ v, bf16_t* __restrict__ vt,
                                                int S, int64_t vt_ld) {
     __shared__ bf16_t tile[32][33];
