@@ -217,13 +217,9 @@ __device__ __forceinline__ void dma_item(char* stage, const Flash72Args& a, cons
     dma16(src, stage + dst);
 }
 
-// Three-input maximum (v_max3_f32). This file is compiled with -fno-honor-nans: with IEEE NaN
-// rules the compiler would first quiet every MFMA result with an extra v_max, doubling the cost
-// of the row maximum. Scores here are finite, or -inf for masked keys.
-__device__ __forceinline__ float max3(float a, float b, float c) {
-    return __builtin_fmaxf(a, __builtin_fmaxf(b, c));
-}
-
+// This file is compiled with -fno-honor-nans: with IEEE NaN rules the compiler would first quiet
+// every MFMA result with an extra v_max before each maximum. Scores here are finite, or -inf for
+// masked keys.
 __device__ __forceinline__ bf16x8_t ld_frag(const char* p) {
     return *reinterpret_cast<const bf16x8_t*>(p);
 }
@@ -323,16 +319,33 @@ __device__ __forceinline__ float lane_max2(float m, bool swap32) {
     return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
-// Maximum of the 32 scores this lane holds for query tile qt (its query's keys 8j + 4h + i of
-// both key tiles).
-__device__ __forceinline__ float tile_max(const WaveState& w, int qt) {
-    float m = max3(w.s[0][qt][0], w.s[0][qt][1], w.s[0][qt][2]);
+// Maxima of the 32 scores this lane holds for each query tile qt (its query's keys 8j + 4h + i of
+// both key tiles): four chains of v_max3 (one per tile), each link taking two new values,
+// interleaved so that no link waits on the one before it (a dependent VALU operand needs two
+// instructions between producer and consumer here). The empty asm makes each link opaque:
+// otherwise the compiler, with NaNs ignored, rebalances the chains into trees of two-input maxima
+// (~50 instructions per 64 values instead of 34).
+__device__ __forceinline__ float max3_link(float m, float a, float b) {
+    m = __builtin_fmaxf(__builtin_fmaxf(m, a), b);
+    asm("" : "+v"(m));
+    return m;
+}
+__device__ __forceinline__ void tile_max(const WaveState& w, float (&tm)[kST]) {
+    float c[kSK][kST];
 #pragma unroll
-    for (int i = 3; i < 15; i += 2) m = max3(m, w.s[0][qt][i], w.s[0][qt][i + 1]);
-    m = max3(m, w.s[0][qt][15], w.s[1][qt][0]);
+    for (int kt = 0; kt < kSK; ++kt)
 #pragma unroll
-    for (int i = 1; i < 15; i += 2) m = max3(m, w.s[1][qt][i], w.s[1][qt][i + 1]);
-    return fmaxf(m, w.s[1][qt][15]);
+        for (int qt = 0; qt < kST; ++qt) c[kt][qt] = max3_link(w.s[kt][qt][0], w.s[kt][qt][1], w.s[kt][qt][2]);
+#pragma unroll
+    for (int i = 3; i < 15; i += 2)
+#pragma unroll
+        for (int kt = 0; kt < kSK; ++kt)
+#pragma unroll
+            for (int qt = 0; qt < kST; ++qt) c[kt][qt] = max3_link(c[kt][qt], w.s[kt][qt][i], w.s[kt][qt][i + 1]);
+#pragma unroll
+    for (int qt = 0; qt < kST; ++qt)
+        tm[qt] = __builtin_fmaxf(__builtin_fmaxf(c[0][qt], w.s[0][qt][15]),
+                                 __builtin_fmaxf(c[1][qt], w.s[1][qt][15]));
 }
 
 // Q's dim 72 := -m (lanes h = 1 of the last K step; their dims 73..79 stay zero).
@@ -340,91 +353,41 @@ __device__ __forceinline__ void set_neg_max(WaveState& w, int h) {
 #pragma unroll
     for (int qt = 0; qt < kST; ++qt) {
         bf16x8_t f = {};
-        f[0] = static_cast<__bf16>(-w.mc[qt]);   // exact: mc is a bf16 value
+        f[0] = static_cast<__bf16>(-w.mc[qt]);   // exact: m is a bf16 value
         if (h) w.qf[qt][kSSteps - 1] = f;
     }
 }
 
-__device__ __forceinline__ float round_bf16(float x) {
-    return static_cast<float>(static_cast<__bf16>(x));
+// The smallest bf16 value not below x (x finite or -inf). Applied to integers it gives integers:
+// below 256 every integer is a bf16 value, from 256 up every bf16 value is an integer.
+__device__ __forceinline__ float ceil_bf16(float x) {
+    const uint32_t t = __float_as_uint(x) & 0xffff0000u;
+    return __uint_as_float(__uint_as_float(t) < x ? t + 0x10000u : t);
 }
 
-// Softmax of the block whose scores are in w.s: masking, the block maximum (the 64 keys of a
-// query sit in lanes l and l ^ 32), the lazy rescale, P = exp2(s c - m) in bf16, regrouped into
-// w.pf.
-template <bool MASKED, bool FIRST>
-__device__ __forceinline__ void softmax(WaveState& w, const Flash72Args& a, int blk,
-                                        unsigned long long bits_all, bool all_masked, int h) {
-    constexpr bool first = FIRST;   // a compile-time branch: a run-time one keeps both forms of S live
-    if (MASKED) {
-        const unsigned long long bits = bits_all >> (4 * h);
-        const unsigned long long inrange =
-            (blk * kKV + kKV <= a.Skv) ? ~0ull : (((1ull << (a.Skv - blk * kKV)) - 1ull) >> (4 * h));
+// P in w.pf times a power of two, per query: pf[u] holds query 16 u + l%16 in every lane row, so
+// tile u takes the factor of the lane that holds that query in the score layout. Exact (the
+// factor is 2^-k) unless a product falls below the normal range.
+__device__ __forceinline__ void scale_p(bf16x8_t& f, float s) {
+    uint32_t x[4];
+    __builtin_memcpy(x, &f, sizeof x);
 #pragma unroll
-        for (int kt = 0; kt < kSK; ++kt)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int bit = 32 * kt + 8 * (r >> 2) + (r & 3);
-                const bool ok = all_masked ? ((inrange >> bit) & 1ull) : ((bits >> bit) & 1ull);
-#pragma unroll
-                for (int qt = 0; qt < kST; ++qt) {
-                    const float v = all_masked ? 0.0f : w.s[kt][qt][r];
-                    w.s[kt][qt][r] = ok ? v : -INFINITY;
-                }
-            }
+    for (int v = 0; v < 4; ++v) {
+        bf16x2_t p;
+        p[0] = static_cast<__bf16>(__uint_as_float(x[v] << 16) * s);
+        p[1] = static_cast<__bf16>(__uint_as_float(x[v] & 0xffff0000u) * s);
+        x[v] = __builtin_bit_cast(uint32_t, p);
     }
-    if (first) {
-        // the first block sets the maximum: per query, over its 64 keys (lanes l, l ^ 32), kept
-        // as a bf16 value
-#pragma unroll
-        for (int qt = 0; qt < kST; ++qt) w.mc[qt] = round_bf16(lane_max2(tile_max(w, qt), true));
-        // x = s c - m in place (the first block's scores were formed against m = 0); later
-        // blocks' scores arrive as s c - m from the matrix cores
-#pragma unroll
-        for (int kt = 0; kt < kSK; ++kt)
-#pragma unroll
-            for (int qt = 0; qt < kST; ++qt)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) w.s[kt][qt][r] -= w.mc[qt];
-        set_neg_max(w, h);
-    }
-    if (!first) {
-        // Later blocks move the maximum only when one of their scores exceeds it by more than
-        // the threshold: one maximum over this lane's 64 values and a wave vote decide; the exact
-        // per-query maxima (across lanes) are formed only then.
-        const float m_all = fmaxf(tile_max(w, 0), tile_max(w, 1));
-        if (__any(m_all > kRescaleThreshold)) {
-            const int lr = __lane_id() & 15;
-#pragma unroll
-            for (int qt = 0; qt < kST; ++qt) {
-                const float m = lane_max2(tile_max(w, qt), true);
-                // the query's new maximum, a bf16 value not below the old one
-                const float mnew = round_bf16(w.mc[qt] + fmaxf(m, 0.0f));
-                const float dm = mnew - w.mc[qt];
-                const float alpha = __builtin_amdgcn_exp2f(-dm);
-                w.mc[qt] = mnew;
-#pragma unroll
-                for (int kt = 0; kt < kSK; ++kt)
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) w.s[kt][qt][r] -= dm;
-                // O^T tile u = 2 qt + t holds query 32 qt + 16 t + l%16 in every lane row
-#pragma unroll
-                for (int t = 0; t < 2; ++t) {
-                    const float au = __shfl(alpha, 16 * t + lr, 64);
-#pragma unroll
-                    for (int e = 0; e < 5; ++e)
-#pragma unroll
-                        for (int r = 0; r < 4; ++r) w.o[e][2 * qt + t][r] *= au;
-                }
-            }
-            set_neg_max(w, h);
-        }
-    }
-    // P: element r = 4j + i of tile (kt, qt) is key 32 kt + 8j + 4h + i. Pairs pk[2j + v] hold
-    // keys (8j + 4h + 2v, +1). X = pk[0..3] (j = 0, 1) and Y = pk[4..7] (j = 2, 3); swapping X's
-    // odd lane rows with Y's even ones leaves in X queries 32 qt + 0..15 and in Y queries
-    // 32 qt + 16..31, lane row r holding keys 16 (r & 1) + 4 (r >> 1) + {0..3, 8..11}: the eight
-    // keys at V^T slots 8r..8r+7 of the chunk (vt_pos).
+    __builtin_memcpy(&f, x, sizeof x);
+}
+
+// P = exp2(x) of the scores in w.s into w.pf. Element r = 4j + i of tile (kt, qt) is key
+// 32 kt + 8j + 4h + i. Pairs pk[2j + v] hold keys (8j + 4h + 2v, +1). X = pk[0..3] (j = 0, 1) and
+// Y = pk[4..7] (j = 2, 3); swapping X's odd lane rows with Y's even ones leaves in X queries
+// 32 qt + 0..15 and in Y queries 32 qt + 16..31, lane row r holding keys
+// 16 (r & 1) + 4 (r >> 1) + {0..3, 8..11}: the eight keys at V^T slots 8r..8r+7 of the chunk
+// (vt_pos).
+__device__ __forceinline__ void form_p(WaveState& w) {
 #pragma unroll
     for (int qt = 0; qt < kST; ++qt)
 #pragma unroll
@@ -450,6 +413,79 @@ __device__ __forceinline__ void softmax(WaveState& w, const Flash72Args& a, int 
             w.pf[2 * qt][kt] = *reinterpret_cast<const bf16x8_t*>(&x);
             w.pf[2 * qt + 1][kt] = *reinterpret_cast<const bf16x8_t*>(&y);
         }
+}
+
+// Softmax of the block whose scores are in w.s: masking, the block maximum (the 64 keys of a
+// query sit in lanes l and l ^ 32), P = exp2(s c - m) in bf16 regrouped into w.pf, the lazy
+// rescale. The running maximum m is an integer-valued bf16 number: -m in Q's dim 72 is exact and
+// a rescale moves it by an integer k, so a rescale multiplies P and O by 2^-k exactly, and P is
+// formed before the decision (the maximum and the exponentials interleave; the scores die as
+// they are used).
+template <bool MASKED, bool FIRST>
+__device__ __forceinline__ void softmax(WaveState& w, const Flash72Args& a, int blk,
+                                        unsigned long long bits_all, bool all_masked, int h) {
+    if (MASKED) {
+        const unsigned long long bits = bits_all >> (4 * h);
+        const unsigned long long inrange =
+            (blk * kKV + kKV <= a.Skv) ? ~0ull : (((1ull << (a.Skv - blk * kKV)) - 1ull) >> (4 * h));
+#pragma unroll
+        for (int kt = 0; kt < kSK; ++kt)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int bit = 32 * kt + 8 * (r >> 2) + (r & 3);
+                const bool ok = all_masked ? ((inrange >> bit) & 1ull) : ((bits >> bit) & 1ull);
+#pragma unroll
+                for (int qt = 0; qt < kST; ++qt) {
+                    const float v = all_masked ? 0.0f : w.s[kt][qt][r];
+                    w.s[kt][qt][r] = ok ? v : -INFINITY;
+                }
+            }
+    }
+    float tm[kST];
+    tile_max(w, tm);
+    if constexpr (FIRST) {
+        // The first block sets the maximum, per query over its 64 keys (lanes l, l ^ 32), rounded
+        // up to an integer-valued bf16 number; its scores were formed against m = 0, so x = s c - m
+        // is formed here (later blocks' scores arrive as s c - m from the matrix cores).
+#pragma unroll
+        for (int qt = 0; qt < kST; ++qt) w.mc[qt] = ceil_bf16(ceilf(lane_max2(tm[qt], true)));
+#pragma unroll
+        for (int kt = 0; kt < kSK; ++kt)
+#pragma unroll
+            for (int qt = 0; qt < kST; ++qt)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) w.s[kt][qt][r] -= w.mc[qt];
+        set_neg_max(w, h);
+        form_p(w);
+    } else {
+        // Later blocks move the maximum only when one of their scores exceeds it by more than
+        // the threshold: one maximum over this lane's 64 values and a wave vote decide; the exact
+        // per-query maxima (across lanes) are formed only then.
+        form_p(w);
+        if (__any(fmaxf(tm[0], tm[1]) > kRescaleThreshold)) {
+            const int lr = __lane_id() & 15;
+#pragma unroll
+            for (int qt = 0; qt < kST; ++qt) {
+                const float m = lane_max2(tm[qt], true);
+                // the query's new maximum, an integer-valued bf16 number not below the old one
+                const float mnew = ceil_bf16(w.mc[qt] + ceilf(fmaxf(m, 0.0f)));
+                const float alpha = __builtin_ldexpf(1.0f, -static_cast<int>(mnew - w.mc[qt]));
+                w.mc[qt] = mnew;
+                // O^T tile u = 2 qt + t and P tile u hold query 32 qt + 16 t + l%16
+#pragma unroll
+                for (int t = 0; t < 2; ++t) {
+                    const float au = __shfl(alpha, 16 * t + lr, 64);
+#pragma unroll
+                    for (int e = 0; e < 5; ++e)
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) w.o[e][2 * qt + t][r] *= au;
+#pragma unroll
+                    for (int cc = 0; cc < 2; ++cc) scale_p(w.pf[2 * qt + t][cc], au);
+                }
+            }
+            set_neg_max(w, h);
+        }
+    }
 }
 
 // RESIDENT (kv_len <= 448): every key block is loaded once, up front, into a stage of its own;
