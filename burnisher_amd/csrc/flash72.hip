@@ -113,6 +113,16 @@ __device__ __forceinline__ void dma16(const void* src, const char* lds) {
                  : "s"(l), "v"(src)
                  : "memory", "m0");
 }
+// The same with a wave-uniform base address in SGPRs and this lane's 32-bit byte offset from it
+// (the saddr form: the per-lane address costs no vector instruction).
+__device__ __forceinline__ void dma16s(uint32_t voff, const void* base, const char* lds) {
+    const uint32_t l = static_cast<uint32_t>(
+        reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const char*)(lds)));
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
+                 :
+                 : "s"(l), "v"(voff), "s"(base)
+                 : "memory", "m0");
+}
 #pragma clang diagnostic pop
 
 // Waits until this wave has at most N DMA instructions outstanding and no LDS operation, then
@@ -134,11 +144,11 @@ __device__ __forceinline__ void wait_and_join() {
 // c ^ ((d >> 1) & 7)) in blocks 9..17, spread over the four DMA waves: instruction i of DMA wave
 // w carries block 4i + w. Blocks 18-19 re-load block 0 into the spare area so every wave issues
 // exactly kDmaPerWave instructions. Which kind an instruction is depends only on (i, wave), so
-// the branch on it is scalar. DmaPlan holds this lane's element offset for each instruction at
-// key 0, relative to the (b, h) base of K or V^T, in 32 bits (the launcher checks that it
-// fits); a block then costs one add per instruction.
+// the branch on it is scalar. DmaPlan holds this lane's byte offset for each instruction from the
+// block's first key row of K or V^T, in 32 bits (the launcher checks that one (b, h) slice spans
+// fewer than 2^31 elements); a block's DMA then needs only its two scalar base addresses.
 struct DmaPlan {
-    int off[kDmaPerWave];
+    uint32_t off[kDmaPerWave];
 };
 
 __device__ __forceinline__ bool dma_is_v(int i, int wave) {
@@ -164,34 +174,35 @@ __device__ __forceinline__ DmaPlan dma_plan(const Flash72Args& a, int wave, int 
         if (dma_is_v(i, wave)) {
             const int d = (item - 9) * 8 + (lane >> 3);
             const int c = (lane & 7) ^ ((d >> 1) & 7);
-            p.off[i] = d * static_cast<int>(a.vt_ld) + c * 8;
+            p.off[i] = 2u * static_cast<uint32_t>(d * static_cast<int>(a.vt_ld) + c * 8);
         } else {
             const int lg = (item < 9 ? item : 0) * 64 + lane;   // spares (18, 19) re-load block 0
             const int row = lg / 9, ch = lg - row * 9;
-            p.off[i] = row * static_cast<int>(a.ld_k) + ch * 8;
+            p.off[i] = 2u * static_cast<uint32_t>(row * static_cast<int>(a.ld_k) + ch * 8);
         }
     }
     return p;
 }
 
-// Key block starting at key kv0 into `stage`. `partial`: the block runs past the last key, whose
-// row then stands in for the missing ones (their scores are masked).
+// Key block starting at key kv0 (wave-uniform) into `stage`. `partial`: the block runs past the
+// last key, whose row then stands in for the missing ones (their scores are masked).
 __device__ __forceinline__ void dma_block(char* stage, const Flash72Args& a, const DmaPlan& p,
                                           const bf16_t* kbh, const bf16_t* vbh, int wave, int lane,
                                           int kv0, bool partial) {
+    const bf16_t* kb = kbh + static_cast<int64_t>(kv0) * a.ld_k;
+    const bf16_t* vb = vbh + kv0;
 #pragma unroll
     for (int i = 0; i < kDmaPerWave; ++i) {
-        const bf16_t* src;
+        char* dst = stage + dma_dst(i, wave);
         if (dma_is_v(i, wave)) {
-            src = vbh + (p.off[i] + kv0);
+            dma16s(p.off[i], vb, dst);
         } else if (!partial) {
-            src = kbh + (p.off[i] + kv0 * static_cast<int>(a.ld_k));
+            dma16s(p.off[i], kb, dst);
         } else {
             const int row = dma_krow(i, wave, lane);
-            const int key = min(kv0 + row, a.Skv - 1);
-            src = kbh + (p.off[i] + (key - row) * static_cast<int>(a.ld_k));
+            const int key = min(kv0 + row, a.Skv - 1);   // from kb: key - kv0 - row <= 0 rows
+            dma16(kb + (static_cast<int>(p.off[i] / 2u) + (key - kv0 - row) * static_cast<int>(a.ld_k)), dst);
         }
-        dma16(src, stage + dma_dst(i, wave));
     }
 }
 
@@ -654,7 +665,7 @@ __global__ void __launch_bounds__(WAVES * 64, 1) k_flash72(Flash72Args a) {
         const int last_full = a.Skv / kKV;   // blocks below this one hold 64 real keys
         const DmaPlan plan = dma_plan(a, wave, lane);
         auto issue = [&](int j) {
-            const int blk = live[min(j, n - 1)];
+            const int blk = __builtin_amdgcn_readfirstlane(live[min(j, n - 1)]);
             dma_block(stage_of(j), a, plan, kbh, vbh, wave, lane, blk * kKV, MASKED && blk >= last_full);
         };
         issue(0);
