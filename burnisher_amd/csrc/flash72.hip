@@ -263,6 +263,8 @@ struct WaveState {
 // K fragments during the last output MFMAs. The sched_group_barrier sequence pins that order (left
 // alone, the scheduler sinks each read next to its first use and the wave waits out the LDS
 // latency in front of every group).
+constexpr int kVAhead = 3;   // V^T fragments read ahead of their MFMAs
+constexpr int kKAhead = 2;   // K fragments read ahead of their MFMAs
 template <bool OUT, bool SCORES>
 __device__ __forceinline__ void matrix_phase(WaveState& w, const char* vstage, const int (&vbase)[2],
                                              const char* kstage, const int (&kb)[3]) {
@@ -276,20 +278,19 @@ __device__ __forceinline__ void matrix_phase(WaveState& w, const char* vstage, c
         kf[p] = ld_frag(kstage + (st < kSSteps - 1 ? kb[0] + kt * 32 * kKRow + st * 32 : kb[1 + kt]));
     };
     if (OUT) {
-        read_v(0);
-        read_v(1);
-        read_v(2);
+#pragma unroll
+        for (int i = 0; i < kVAhead; ++i) read_v(i);
 #pragma unroll
         for (int i = 0; i < kVF; ++i) {
 #pragma unroll
             for (int u = 0; u < kQT; ++u)
                 w.o[i >> 1][u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf[i], w.pf[u][i & 1], w.o[i >> 1][u], 0, 0, 0);
-            if (i + 3 < kVF) read_v(i + 3);
-            else if (SCORES && i >= kVF - 2) read_k(i - (kVF - 2));
+            if (i + kVAhead < kVF) read_v(i + kVAhead);
+            else if (SCORES && i >= kVF - kKAhead) read_k(i - (kVF - kKAhead));
         }
     } else if (SCORES) {
-        read_k(0);
-        read_k(1);
+#pragma unroll
+        for (int p = 0; p < kKAhead; ++p) read_k(p);
     }
     if (SCORES) {
         const f32x16_t zero = {};
@@ -300,25 +301,25 @@ __device__ __forceinline__ void matrix_phase(WaveState& w, const char* vstage, c
             for (int qt = 0; qt < kST; ++qt)
                 w.s[kt][qt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
                     kf[p], w.qf[qt][st], st == 0 ? zero : w.s[kt][qt], 0, 0, 0);
-            if (p + 2 < kKF) read_k(p + 2);
+            if (p + kKAhead < kKF) read_k(p + kKAhead);
         }
     }
     // the issue order
     if (OUT) {
-        __builtin_amdgcn_sched_group_barrier(0x100, 3, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, kVAhead, 0);
 #pragma unroll
         for (int i = 0; i < kVF; ++i) {
             __builtin_amdgcn_sched_group_barrier(0x008, kQT, 0);
-            if (i + 3 < kVF || (SCORES && i >= kVF - 2)) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            if (i + kVAhead < kVF || (SCORES && i >= kVF - kKAhead)) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
         }
     } else if (SCORES) {
-        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, kKAhead, 0);
     }
     if (SCORES) {
 #pragma unroll
         for (int p = 0; p < kKF; ++p) {
             __builtin_amdgcn_sched_group_barrier(0x008, kST, 0);
-            if (p + 2 < kKF) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            if (p + kKAhead < kKF) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
         }
     }
 }
