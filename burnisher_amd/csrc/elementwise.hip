@@ -432,18 +432,21 @@ __global__ void __launch_bounds__(256) k_modulate(const T* __restrict__ x, const
     }
 }
 
-// bf16, channels % 8 == 0: 8 elements of one (b, token) row per thread.
+// bf16, channels % 8 == 0: 8 elements of one (b, token) row per thread. I is the index type:
+// 32-bit whenever the tensor has fewer than 2^31 vectors (the divisions by the row and batch
+// lengths are then 32-bit).
+template <typename I>
 __global__ void __launch_bounds__(256) k_modulate_v8(const bf16_t* __restrict__ x,
                                                      const bf16_t* __restrict__ scale,
                                                      const bf16_t* __restrict__ shift, bf16_t* out,
-                                                     int64_t nvec, int64_t tokens, int64_t channels,
+                                                     I nvec, I tokens, I channels,
                                                      const bf16_t* residual,
                                                      const bf16_t* __restrict__ gate) {
-    const int64_t cv = channels / 8;
-    for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < nvec;
-         i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-        const int64_t c = (i % cv) * 8;
-        const int64_t bc = (i / (tokens * cv)) * channels + c;
+    const I cv = channels / 8, bv = tokens * cv;
+    for (I i = blockIdx.x * static_cast<I>(blockDim.x) + threadIdx.x; i < nvec;
+         i += static_cast<I>(gridDim.x) * blockDim.x) {
+        const I c = (i % cv) * 8;
+        const I bc = (i / bv) * channels + c;
         const V8 xv = load8(x + i * 8), sc = load8(scale + bc), sh = load8(shift + bc);
         V8 g, r, o;
         if (gate) g = load8(gate + bc);
@@ -469,6 +472,23 @@ __global__ void __launch_bounds__(256) k_add(const T* a, const T* __restrict__ b
          i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
         const int64_t bi = broadcast ? (i % inner) : i;
         Io<T>::st(out, i, __fadd_rn(Io<T>::ld(a, i), __fmul_rn(scale, Io<T>::ld(b, bi))));
+    }
+}
+
+// bf16, n and inner multiples of 8, every operand 16-byte aligned: 8 elements per thread (a may
+// alias out: each thread reads its vector before writing it).
+template <typename I>
+__global__ void __launch_bounds__(256) k_add_v8(const bf16_t* a, const bf16_t* __restrict__ b,
+                                                bf16_t* out, I nvec, I inner_vec, float scale,
+                                                bool broadcast) {
+    for (I i = blockIdx.x * static_cast<I>(blockDim.x) + threadIdx.x; i < nvec;
+         i += static_cast<I>(gridDim.x) * blockDim.x) {
+        const I bi = broadcast ? i % inner_vec : i;
+        const V8 av = load8(a + static_cast<int64_t>(i) * 8), bv = load8(b + static_cast<int64_t>(bi) * 8);
+        V8 o;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o.f[e] = __fadd_rn(av.f[e], __fmul_rn(scale, bv.f[e]));
+        store8(out + static_cast<int64_t>(i) * 8, o);
     }
 }
 
@@ -758,10 +778,18 @@ void launch_modulate(const void* x, const void* scale, const void* shift, void* 
             static_cast<const float*>(residual), static_cast<const float*>(gate));
     } else if (channels % 8 == 0 && aligned16(x) && aligned16(scale) && aligned16(shift) &&
                aligned16(out) && aligned16(residual) && aligned16(gate)) {
-        k_modulate_v8<<<grid_for(n / 8), 256, 0, s>>>(
-            static_cast<const bf16_t*>(x), static_cast<const bf16_t*>(scale),
-            static_cast<const bf16_t*>(shift), static_cast<bf16_t*>(out), n / 8, tokens, channels,
-            static_cast<const bf16_t*>(residual), static_cast<const bf16_t*>(gate));
+        if (n / 8 < (int64_t{1} << 31))
+            k_modulate_v8<uint32_t><<<grid_for(n / 8), 256, 0, s>>>(
+                static_cast<const bf16_t*>(x), static_cast<const bf16_t*>(scale),
+                static_cast<const bf16_t*>(shift), static_cast<bf16_t*>(out),
+                static_cast<uint32_t>(n / 8), static_cast<uint32_t>(tokens),
+                static_cast<uint32_t>(channels), static_cast<const bf16_t*>(residual),
+                static_cast<const bf16_t*>(gate));
+        else
+            k_modulate_v8<int64_t><<<grid_for(n / 8), 256, 0, s>>>(
+                static_cast<const bf16_t*>(x), static_cast<const bf16_t*>(scale),
+                static_cast<const bf16_t*>(shift), static_cast<bf16_t*>(out), n / 8, tokens,
+                channels, static_cast<const bf16_t*>(residual), static_cast<const bf16_t*>(gate));
     } else {
         k_modulate<bf16_t><<<grid_for(n), 256, 0, s>>>(
             static_cast<const bf16_t*>(x), static_cast<const bf16_t*>(scale),
@@ -806,6 +834,16 @@ void launch_add(const void* a, const void* b, void* out, int64_t outer, int64_t 
                                                  static_cast<const float*>(b),
                                                  static_cast<float*>(out), n, inner, scale,
                                                  broadcast_b);
+    } else if (n % 8 == 0 && inner % 8 == 0 && aligned16(a) && aligned16(b) && aligned16(out)) {
+        if (n / 8 < (int64_t{1} << 31))
+            k_add_v8<uint32_t><<<grid_for(n / 8), 256, 0, s>>>(
+                static_cast<const bf16_t*>(a), static_cast<const bf16_t*>(b),
+                static_cast<bf16_t*>(out), static_cast<uint32_t>(n / 8),
+                static_cast<uint32_t>(inner / 8), scale, broadcast_b);
+        else
+            k_add_v8<int64_t><<<grid_for(n / 8), 256, 0, s>>>(
+                static_cast<const bf16_t*>(a), static_cast<const bf16_t*>(b),
+                static_cast<bf16_t*>(out), n / 8, inner / 8, scale, broadcast_b);
     } else {
         k_add<bf16_t><<<grid_for(n), 256, 0, s>>>(static_cast<const bf16_t*>(a),
                                                   static_cast<const bf16_t*>(b),

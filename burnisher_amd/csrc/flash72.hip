@@ -888,12 +888,56 @@ int64_t flash72_part_floats(int64_t batch, int64_t heads, int64_t q_len, int spl
     return splits > 1 ? static_cast<int64_t>(splits) * batch * heads * q_len * 80 : 0;
 }
 
+// The same with 16-byte accesses (V and V^T 16-byte aligned, ld_v % 8 == 0, vt_ld % 64 == 0):
+// a thread loads 8 dims of one key, then stores the 8 keys of one dim that sit at V^T slots
+// 8q..8q+7 of the block. Those are two runs of four keys (vt_pos keeps runs of four):
+// 32 (q / 4) + 16 (q & 1) + 4 ((q >> 1) & 1) + {0..3, 8..11}.
+__global__ void __launch_bounds__(256) k_transpose_v72_v16(const bf16_t* __restrict__ v, int64_t ld_v,
+                                                           int B, int H, int Skv, bf16_t* vt,
+                                                           int64_t vt_ld) {
+    constexpr int kRow = D + 8;   // 160-byte LDS rows keep every 16-byte chunk aligned
+    __shared__ __attribute__((aligned(16))) bf16_t tile[kKV][kRow];
+    const int nblk = static_cast<int>(vt_ld / kKV);
+    const int blk = blockIdx.x % nblk;
+    const int bh = blockIdx.x / nblk;
+    const int b = bh / H, h = bh - b * H;
+    const int kv0 = blk * kKV;
+    for (int i = threadIdx.x; i < kKV * (D / 8); i += 256) {
+        const int r = i / (D / 8), ch = i - r * (D / 8);
+        const int key = kv0 + r;
+        uint4 x = make_uint4(0u, 0u, 0u, 0u);
+        if (key < Skv)
+            x = *reinterpret_cast<const uint4*>(v + (static_cast<int64_t>(b) * Skv + key) * ld_v + h * D + ch * 8);
+        *reinterpret_cast<uint4*>(&tile[r][ch * 8]) = x;
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < D * (kKV / 8); i += 256) {
+        const int d = i / (kKV / 8), q = i - d * (kKV / 8);
+        const int k0 = 32 * (q >> 2) + 16 * (q & 1) + 4 * ((q >> 1) & 1);
+        uint32_t w[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const int ka = k0 + (t < 2 ? 2 * t : 8 + 2 * (t - 2));
+            w[t] = static_cast<uint32_t>(tile[ka][d]) | (static_cast<uint32_t>(tile[ka + 1][d]) << 16);
+        }
+        *reinterpret_cast<uint4*>(vt + ((static_cast<int64_t>(b) * H + h) * D + d) * vt_ld + kv0 + 8 * q) =
+            make_uint4(w[0], w[1], w[2], w[3]);
+    }
+}
+
 void launch_transpose_v72(const bf16_t* v, int64_t ld_v, int64_t batch, int64_t heads,
                           int64_t kv_len, bf16_t* vt, int64_t vt_ld, hipStream_t s) {
     const int64_t nblk = (vt_ld + kKV - 1) / kKV;
-    k_transpose_v72<<<static_cast<int>(batch * heads * nblk), 256, 0, s>>>(
-        v, ld_v, static_cast<int>(batch), static_cast<int>(heads), static_cast<int>(kv_len), vt,
-        vt_ld);
+    const bool v16 = ld_v % 8 == 0 && vt_ld % kKV == 0 && reinterpret_cast<uintptr_t>(v) % 16 == 0 &&
+                     reinterpret_cast<uintptr_t>(vt) % 16 == 0;
+    if (v16)
+        k_transpose_v72_v16<<<static_cast<int>(batch * heads * nblk), 256, 0, s>>>(
+            v, ld_v, static_cast<int>(batch), static_cast<int>(heads), static_cast<int>(kv_len), vt,
+            vt_ld);
+    else
+        k_transpose_v72<<<static_cast<int>(batch * heads * nblk), 256, 0, s>>>(
+            v, ld_v, static_cast<int>(batch), static_cast<int>(heads), static_cast<int>(kv_len), vt,
+            vt_ld);
     launch_check("transpose V (head_dim 72)");
 }
 

@@ -401,6 +401,19 @@ def test_add_chunk_activation_patch(hip):
         got = empty((B, T * C))
         call("bh_add", P(dev(a)), P(dev(bb)), P(got), B, T * C, 1.0, bc, BF16, None)
         assert np.array_equal(host(got, want), want)
+        # in place on a (the graph's residual add), with a scale
+        want = np.zeros_like(a)
+        st("stock_add", addr(a), addr(bb), addr(want), B, T * C, -0.5, bc, BF16)
+        da = dev(a)
+        call("bh_add", P(da), P(dev(bb)), P(da), B, T * C, -0.5, bc, BF16, None)
+        assert np.array_equal(host(da, want), want)
+    # rows that are not whole 16-byte vectors take the element-wise kernel
+    a3, b3 = randn_bf16(RNG, (3, 36)), randn_bf16(RNG, (36,))
+    want = np.zeros_like(a3)
+    st("stock_add", addr(a3), addr(b3), addr(want), 3, 36, 1.0, 1, BF16)
+    got = empty((3, 36))
+    call("bh_add", P(dev(a3)), P(dev(b3)), P(got), 3, 36, 1.0, 1, BF16, None)
+    assert np.array_equal(host(got, want), want)
     mod, table, emb, out_table = (randn_bf16(RNG, s) for s in ((B, 6 * C), (6, C), (B, C), (2, C)))
     for m, t, chunks, chunk, trow in ((mod, table, 6, 2, 2), (mod, table, 6, 5, -1), (emb, out_table, 1, 0, 1)):
         want = np.zeros((B, C), np.uint16)
