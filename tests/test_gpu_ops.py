@@ -346,6 +346,15 @@ def test_norm_affine_and_unsupported_groupnorm_refused(hip):
     got = empty((rows, cols))
     call("bh_norm", P(dev(x)), P(dev(w)), P(dev(b)), P(got), rows, cols, 1e-6, 0, 0, 0, BF16, None)
     assert np.array_equal(host(got, want), want)
+    # the lane-dense kernel (1152 channels) with weight and bias, LayerNorm and RMSNorm
+    x2, w2, b2 = randn_bf16(RNG, (9, 1152), 1.5), randn_bf16(RNG, (1152,)), randn_bf16(RNG, (1152,))
+    for rms in (0, 1):
+        want = np.zeros_like(x2)
+        st("stock_norm", addr(x2), addr(w2), addr(b2), addr(want), 9, 1152, 1e-6, rms, BF16, 1)
+        got = empty((9, 1152))
+        call("bh_norm", P(dev(x2)), P(dev(w2)), P(dev(b2)), P(got), 9, 1152, 1e-6, rms, 0, 0, BF16, None)
+        s = assert_within(from_bf16(host(got, want)), from_bf16(want), "norm", f"affine 9x1152 rms={rms}")
+        assert s["mismatch_frac"] <= 1e-4, s
     # GroupNorm runs where its channel split fits the kernel (tests/test_gpu_vae.py); 4 channels
     # do not (channels % 8 != 0) and are refused with a sentence, not run approximately
     with pytest.raises(bh.BurnisherError, match="groupnorm"):
