@@ -367,6 +367,12 @@ void forward_fused(bh_dit& e, const void* latent, double t, const void* caption,
         int64_t b0, nb;
         hipStream_t s;
     };
+    // The offset of a row group's V^T in e.vt_op (the op-level attention transposes V there when
+    // the projections do not write V^T): each group gets its own rows, so the two groups of the
+    // split schedule never write the same V^T on their two streams.
+    auto vt_op_offset = [&](const Rows& g, int64_t kv_len) {
+        return g.b0 * H * 72 * flash72_vt_ld(kv_len);
+    };
     // LayerNorm + modulation of x into `modded` with chunk pair (shift c, scale c + 1).
     auto norm = [&](int64_t l, int c, const Rows& g) {
         const int64_t o = g.b0 * N * d;
@@ -411,8 +417,9 @@ void forward_fused(bh_dit& e, const void* latent, double t, const void* caption,
                            e.vt_ld_self, ctx, d, g.nb, H, N, N, scale, nullptr, false, g.s, sp,
                            part, pf);
         } else {
+            const int64_t vo = vt_op_offset(g, N);
             launch_attention_bf16(q, q + d, q + 2 * d, ctx, AttnShape{g.nb, H, N, N, Dh, 3 * d, 3 * d, d, scale},
-                                  nullptr, false, g.s, nullptr, e.vt_op.bf(), e.vt_op_elems, sp,
+                                  nullptr, false, g.s, nullptr, e.vt_op.bf() + vo, e.vt_op_elems - vo, sp,
                                   part, pf);
         }
     };
@@ -444,9 +451,10 @@ void forward_fused(bh_dit& e, const void* latent, double t, const void* caption,
                            e.vt_cross.bf() + (l * B + g.b0) * H * Dh * e.vt_ld_cross, e.vt_ld_cross,
                            ctx, d, g.nb, H, N, e.cap_len, scale, m, mask_f32, g.s, sp, part, pf);
         } else {
+            const int64_t vo = vt_op_offset(g, e.cap_len);
             launch_attention_bf16(q2, kv, kv + d, ctx, AttnShape{g.nb, H, N, e.cap_len, Dh, d, L * 2 * d, d, scale},
-                                  m, mask_f32, g.s, nullptr, e.vt_op.bf(), e.vt_op_elems, sp, part,
-                                  pf);
+                                  m, mask_f32, g.s, nullptr, e.vt_op.bf() + vo, e.vt_op_elems - vo, sp,
+                                  part, pf);
         }
         {
             GemmEpilogue ep;

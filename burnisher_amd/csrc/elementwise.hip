@@ -867,7 +867,8 @@ void launch_modulate(const void* x, const void* scale, const void* shift, void* 
             static_cast<const float*>(residual), static_cast<const float*>(gate));
     } else if (channels % 8 == 0 && aligned16(x) && aligned16(scale) && aligned16(shift) &&
                aligned16(out) && aligned16(residual) && aligned16(gate)) {
-        if (n / 8 < (int64_t{1} << 31))
+        // 32-bit indices while every element offset (i * 8 < n) fits in 32 bits
+        if (n < (int64_t{1} << 32))
             k_modulate_v8<uint32_t><<<grid_for(n / 8), 256, 0, s>>>(
                 static_cast<const bf16_t*>(x), static_cast<const bf16_t*>(scale),
                 static_cast<const bf16_t*>(shift), static_cast<bf16_t*>(out),

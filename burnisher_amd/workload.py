@@ -26,7 +26,7 @@ PIXART_SIGMA = dict(num_layers=28, num_heads=16, head_dim=72, patch_size=2, in_c
                     eps=1e-6)
 
 # The BASELINE configs by resolution: latent side = resolution / 8 (the VAE factor).
-RESOLUTIONS = {512: 64, 1024: 128, 2048: 256}
+RESOLUTIONS = {512: 64, 768: 96, 1024: 128, 1152: 144, 2048: 256}
 
 # checkpoint name <- engine struct field
 TOP_NAMES = {

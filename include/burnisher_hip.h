@@ -297,8 +297,10 @@ typedef enum {
     /* The whole batch through each launch, on the caller's stream (the default). */
     BH_DIT_ROWS_JOINED = 0,
     /* The rows in two groups, each on its own stream from the block loop's start to the output
-     * head: one group's launch tails and epilogues overlap the other group's work (measured
-     * 1.1% faster at 1024px, 1.4% at 2048px). The second stream is the engine's own (default
+     * head, so one group's launch tails and epilogues can overlap the other group's work. At
+     * the current kernels it is slower than JOINED (15.12 against 13.93 ms per 1024px step: each
+     * group's GEMMs have half the tiles, and the two streams' persistent kernels contend for the
+     * CUs), so it is not the default. The second stream is the engine's own (default
      * priority); it joins the caller's stream by events, so a forward on a capturing stream is
      * captured whole. Each launch then covers half the batch and runs beside the other half's,
      * so per-launch kernel timings no longer describe a kernel alone. */

@@ -15,6 +15,10 @@ pytestmark = pytest.mark.gpu
 
 SMALL = dict(num_layers=2, num_heads=4, head_dim=8, patch_size=2, in_channels=4, out_channels=8,
              caption_channels=32, sample_size=8, mlp_ratio=4.0, eps=1e-6)
+# head_dim 72 with an odd head count: the width (216) is no multiple of 144, so the projections
+# do not write V^T and the attention op transposes V into the engine's own buffer.
+ODD72 = dict(num_layers=2, num_heads=3, head_dim=72, patch_size=2, in_channels=4, out_channels=8,
+             caption_channels=64, sample_size=16, mlp_ratio=4.0, eps=1e-6)
 
 
 class Engine:
@@ -88,6 +92,16 @@ def test_small_config_matches_oracle(hip, mode):
         e.close()
 
 
+@pytest.mark.parametrize("mode", [0, 1], ids=["fused", "opwise"])
+def test_odd_heads_head_dim72_matches_oracle(hip, mode):
+    wl = make_workload(ODD72, batch=2, latent_hw=16, caption_len=20)
+    e = Engine(wl, mode)
+    try:
+        check_step(e.forward(), oracle_forward(wl), f"odd72 mode={mode}", gate="dit_block")
+    finally:
+        e.close()
+
+
 def test_fused_plan_equals_opwise_plan(hip):
     # Fusion moves no rounding point, so the two plans agree bit for bit.
     wl = make_workload(PIXART_SIGMA, batch=2, latent_hw=64, caption_len=300, layers=2)
@@ -102,7 +116,8 @@ def test_fused_plan_equals_opwise_plan(hip):
 @pytest.mark.parametrize("cfg,batch,hw,cap,layers", [
     (PIXART_SIGMA, 2, 64, 300, 2),   # the CFG pair at 512px: one row per stream, head_dim 72
     (SMALL, 3, 8, 5, None),          # groups of two rows and one, the generic attention
-], ids=["512px_b2", "small_b3"])
+    (ODD72, 2, 16, 20, None),        # head_dim 72, V transposed per row group by the attention op
+], ids=["512px_b2", "small_b3", "odd72_b2"])
 def test_row_schedules_are_bit_identical(hip, cfg, batch, hw, cap, layers):
     # Rows never mix, so running the two row groups on two streams changes no bit of the output,
     # forward after forward.
@@ -199,6 +214,60 @@ def test_one_block_2048px_matches_oracle(hip):
     finally:
         e.close()
     check_step(got, oracle_forward(wl), "2048px, 1 block", "dit_block")
+
+
+# The reference scores every cell on a resolution and caption length held out from tuning
+# (768 or 1152 px, caption 128 or 300: /root/reference/configs/axes.json:10-24,
+# eval/bench.py:221-224). 1152px has 2 x 5184 = 10368 token rows, no multiple of the GEMMs'
+# 256-row tile, and a 5184-key self-attention whose last 512-query block is ragged.
+@pytest.mark.parametrize("hw,cap", [(96, 128), (96, 300), (144, 128), (144, 300)],
+                         ids=["768px_cap128", "768px_cap300", "1152px_cap128", "1152px_cap300"])
+def test_held_out_shapes_one_block_match_oracle(hip, hw, cap):
+    wl = make_workload(PIXART_SIGMA, batch=2, latent_hw=hw, caption_len=cap, layers=1)
+    for mode in (0, 1):
+        e = Engine(wl, mode)
+        try:
+            got = e.forward()
+        finally:
+            e.close()
+        check_step(got, oracle_forward(wl), f"{hw * 8}px caption {cap}, 1 block, mode={mode}", "dit_block")
+
+
+def test_full_depth_768px_matches_oracle(hip):
+    wl = make_workload(PIXART_SIGMA, batch=2, latent_hw=96, caption_len=300)
+    e = Engine(wl, 0)
+    try:
+        got = e.forward()
+    finally:
+        e.close()
+    check_step(got, oracle_forward(wl), "768px, 28 blocks")
+
+
+def test_full_depth_1152px_invariants(hip):
+    # The held-out 1152px shape at full depth: finite, varied, replayable, timestep- and
+    # caption-sensitive, blind to masked caption positions, and the two plans bit-equal.
+    import torch
+    wl = make_workload(PIXART_SIGMA, batch=2, latent_hw=144, caption_len=128)
+    e = Engine(wl, 0)
+    try:
+        a = e.forward()
+        fa = from_bf16(a)
+        assert np.all(np.isfinite(fa)) and fa.std() > 1e-3
+        assert np.array_equal(a, e.forward())
+        assert np.max(np.abs(fa - from_bf16(e.forward(timestep=100.0)))) > 1e-3
+        cap = e.caption.clone()
+        for b in range(wl.batch):
+            keep = int(wl.mask[b].sum())
+            cap[b, keep:, :] = 99.0
+        assert np.array_equal(a, e.forward(caption=cap))
+        assert np.max(np.abs(fa - from_bf16(e.forward(mask=torch.ones_like(e.mask))))) > 1e-3
+    finally:
+        e.close()
+    o = Engine(wl, 1)
+    try:
+        assert np.array_equal(a, o.forward()), "fused and op-by-op plans differ at 1152px"
+    finally:
+        o.close()
 
 
 def test_full_depth_2048px_invariants(hip):
