@@ -42,7 +42,7 @@ METRIC = "dit-step ms @1024px bf16 (1 GPU) + % of MI355X bf16 MFMA roofline"
 PEAK_BF16_TFLOPS = 2516.6          # 256 CU x 4096 FLOP/clk x 2.4 GHz, dense
 PEAK_HBM_GBS = 8000.0
 REFERENCE_5090_MS = 97.85          # eval/cells/BG-1/reference.json:28 (RTX 5090, cuda impl)
-HW = {512: 64, 1024: 128, 2048: 256}
+HW = {512: 64, 768: 96, 1024: 128, 1152: 144, 2048: 256}
 
 
 # HBM bytes per launch of a kernel, from the rocprofv3 FETCH_SIZE / WRITE_SIZE summaries committed
@@ -356,6 +356,7 @@ def vae(args) -> int:
                  "mfma_frac": round(tflops / PEAK_BF16_TFLOPS, 4),
                  "ceiling_ms": round(flops["total"] / (PEAK_BF16_TFLOPS * 1e12) * 1e3, 3)},
         "kernels": breakdown,
+        "output_stats": output_stats,
     }
     if not args.no_cpu:
         import oracle
@@ -467,6 +468,7 @@ def t5(args) -> int:
                  "mfma_frac": round(tflops / PEAK_BF16_TFLOPS, 4),
                  "ceiling_ms": round(flops["total"] / (PEAK_BF16_TFLOPS * 1e12) * 1e3, 3)},
         "kernels": breakdown,
+        "output_stats": output_stats,
     }
     del tensors, keep, w
     torch.cuda.empty_cache()
@@ -506,6 +508,33 @@ def stock_step(wl, threads: int):
                 wl.batch, wl.latent_hw, wl.caption_len, wl.latent.ctypes.data, wl.timestep,
                 wl.caption.ctypes.data, wl.mask.ctypes.data, 0, out.ctypes.data, threads, -1)
     return out, time.perf_counter() - t0
+
+
+def reference_stock_block(wl):
+    """The reference's own single-threaded stock dit-step (PixArtDiT::forward with every op
+    resolved to `stock`, compiled from /root/reference into oracle/_ref by oracle/Makefile) on
+    workload wl, timed on this host; None where that library was not built. Its output is
+    checked bit for bit against the port's."""
+    import numpy as np
+    import oracle
+    from burnisher_amd.workload import config_struct
+
+    lib = oracle.ref()
+    if lib is None:
+        return None
+    cfg = config_struct(wl.cfg)
+    w, keep = wl.weight_struct(wl.top, wl.blocks)
+    out = np.zeros((wl.batch, wl.cfg["out_channels"], wl.latent_hw, wl.latent_hw), np.uint16)
+    t0 = time.perf_counter()
+    oracle.call(lib, "ref_dit_forward", ctypes.byref(cfg), ctypes.byref(w), wl.batch, wl.latent_hw,
+                wl.caption_len, wl.latent.ctypes.data, wl.timestep, wl.caption.ctypes.data,
+                wl.mask.ctypes.data, 0, out.ctypes.data, -1)
+    secs = time.perf_counter() - t0
+    port, _ = stock_step(wl, 1)
+    return {"config0_block_512px_b1_cap120_ms": round(secs * 1e3, 1), "cores": 1, "kind": "reference",
+            "equals_port": bool(np.array_equal(out, port)),
+            "sample": "BASELINE configs[0]: one block at 512px, batch 1, caption 120, the reference's "
+                      "stock PixArtDiT::forward (oracle/_ref/libref_stock.so), one thread"}
 
 
 def parity(got, want) -> dict:
@@ -669,9 +698,9 @@ def main() -> int:
     log(f"generating the {args.resolution}px workload (seeded synthetic bf16)")
     wl = make_workload(PIXART_SIGMA, batch=args.batch, latent_hw=hw, caption_len=args.caption_len)
     free0 = torch.cuda.mem_get_info()[0]
-    t = lambda a: torch.from_numpy(a.view(np.int16)).view(torch.bfloat16).cuda()
-    top = {k: t(v) for k, v in wl.top.items()}
-    blocks = [{k: t(v) for k, v in b.items()} for b in wl.blocks]
+    # the checkpoint loader's layout (bh_dit_weights_load): packed Q/K/V and caption K/V, which
+    # the engine reads in place
+    top, blocks = wl.weights_to_device()
     weight_bytes = sum(x.numel() * 2 for x in top.values()) + \
         sum(x.numel() * 2 for b in blocks for x in b.values())
     stream = torch.cuda.Stream()
@@ -721,6 +750,9 @@ def main() -> int:
     log(f"timed {args.steps} steps: {ms_per_step:.3f} ms/step; {dominant}: {dn.value} launches, "
         f"{avg_launch_ms * 1e3:.1f} us avg, {achieved:.1f} TFLOP/s")
     got = eng.output()
+    gf = (got.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+    output_stats = {"mean": float(gf.mean()), "std": float(gf.std()), "absmax": float(np.abs(gf).max()),
+                    "finite": bool(np.all(np.isfinite(gf)))}
 
     # the same steps with no event inside a step, and the reference's synchronised median
     plain_ms = timed_steps(eng.step, stream, args.steps)
@@ -802,6 +834,7 @@ def main() -> int:
                             "driver_used_bytes: the drop in the driver's free memory over the same "
                             "allocations, allocator granularity included"},
         "kernels": breakdown,
+        "output_stats": output_stats,
     }
     eng.close()
     if args.headline_only:
@@ -819,12 +852,15 @@ def main() -> int:
     log(f"op-by-op plan: {opwise_ms:.3f} ms/step")
     line["opwise_equals_fused"] = bool(np.array_equal(opwise_out, got))
 
-    # the other full-step configs (BASELINE configs[2] and [4]) on the same device weights
+    # the other full-step configs on the same device weights: BASELINE configs[2] and [4], and
+    # the reference's held-out scoring shapes (768 and 1152 px; caption 300 and 128 --
+    # configs/axes.json:10-24)
     others = {}
-    for res in (512, 2048):
-        if res == args.resolution:
+    for res, cap in ((512, wl.caption_len), (768, wl.caption_len), (1152, wl.caption_len), (1152, 128),
+                     (2048, wl.caption_len)):
+        if res == args.resolution and cap == wl.caption_len:
             continue
-        owl = make_workload(PIXART_SIGMA, batch=wl.batch, latent_hw=HW[res], caption_len=wl.caption_len,
+        owl = make_workload(PIXART_SIGMA, batch=wl.batch, latent_hw=HW[res], caption_len=cap,
                             layers=0)
         owl.cfg["num_layers"] = wl.cfg["num_layers"]
         owl.top, owl.blocks = wl.top, wl.blocks
@@ -836,10 +872,11 @@ def main() -> int:
         ores = oe.output()
         oe.close()
         fo = (ores.astype(np.uint32) << 16).view(np.float32)
-        others[f"{res}px"] = {"ms_per_step": round(o_ms, 4), "flop": of["total"],
-                              "mfma_frac": round(of["total"] / (o_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
-                              "finite": bool(np.all(np.isfinite(fo)))}
-        log(f"{res}px: {o_ms:.3f} ms/step")
+        key = f"{res}px" if cap == wl.caption_len else f"{res}px_cap{cap}"
+        others[key] = {"ms_per_step": round(o_ms, 4), "flop": of["total"],
+                       "mfma_frac": round(of["total"] / (o_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+                       "finite": bool(np.all(np.isfinite(fo)))}
+        log(f"{key}: {o_ms:.3f} ms/step")
     # one block at 512px, batch 1, a 120-token caption (block 0's weights)
     cwl = make_workload(PIXART_SIGMA, batch=1, latent_hw=64, caption_len=120, layers=0)
     cwl.cfg["num_layers"] = 1
@@ -887,6 +924,12 @@ def main() -> int:
             cpu_cfg["config2_step_512px_ms"] = round(s2 * 1e3, 1)
         line["cpu_baseline"]["other_configs"] = cpu_cfg
         log(f"cpu baseline, other configs: {cpu_cfg}")
+        # the reference's own stock path (oracle/_ref, built from its sources; single-threaded as
+        # the reference is), on configs[0] only: its full step would take many minutes
+        ref = reference_stock_block(c0)
+        if ref is not None:
+            line["cpu_baseline"]["reference_single_thread"] = ref
+            log(f"cpu baseline, the reference's own stock on configs[0]: {json.dumps(ref)}")
     print(json.dumps(line), flush=True)
     return status
 

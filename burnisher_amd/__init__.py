@@ -113,6 +113,7 @@ SIGNATURES = {
     "bh_build_info": ([], ctypes.c_char_p),
     "bh_last_error": ([], ctypes.c_char_p),
     "bh_init": ([_I], _I),
+    "bh_set_operand_checks": ([_I], _I),
     "bh_synchronize": ([_V], _I),
     "bh_gemm": ([_V, _V, _V, _V, _I64, _I64, _I64, _I, _I, _I, _V], _I),
     "bh_gemm_fused_run": ([_V, _V, _V, _V, _I64, _I64, _I64, ctypes.POINTER(GemmFused), _V], _I),

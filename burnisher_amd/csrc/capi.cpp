@@ -22,6 +22,7 @@ namespace bh {
 namespace {
 
 thread_local std::string g_error;
+thread_local bool g_operand_checks = true;
 
 hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
 
@@ -123,6 +124,7 @@ ProfileScope::~ProfileScope() {
 void set_gemm_subclass(int cls) { g_gemm_subclass = cls; }
 
 void set_last_error(const std::string& msg) { g_error = msg; }
+bool operand_checks() { return g_operand_checks; }
 int gemm_subclass() { return g_gemm_subclass; }
 
 }  // namespace bh
@@ -139,6 +141,12 @@ const char* bh_build_info(void) {
 }
 
 const char* bh_last_error(void) { return g_error.c_str(); }
+
+int bh_set_operand_checks(int on) {
+    bh::g_operand_checks = on != 0;
+    bh::set_last_error("");
+    return 0;
+}
 
 int bh_init(int device) {
     return guarded([&] {

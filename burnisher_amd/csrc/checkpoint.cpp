@@ -547,23 +547,39 @@ std::vector<Want> dit_tensors(const bh_dit_config& c, bh_dit_device_weights& w) 
         {"proj_out.weight", {p * p * c.out_channels, d}, &t.proj_out_w},
         {"proj_out.bias", {p * p * c.out_channels}, &t.proj_out_b},
     };
+    // The arena keeps this order (each tensor 256-byte aligned): a layer's self-attention Q, K
+    // and V weights back to back, then their biases, and every layer's cross-attention K and V
+    // weights back to back in layer order after all other layer tensors, then their biases. The
+    // fused dit-step engine then reads the packed [3d, d] and [L * 2d, d] projections in place
+    // instead of copying them (when d * 2 bytes is a multiple of the alignment, as at d = 1152).
+    const auto pre = [](int i) { return "transformer_blocks." + std::to_string(i) + "."; };
     for (int i = 0; i < c.num_layers; ++i) {
         bh_dit_block_weights& b = w.blocks[static_cast<size_t>(i)];
-        const std::string pre = "transformer_blocks." + std::to_string(i) + ".";
         const auto add = [&](const char* n, std::vector<int64_t> s, const void** slot) {
-            out.push_back({pre + n, std::move(s), slot});
+            out.push_back({pre(i) + n, std::move(s), slot});
         };
         add("scale_shift_table", {6, d}, &b.scale_shift_table);
-        add("attn1.to_q.weight", {d, d}, &b.attn1_q_w); add("attn1.to_q.bias", {d}, &b.attn1_q_b);
-        add("attn1.to_k.weight", {d, d}, &b.attn1_k_w); add("attn1.to_k.bias", {d}, &b.attn1_k_b);
-        add("attn1.to_v.weight", {d, d}, &b.attn1_v_w); add("attn1.to_v.bias", {d}, &b.attn1_v_b);
+        add("attn1.to_q.weight", {d, d}, &b.attn1_q_w);
+        add("attn1.to_k.weight", {d, d}, &b.attn1_k_w);
+        add("attn1.to_v.weight", {d, d}, &b.attn1_v_w);
+        add("attn1.to_q.bias", {d}, &b.attn1_q_b);
+        add("attn1.to_k.bias", {d}, &b.attn1_k_b);
+        add("attn1.to_v.bias", {d}, &b.attn1_v_b);
         add("attn1.to_out.0.weight", {d, d}, &b.attn1_o_w); add("attn1.to_out.0.bias", {d}, &b.attn1_o_b);
         add("attn2.to_q.weight", {d, d}, &b.attn2_q_w); add("attn2.to_q.bias", {d}, &b.attn2_q_b);
-        add("attn2.to_k.weight", {d, d}, &b.attn2_k_w); add("attn2.to_k.bias", {d}, &b.attn2_k_b);
-        add("attn2.to_v.weight", {d, d}, &b.attn2_v_w); add("attn2.to_v.bias", {d}, &b.attn2_v_b);
         add("attn2.to_out.0.weight", {d, d}, &b.attn2_o_w); add("attn2.to_out.0.bias", {d}, &b.attn2_o_b);
         add("ff.net.0.proj.weight", {dff, d}, &b.ff0_w); add("ff.net.0.proj.bias", {dff}, &b.ff0_b);
         add("ff.net.2.weight", {d, dff}, &b.ff2_w); add("ff.net.2.bias", {d}, &b.ff2_b);
+    }
+    for (int i = 0; i < c.num_layers; ++i) {
+        bh_dit_block_weights& b = w.blocks[static_cast<size_t>(i)];
+        out.push_back({pre(i) + "attn2.to_k.weight", {d, d}, &b.attn2_k_w});
+        out.push_back({pre(i) + "attn2.to_v.weight", {d, d}, &b.attn2_v_w});
+    }
+    for (int i = 0; i < c.num_layers; ++i) {
+        bh_dit_block_weights& b = w.blocks[static_cast<size_t>(i)];
+        out.push_back({pre(i) + "attn2.to_k.bias", {d}, &b.attn2_k_b});
+        out.push_back({pre(i) + "attn2.to_v.bias", {d}, &b.attn2_v_b});
     }
     return out;
 }

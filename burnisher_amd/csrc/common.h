@@ -121,8 +121,11 @@ void set_last_error(const std::string& msg);
 // A pointer the GPU cannot dereference is refused at the boundary rather than faulting in a
 // kernel (the reference's `require_device`, ops_cuda.cu:79-88): null, memory the HIP runtime
 // does not know, and registered or pinned HOST memory are all errors naming the operand.
+// Whether this host thread's calls look operands up (bh_set_operand_checks, capi.cpp).
+bool operand_checks();
 inline void require_device_ptr(const void* p, const char* op, const char* operand) {
     if (!p) throw Error(std::string(op) + ": " + operand + " is null");
+    if (!operand_checks()) return;
     hipPointerAttribute_t attr;
     if (hipPointerGetAttributes(&attr, p) != hipSuccess) {
         (void)hipGetLastError();

@@ -114,12 +114,20 @@ struct bh_dit {
     DevBuf temb, h_t, emb_t, silu_t, modulation, cap_h, cap, kv_all, chunks, tables_dev;
     DevBuf chunks_f32;   // the chunks as floats, scales as 1 + scale (fused norm kernel)
     DevBuf shift, scale, gate, zero, tokens;
-    DevBuf w_qkv, b_qkv, w_kv, b_kv;   // repacked weights (fused plan)
+    // The fused plan's packed projections: every layer's [3d, d] Q/K/V weight and [3d] bias, and
+    // all layers' caption K/V as one [L * 2d, d] weight and [L * 2d] bias. When the caller's
+    // weights already lie that way (each layer's q, k, v back to back; every layer's attn2 k, v
+    // back to back in layer order) these point into them; otherwise into copies in w_qkv ...
+    std::vector<const bf16_t*> qkv_w, qkv_b;
+    const bf16_t* kv_w = nullptr;
+    const bf16_t* kv_b = nullptr;
+    DevBuf w_qkv, b_qkv, w_kv, b_kv;   // ... made at create (fused plan, scattered weights only)
     DevBuf vt_self, vt_cross;         // V transposed for the attention kernel (fused plan)
     DevBuf vt_op;                     // head_dim 72 without the transposed store: the engine's
     int64_t vt_op_elems = 0;          // own V^T buffer (never the op-level shared workspace)
     int64_t vt_ld_self = 0, vt_ld_cross = 0;
     bool vt72 = false;
+    int64_t qkv_ld = 0;               // row stride of qkv: 2d when V goes to V^T, else 3d
     int64_t workspace = 0;
     // Row-group schedule of the fused plan (BH_DIT_ROWS_*): the second row group's stream and the
     // fork/join events, created with the engine when the batch has two or more rows.
@@ -349,7 +357,7 @@ void forward_fused(bh_dit& e, const void* latent, double t, const void* caption,
             kv.vt_heads = c.num_heads;
             kv.vt_dim = c.head_dim;
         }
-        gemm(e, e.cap.bf(), e.w_kv.p, e.b_kv.p, e.kv_all.bf(), e.Mcap, L * 2 * d, d, kv, s);
+        gemm(e, e.cap.bf(), e.kv_w, e.kv_b, e.kv_all.bf(), e.Mcap, L * 2 * d, d, kv, s);
     }
     {
         ProfileScope ps(K_ELEMENTWISE, s, 2.0 * (B * 6 * d + L * 6 * d + L * 6 * B * d));
@@ -387,12 +395,15 @@ void forward_fused(bh_dit& e, const void* latent, double t, const void* caption,
                                      g.s);
         }
     };
-    // 1a. norm, then Q and K into the [M, 3d] buffer; at head_dim 72, V straight into V^T for
-    // the attention kernel (other widths keep V in the buffer for the generic attention)
+    // 1a. norm, then Q and K into the [M, qkv_ld] buffer; at head_dim 72, V straight into V^T
+    // for the attention kernel and the buffer is [M, 2d] (other widths keep V in a [M, 3d]
+    // buffer for the generic attention)
+    const int64_t qkv_ld = e.qkv_ld;
     auto qkv = [&](int64_t l, const Rows& g) {
         norm(l, 0, g);
         SubclassScope sc(K_GEMM_QKV);
         GemmEpilogue ep;
+        ep.ld_out = qkv_ld;
         if (e.vt72) {
             ep.vt = e.vt_self.bf() + g.b0 * H * Dh * e.vt_ld_self;
             ep.vt_period = 3 * d;
@@ -402,18 +413,18 @@ void forward_fused(bh_dit& e, const void* latent, double t, const void* caption,
             ep.vt_heads = static_cast<int>(H);
             ep.vt_dim = static_cast<int>(Dh);
         }
-        gemm(e, e.modded.bf() + g.b0 * N * d, e.w_qkv.bf() + l * 3 * d * d, e.b_qkv.bf() + l * 3 * d,
-             e.qkv.bf() + g.b0 * N * 3 * d, g.nb * N, 3 * d, d, ep, g.s, g.b0 * N, M);
+        gemm(e, e.modded.bf() + g.b0 * N * d, e.qkv_w[l], e.qkv_b[l],
+             e.qkv.bf() + g.b0 * N * qkv_ld, g.nb * N, 3 * d, d, ep, g.s, g.b0 * N, M);
     };
     // 1b. self-attention into ctx
     auto self_attention = [&](const Rows& g) {
-        const bf16_t* q = e.qkv.bf() + g.b0 * N * 3 * d;
+        const bf16_t* q = e.qkv.bf() + g.b0 * N * qkv_ld;
         bf16_t* ctx = e.ctx.bf() + g.b0 * N * d;
         const int sp = e.splits_self;
         float* part = attn_part(e, sp, g.b0, g.nb, N);
         const int64_t pf = flash72_part_floats(g.nb, H, N, sp);
         if (e.vt72) {
-            launch_flash72(q, 3 * d, q + d, 3 * d, e.vt_self.bf() + g.b0 * H * Dh * e.vt_ld_self,
+            launch_flash72(q, qkv_ld, q + d, qkv_ld, e.vt_self.bf() + g.b0 * H * Dh * e.vt_ld_self,
                            e.vt_ld_self, ctx, d, g.nb, H, N, N, scale, nullptr, false, g.s, sp,
                            part, pf);
         } else {
@@ -596,13 +607,15 @@ int bh_dit_create(const bh_dit_config* cfg, const bh_dit_weights* w, int64_t bat
             e->gate = e->make(B * d);
             e->zero = e->make(B * d);
         } else {
-            e->qkv = e->make(M * 3 * d);
+            // the QKV projection's output rows; V goes to V^T instead at head_dim 72 (below)
+            e->vt72 = c.head_dim == 72 && e->N <= 16384 && caption_len <= 16384 && d % 144 == 0;
+            e->qkv_ld = e->vt72 ? 2 * d : 3 * d;
+            e->qkv = e->make(M * e->qkv_ld);
             e->q2 = e->make(M * d);
             e->kv_all = e->make(e->Mcap * L * 2 * d);
             e->chunks = e->make(L * 6 * B * d);
             if (norm_modulate_f32_supported(d)) e->chunks_f32 = e->make_f32(L * 6 * B * d);
             // the head_dim-72 attention reads V transposed, written by the projections' epilogue
-            e->vt72 = c.head_dim == 72 && e->N <= 16384 && caption_len <= 16384 && d % 144 == 0;
             if (e->vt72) {
                 e->vt_ld_self = flash72_vt_ld(e->N);
                 e->vt_ld_cross = flash72_vt_ld(caption_len);
@@ -614,30 +627,68 @@ int bh_dit_create(const bh_dit_config* cfg, const bh_dit_weights* w, int64_t bat
                 e->vt_op_elems = B * c.num_heads * 72 * flash72_vt_ld(std::max(e->N, caption_len));
                 e->vt_op = e->make(e->vt_op_elems);
             }
-            e->w_qkv = e->make(L * 3 * d * d);
-            e->b_qkv = e->make(L * 3 * d);
-            e->w_kv = e->make(L * 2 * d * d);
-            e->b_kv = e->make(L * 2 * d);
             const size_t wb = static_cast<size_t>(d * d) * 2, bb = static_cast<size_t>(d) * 2;
+            auto at = [](const void* base, size_t bytes) {
+                return static_cast<const void*>(static_cast<const char*>(base) + bytes);
+            };
+            // packed in place: Q, K, V of one layer back to back (weights and biases) ...
+            bool qkv_packed = true;
+            for (int64_t l = 0; l < L; ++l) {
+                const bh_dit_block_weights& bw = e->blocks[l];
+                qkv_packed = qkv_packed && bw.attn1_k_w == at(bw.attn1_q_w, wb) &&
+                             bw.attn1_v_w == at(bw.attn1_q_w, 2 * wb) && bw.attn1_k_b == at(bw.attn1_q_b, bb) &&
+                             bw.attn1_v_b == at(bw.attn1_q_b, 2 * bb);
+            }
+            // ... and every layer's caption K, V back to back in layer order
+            bool kv_packed = true;
+            for (int64_t l = 0; l < L; ++l) {
+                const bh_dit_block_weights& bw = e->blocks[l];
+                const bh_dit_block_weights& b0 = e->blocks[0];
+                kv_packed = kv_packed && bw.attn2_k_w == at(b0.attn2_k_w, 2 * l * wb) &&
+                            bw.attn2_v_w == at(b0.attn2_k_w, (2 * l + 1) * wb) &&
+                            bw.attn2_k_b == at(b0.attn2_k_b, 2 * l * bb) &&
+                            bw.attn2_v_b == at(b0.attn2_k_b, (2 * l + 1) * bb);
+            }
+            if (!qkv_packed) {
+                e->w_qkv = e->make(L * 3 * d * d);
+                e->b_qkv = e->make(L * 3 * d);
+            }
+            if (!kv_packed) {
+                e->w_kv = e->make(L * 2 * d * d);
+                e->b_kv = e->make(L * 2 * d);
+            }
+            e->qkv_w.resize(L);
+            e->qkv_b.resize(L);
             std::vector<const bf16_t*> tables(L);
             for (int64_t l = 0; l < L; ++l) {
                 const bh_dit_block_weights& bw = e->blocks[l];
-                char* wq = static_cast<char*>(e->w_qkv.p) + l * 3 * wb;
-                char* bq = static_cast<char*>(e->b_qkv.p) + l * 3 * bb;
-                d2d(wq, bw.attn1_q_w, wb, nullptr);
-                d2d(wq + wb, bw.attn1_k_w, wb, nullptr);
-                d2d(wq + 2 * wb, bw.attn1_v_w, wb, nullptr);
-                d2d(bq, bw.attn1_q_b, bb, nullptr);
-                d2d(bq + bb, bw.attn1_k_b, bb, nullptr);
-                d2d(bq + 2 * bb, bw.attn1_v_b, bb, nullptr);
-                char* wk = static_cast<char*>(e->w_kv.p) + l * 2 * wb;
-                char* bk = static_cast<char*>(e->b_kv.p) + l * 2 * bb;
-                d2d(wk, bw.attn2_k_w, wb, nullptr);
-                d2d(wk + wb, bw.attn2_v_w, wb, nullptr);
-                d2d(bk, bw.attn2_k_b, bb, nullptr);
-                d2d(bk + bb, bw.attn2_v_b, bb, nullptr);
+                if (qkv_packed) {
+                    e->qkv_w[l] = static_cast<const bf16_t*>(bw.attn1_q_w);
+                    e->qkv_b[l] = static_cast<const bf16_t*>(bw.attn1_q_b);
+                } else {
+                    char* wq = static_cast<char*>(e->w_qkv.p) + l * 3 * wb;
+                    char* bq = static_cast<char*>(e->b_qkv.p) + l * 3 * bb;
+                    d2d(wq, bw.attn1_q_w, wb, nullptr);
+                    d2d(wq + wb, bw.attn1_k_w, wb, nullptr);
+                    d2d(wq + 2 * wb, bw.attn1_v_w, wb, nullptr);
+                    d2d(bq, bw.attn1_q_b, bb, nullptr);
+                    d2d(bq + bb, bw.attn1_k_b, bb, nullptr);
+                    d2d(bq + 2 * bb, bw.attn1_v_b, bb, nullptr);
+                    e->qkv_w[l] = reinterpret_cast<const bf16_t*>(wq);
+                    e->qkv_b[l] = reinterpret_cast<const bf16_t*>(bq);
+                }
+                if (!kv_packed) {
+                    char* wk = static_cast<char*>(e->w_kv.p) + l * 2 * wb;
+                    char* bk = static_cast<char*>(e->b_kv.p) + l * 2 * bb;
+                    d2d(wk, bw.attn2_k_w, wb, nullptr);
+                    d2d(wk + wb, bw.attn2_v_w, wb, nullptr);
+                    d2d(bk, bw.attn2_k_b, bb, nullptr);
+                    d2d(bk + bb, bw.attn2_v_b, bb, nullptr);
+                }
                 tables[l] = static_cast<const bf16_t*>(bw.scale_shift_table);
             }
+            e->kv_w = kv_packed ? static_cast<const bf16_t*>(e->blocks[0].attn2_k_w) : e->w_kv.bf();
+            e->kv_b = kv_packed ? static_cast<const bf16_t*>(e->blocks[0].attn2_k_b) : e->b_kv.bf();
             e->tables_dev = DevBuf(sizeof(void*) * L);
             e->workspace += static_cast<int64_t>(sizeof(void*) * L);
             hip_check(hipMemcpy(e->tables_dev.p, tables.data(), sizeof(void*) * L,

@@ -36,6 +36,10 @@ struct Pool {
     size_t live = 0, peak = 0;
     std::multimap<size_t, void*> cached;    // size -> free block
     std::map<void*, size_t> owned;          // block -> size, for every live block
+    // The driver's free bytes as of the last fresh allocation, moved by this pool's own frees
+    // since: a release decides between caching and freeing on it without a driver query (each
+    // query is a system call, and a forward releases every intermediate).
+    size_t free_est = 0;
 };
 
 // Leaked on purpose: Tensor deleters can run after static destruction.
@@ -54,7 +58,10 @@ size_t free_bytes() {
 }
 
 void drop_cache_locked(Pool& p) {
-    for (auto& kv : p.cached) (void)hipFree(kv.second);
+    for (auto& kv : p.cached) {
+        (void)hipFree(kv.second);
+        p.free_est += kv.first;
+    }
     p.cached.clear();
 }
 
@@ -84,9 +91,12 @@ void* alloc(size_t bytes) {
             ptr = nullptr;
             check(hipMalloc(&ptr, bytes), "hipMalloc");
         }
-        if (free_bytes() < kHeadroom) {
-            std::lock_guard<std::mutex> lock(p.mu);
+        const size_t f = free_bytes();
+        std::lock_guard<std::mutex> lock(p.mu);
+        p.free_est = f;
+        if (f < kHeadroom) {
             drop_cache_locked(p);
+            p.free_est = free_bytes();
         }
     }
     check(hipMemsetAsync(ptr, 0, bytes, nullptr), "hipMemsetAsync (zero fill)");
@@ -109,8 +119,12 @@ void release(void* ptr) {
     const size_t bytes = it->second;
     p.owned.erase(it);
     p.live -= std::min(p.live, bytes);
-    if (free_bytes() >= kHeadroom) p.cached.emplace(bytes, ptr);
-    else (void)hipFree(ptr);
+    if (p.free_est >= kHeadroom) {
+        p.cached.emplace(bytes, ptr);
+    } else {
+        (void)hipFree(ptr);
+        p.free_est += bytes;
+    }
 }
 
 void copy_to_device(void* dst, const void* src, size_t bytes) {

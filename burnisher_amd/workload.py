@@ -127,15 +127,40 @@ class DitWorkload:
         return w, blocks
 
     def to_device(self, device="cuda"):
-        """(top, blocks, latent, caption, mask) as torch tensors on `device` (bf16; mask fp32)."""
+        """(top, blocks, latent, caption, mask) as torch tensors on `device` (bf16; mask fp32).
+
+        Laid out as the checkpoint loader lays them (bh_dit_weights_load): each layer's
+        self-attention Q, K, V weights in one allocation (and their biases in another), and every
+        layer's cross-attention K, V weights in one allocation in layer order (biases likewise),
+        so the fused engine reads its packed projections in place rather than copying them."""
         import torch
 
         def t(a):
-            return torch.from_numpy(a.view(np.int16)).view(torch.bfloat16).to(device)
-        top = {k: t(v) for k, v in self.top.items()}
-        blocks = [{k: t(v) for k, v in b.items()} for b in self.blocks]
+            return torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).view(torch.bfloat16).to(device)
+        top, blocks = self.weights_to_device(device)
         return (top, blocks, t(self.latent), t(self.caption),
                 torch.from_numpy(self.mask).to(device))
+
+    def weights_to_device(self, device="cuda"):
+        """(top, blocks) of to_device: the weights alone, in the same packed layout."""
+        import torch
+
+        def t(a):
+            return torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).view(torch.bfloat16).to(device)
+        top = {k: t(v) for k, v in self.top.items()}
+        packed = ("attn1_q", "attn1_k", "attn1_v", "attn2_k", "attn2_v")
+        blocks = [{k: t(v) for k, v in b.items() if not k.startswith(packed)} for b in self.blocks]
+        if self.blocks:
+            kv_w = t(np.stack([np.stack([b["attn2_k_w"], b["attn2_v_w"]]) for b in self.blocks]))
+            kv_b = t(np.stack([np.stack([b["attn2_k_b"], b["attn2_v_b"]]) for b in self.blocks]))
+        for i, (src, blk) in enumerate(zip(self.blocks, blocks)):
+            qkv_w = t(np.stack([src["attn1_q_w"], src["attn1_k_w"], src["attn1_v_w"]]))
+            qkv_b = t(np.stack([src["attn1_q_b"], src["attn1_k_b"], src["attn1_v_b"]]))
+            for j, p in enumerate("qkv"):
+                blk[f"attn1_{p}_w"], blk[f"attn1_{p}_b"] = qkv_w[j], qkv_b[j]
+            for j, p in enumerate("kv"):
+                blk[f"attn2_{p}_w"], blk[f"attn2_{p}_b"] = kv_w[i, j], kv_b[i, j]
+        return top, blocks
 
 
 def prefix_mask(batch: int, caption_len: int) -> np.ndarray:

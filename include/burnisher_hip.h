@@ -48,6 +48,14 @@ const char* bh_last_error(void);
 int bh_init(int device);
 /* hipStreamSynchronize(stream) with error reporting. */
 int bh_synchronize(void* stream);
+/* Whether the entry points called from this host thread ask the HIP runtime about every operand
+ * pointer (hipPointerGetAttributes) to refuse host memory (on = 1, the default) or only refuse
+ * null operands (0). No counterpart in the reference, whose ops read the device from the Tensor
+ * (Tensor::device(), tensor.h:39) and refuse a host tensor in `require_device`
+ * (ops_cuda.cu:79-88). A caller that knows where its operands live the same way -- the registry
+ * adapter, which checks each Tensor's device before every call -- turns the runtime lookups off:
+ * they cost several host microseconds per operand and per op. */
+int bh_set_operand_checks(int on);
 
 /* ---- per-op entry points (the registry boundary) ------------------------------------------ */
 

@@ -102,6 +102,31 @@ def test_odd_heads_head_dim72_matches_oracle(hip, mode):
         e.close()
 
 
+def test_packed_and_scattered_weights_agree(hip):
+    # The fused engine reads Q/K/V and the caption K/V in place when the caller's weights are laid
+    # out packed (the checkpoint loader's and the workload's layout) and copies them otherwise:
+    # both give the same bytes, and the packed engine holds no copy (3 + 2 d x d per layer less).
+    import torch
+    import burnisher_amd as bh
+    wl = make_workload(PIXART_SIGMA, batch=2, latent_hw=32, caption_len=120, layers=3)
+    packed = Engine(wl, 0)
+    scattered = Engine(wl, 0)
+    try:
+        scattered.close()
+        scattered.blocks = [{k: v.clone() for k, v in b.items()} for b in packed.blocks]   # one allocation each
+        scattered.w, scattered._keep = wl.weight_struct(scattered.top, scattered.blocks)
+        scattered.handle = ctypes.c_void_p()
+        bh.call("bh_dit_create", ctypes.byref(scattered.cfg), ctypes.byref(scattered.w), wl.batch,
+                wl.latent_hw, wl.caption_len, 0, ctypes.byref(scattered.handle))
+        assert np.array_equal(packed.forward(), scattered.forward())
+        d = 1152
+        saved = bh.lib().bh_dit_workspace_bytes(scattered.handle) - bh.lib().bh_dit_workspace_bytes(packed.handle)
+        assert saved == 3 * (5 * d * d + 5 * d) * 2, saved
+    finally:
+        packed.close()
+        scattered.close()
+
+
 def test_fused_plan_equals_opwise_plan(hip):
     # Fusion moves no rounding point, so the two plans agree bit for bit.
     wl = make_workload(PIXART_SIGMA, batch=2, latent_hw=64, caption_len=300, layers=2)

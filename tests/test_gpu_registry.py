@@ -73,10 +73,45 @@ def test_reference_graph_through_registry_equals_engines(driver, tmp_path, hip, 
     assert np.array_equal(got, engine_output(wl, 0)), "differs from the fused engine"
 
 
+def engine_median_ms(wl, mode, iters):
+    # the reference bench's method (burnisher_main.cpp:451-464): each forward timed on the host
+    # clock from launch to device synchronisation, median of `iters` after one warm-up
+    import time
+    import torch
+    import burnisher_amd as bh
+    top, blocks, latent, caption, mask = wl.to_device()
+    cfg = config_struct(wl.cfg)
+    w, keep = wl.weight_struct(top, blocks)
+    h = ctypes.c_void_p()
+    bh.call("bh_dit_create", ctypes.byref(cfg), ctypes.byref(w), wl.batch, wl.latent_hw, wl.caption_len,
+            mode, ctypes.byref(h))
+    try:
+        out = torch.zeros((wl.batch, cfg.out_channels, wl.latent_hw, wl.latent_hw), dtype=torch.bfloat16,
+                          device="cuda")
+        ms = []
+        for i in range(iters + 1):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            bh.call("bh_dit_forward", h, latent.data_ptr(), wl.timestep, caption.data_ptr(), mask.data_ptr(),
+                    F32, out.data_ptr(), None)
+            torch.cuda.synchronize()
+            if i:
+                ms.append((time.perf_counter() - t0) * 1e3)
+        return float(np.median(ms))
+    finally:
+        bh.lib().bh_dit_destroy(h)
+
+
 def test_reference_graph_1024px_full_depth_equals_engine_and_is_timed(driver, tmp_path, hip):
     # The headline configuration through the reference's own graph and the registry: the output
-    # equals the fused engine's, and the driver reports the reference bench's median and peak.
-    got, line = reference_graph(driver, tmp_path, 28, 2, 128, 300, iters=5)
+    # equals the fused engine's, and the driver reports the reference bench's median and peak,
+    # printed beside the library's op-by-op and fused engines timed the same way in this process.
+    got, line = reference_graph(driver, tmp_path, 28, 2, 128, 300, iters=10)
     wl = make_workload(PIXART_SIGMA, batch=2, latent_hw=128, caption_len=300)
     assert np.array_equal(got, engine_output(wl, 0))
     assert line["median_ms"] > 0 and line["peak_vram_bytes"] >= line["weights_bytes"] > 1_000_000_000
+    opwise, fused = engine_median_ms(wl, 1, 10), engine_median_ms(wl, 0, 10)
+    print("registry path vs engines (host-clock median, ms):", json.dumps({
+        "registry_ms_per_step": line["median_ms"], "opwise_ms_per_step": round(opwise, 4),
+        "fused_ms_per_step": round(fused, 4), "registry_over_opwise": round(line["median_ms"] / opwise, 4),
+        "registry_peak_vram_bytes": line["peak_vram_bytes"], "effective": line["effective"]}), flush=True)
