@@ -339,7 +339,13 @@ __global__ void __launch_bounds__(256) k_norm_mod_dense(
     constexpr int kE = Row::kE;
     constexpr int pair0 = NV * 8 * kWave;   // first channel of the pairs
     const int lane = threadIdx.x % kWave;
-    const int64_t row = static_cast<int64_t>(blockIdx.x) * (blockDim.x / kWave) + wave_index();
+    // Workgroup i runs on XCD i % 8. With a grid of whole eighths, XCD x takes the x-th eighth of
+    // the rows: the rows the GEMM before this norm wrote from that XCD's CUs (its tile order gives
+    // XCD x the x-th eighth of the M-tiles) and the rows the GEMM after it reads there, so both
+    // meet in that XCD's L2.
+    int64_t wg = blockIdx.x;
+    if ((gridDim.x & 7) == 0) wg = (wg & 7) * (gridDim.x >> 3) + (wg >> 3);
+    const int64_t row = wg * (blockDim.x / kWave) + wave_index();
     if (row >= rows) return;
     Row cur;
     cur.load(x + row * cols, lane);

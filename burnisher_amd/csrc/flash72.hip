@@ -521,16 +521,33 @@ __global__ void __launch_bounds__(WAVES * 64, 1) k_flash72(Flash72Args a) {
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lr = lane & 15, g = lane >> 4;
 
-    // ---- which (b, h, query block, key split): the blocks of one (b, h) stay on one XCD ----
+    // ---- which (b, h, query block, key split): the blocks of one (b, h) stay on one XCD (the
+    // self-attention: a head's K and V are read by all its query blocks) ----
     const int splits = SPLIT ? a.splits : 1;
     const int T = a.B * a.H * a.qblocks * splits;
-    int bid = blockIdx.x;
-    if ((T & 7) == 0) bid = (bid & 7) * (T >> 3) + (bid >> 3);
-    const int split = SPLIT ? bid % splits : 0;
-    if (SPLIT) bid /= splits;
-    const int bh = bid / a.qblocks;
-    const int b = bh / a.H, h = bh - b * a.H;
-    const int q_base = (bid - bh * a.qblocks) * (WAVES * kQPerWave) + wave * kQPerWave;
+    int b, h, qblk, split = 0;
+    if (RESIDENT && ((a.B * a.qblocks) & 7) == 0) {
+        // The caption cross-attention: its keys are few and every workgroup loads all of them, so
+        // workgroups are placed by query rows instead: XCD x (workgroup i runs on XCD i % 8) takes
+        // the x-th eighth of the batch's query rows, every head. Those are the rows the XCD's own
+        // CUs wrote in the Q projection just before (the GEMM gives XCD x the x-th eighth of its
+        // M-tiles), and the rows its out-projection reads next: both meet this XCD's L2.
+        const int x = blockIdx.x & 7, i = blockIdx.x >> 3;
+        const int rb = x * (a.B * a.qblocks / 8) + i / a.H;
+        h = i % a.H;
+        b = rb / a.qblocks;
+        qblk = rb - b * a.qblocks;
+    } else {
+        int bid = blockIdx.x;
+        if ((T & 7) == 0) bid = (bid & 7) * (T >> 3) + (bid >> 3);
+        split = SPLIT ? bid % splits : 0;
+        if (SPLIT) bid /= splits;
+        const int bh = bid / a.qblocks;
+        b = bh / a.H;
+        h = bh - b * a.H;
+        qblk = bid - bh * a.qblocks;
+    }
+    const int q_base = qblk * (WAVES * kQPerWave) + wave * kQPerWave;
     const int nblk = (a.Skv + kKV - 1) / kKV;
     const int kb0 = SPLIT ? split * nblk / splits : 0;
     const int kb1 = SPLIT ? (split + 1) * nblk / splits : nblk;
