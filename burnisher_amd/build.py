@@ -50,6 +50,7 @@ def sources() -> list[Path]:
 # rescaled by VALU multiplies, and in the default AGPR form every rescale and loop iteration
 # copies all 80 of them between the register files), and it is compiled without IEEE NaN rules
 # so a maximum over MFMA results is one v_max3 per two inputs, not a quieting v_max per input.
+# cross_fused.hip runs the same attention code after its projection, so it takes the same options.
 # denoise.hip evaluates the guidance combine and the solver update in fp64 exactly as the
 # reference's x86-64 build does, which forms no multiply-add. elementwise.hip holds the kernels
 # that reproduce the oracle's arithmetic bit for bit (norms, modulate, add, chunk, activation,
@@ -59,6 +60,7 @@ def sources() -> list[Path]:
 # accumulators in VGPRs: in the AGPR form the compiler rotates them through ~50 copies per
 # eight MFMAs, which would measure the copies rather than the matrix cores.
 EXTRA_FLAGS = {"flash72.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form", "-fno-honor-nans"],
+               "cross_fused.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form", "-fno-honor-nans"],
                "denoise.hip": ["-ffp-contract=off"],
                "elementwise.hip": ["-ffp-contract=off"],
                "probe.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}

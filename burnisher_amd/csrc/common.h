@@ -366,6 +366,16 @@ void launch_flash72(const bf16_t* q, int64_t ld_q, const bf16_t* k, int64_t ld_k
 // each) would fill at most half the CUs: as many as still fit at once, at least two key blocks
 // each; 1 for the resident (kv_len <= 448) kernel and for an output whose rows are not 16-byte
 // aligned.
+// The cross-attention block's Q projection and its head_dim-72 attention over a short caption in
+// one launch (cross_fused.hip): ctx = attention(bf16(x wq^T + bq), K, V^T, mask), bit-identical
+// with launch_gemm_bf16 followed by launch_flash72. x is [batch * tokens, heads * 72]; K rows of
+// stride ld_k at [batch, kv_len]; V^T as launch_flash72 reads it. Supported when tokens % 256 == 0,
+// the head count is even, kv_len <= 448 and the 256 x 144 tiles fill the chip.
+bool cross_fused_supported(int64_t batch, int64_t tokens, int64_t heads, int64_t head_dim, int64_t kv_len);
+void launch_cross_fused(const bf16_t* x, const bf16_t* wq, const bf16_t* bq, int64_t batch,
+                        int64_t tokens, int64_t heads, const bf16_t* k, int64_t ld_k, const bf16_t* vt,
+                        int64_t vt_ld, int64_t kv_len, const void* key_mask, bool mask_f32,
+                        bf16_t* ctx, int64_t ld_o, float scale, hipStream_t s);
 int flash72_splits(int64_t batch, int64_t heads, int64_t q_len, int64_t kv_len,
                    const void* out = nullptr, int64_t ld_o = 8);
 int64_t flash72_part_floats(int64_t batch, int64_t heads, int64_t q_len, int splits);

@@ -128,6 +128,10 @@ struct bh_dit {
     int64_t vt_ld_self = 0, vt_ld_cross = 0;
     bool vt72 = false;
     int64_t qkv_ld = 0;               // row stride of qkv: 2d when V goes to V^T, else 3d
+    // The cross-attention's Q projection fused into its attention (cross_fused.hip), for launches
+    // of at least cross_fused_min_rows batch rows (its 256 x 144 tiles must fill the chip).
+    bool cross_fused = false;
+    int64_t cross_fused_min_rows = 0;
     int64_t workspace = 0;
     // Row-group schedule of the fused plan (BH_DIT_ROWS_*): the second row group's stream and the
     // fork/join events, created with the engine when the batch has two or more rows.
@@ -450,22 +454,31 @@ void forward_fused(bh_dit& e, const void* latent, double t, const void* caption,
             gemm(e, ctx, bw.attn1_o_w, bw.attn1_o_b, x, rows, d, d, ep, g.s, g.b0 * N, M);
         }
         // 2. cross-attention (no norm before it: pixart_dit.cpp:251-253)
-        bf16_t* q2 = e.q2.bf() + o;
-        gemm(e, x, bw.attn2_q_w, bw.attn2_q_b, q2, rows, d, d, plain, g.s, g.b0 * N, M);
         const bf16_t* kv = e.kv_all.bf() + g.b0 * e.cap_len * L * 2 * d + l * 2 * d;
         const void* m = static_cast<const char*>(mask) + g.b0 * e.cap_len * mask_elem;
         const int sp = e.splits_cross;
         float* part = attn_part(e, sp, g.b0, g.nb, N);
         const int64_t pf = flash72_part_floats(g.nb, H, N, sp);
-        if (e.vt72) {
-            launch_flash72(q2, d, kv, L * 2 * d,
-                           e.vt_cross.bf() + (l * B + g.b0) * H * Dh * e.vt_ld_cross, e.vt_ld_cross,
-                           ctx, d, g.nb, H, N, e.cap_len, scale, m, mask_f32, g.s, sp, part, pf);
+        if (e.cross_fused && g.nb >= e.cross_fused_min_rows) {
+            // the Q projection and the attention in one launch, bit-identical with the two below
+            launch_cross_fused(x, static_cast<const bf16_t*>(bw.attn2_q_w),
+                               static_cast<const bf16_t*>(bw.attn2_q_b), g.nb, N, H, kv, L * 2 * d,
+                               e.vt_cross.bf() + (l * B + g.b0) * H * Dh * e.vt_ld_cross, e.vt_ld_cross,
+                               e.cap_len, m, mask_f32, ctx, d, scale, g.s);
         } else {
-            const int64_t vo = vt_op_offset(g, e.cap_len);
-            launch_attention_bf16(q2, kv, kv + d, ctx, AttnShape{g.nb, H, N, e.cap_len, Dh, d, L * 2 * d, d, scale},
-                                  m, mask_f32, g.s, nullptr, e.vt_op.bf() + vo, e.vt_op_elems - vo, sp,
-                                  part, pf);
+            bf16_t* q2 = e.q2.bf() + o;
+            gemm(e, x, bw.attn2_q_w, bw.attn2_q_b, q2, rows, d, d, plain, g.s, g.b0 * N, M);
+            if (e.vt72) {
+                launch_flash72(q2, d, kv, L * 2 * d,
+                               e.vt_cross.bf() + (l * B + g.b0) * H * Dh * e.vt_ld_cross, e.vt_ld_cross,
+                               ctx, d, g.nb, H, N, e.cap_len, scale, m, mask_f32, g.s, sp, part, pf);
+            } else {
+                const int64_t vo = vt_op_offset(g, e.cap_len);
+                launch_attention_bf16(q2, kv, kv + d, ctx,
+                                      AttnShape{g.nb, H, N, e.cap_len, Dh, d, L * 2 * d, d, scale}, m,
+                                      mask_f32, g.s, nullptr, e.vt_op.bf() + vo, e.vt_op_elems - vo, sp,
+                                      part, pf);
+            }
         }
         {
             GemmEpilogue ep;
@@ -617,6 +630,12 @@ int bh_dit_create(const bh_dit_config* cfg, const bh_dit_weights* w, int64_t bat
             if (norm_modulate_f32_supported(d)) e->chunks_f32 = e->make_f32(L * 6 * B * d);
             // the head_dim-72 attention reads V transposed, written by the projections' epilogue
             if (e->vt72) {
+                for (int64_t nb = 1; nb <= B && !e->cross_fused; ++nb) {
+                    if (cross_fused_supported(nb, e->N, c.num_heads, c.head_dim, caption_len)) {
+                        e->cross_fused = true;
+                        e->cross_fused_min_rows = nb;
+                    }
+                }
                 e->vt_ld_self = flash72_vt_ld(e->N);
                 e->vt_ld_cross = flash72_vt_ld(caption_len);
                 e->vt_self = e->make(B * c.num_heads * 72 * e->vt_ld_self);

@@ -56,449 +56,8 @@
 namespace bh {
 namespace {
 
-constexpr int D = 72;
-constexpr int kWaves = 8;
-constexpr int kThreads = kWaves * 64;
-constexpr int kQPerWave = 64;
-constexpr int kQPerWg = kWaves * kQPerWave;   // 512
-constexpr int kKV = 64;                       // keys per block
-constexpr int kQT = 4;                        // 16-query tiles per wave (output product)
-constexpr int kST = 2;                        // 32-query tiles per wave (score product)
-constexpr int kSK = 2;                        // 32-key tiles per block (score product)
-constexpr int kSSteps = 5;                    // K = 16 steps of the score product: dims 0..79
-constexpr int kKRow = D * 2;                  // 144 bytes per K row in LDS
-constexpr int kKBytes = kKV * kKRow;          // 9216 = 9 DMA blocks
-constexpr int kVRows = 80;                    // 72 dims + the ones row + zero rows
-constexpr int kVBytes = kVRows * 128;         // 128 bytes = 64 keys per V^T row
-constexpr int kOnesOff = kKBytes + D * 128;   // V^T row 72 of a stage: 64 bf16 ones
-constexpr int kSpareBytes = 2 * 1024;
-constexpr int kStage = kKBytes + kVBytes + kSpareBytes;   // 21504
-constexpr int kStages = 4;
-constexpr int kResidentBlocks = 7;            // key blocks a resident launch holds (kv_len <= 448)
-constexpr int kDmaWaves = 4;                  // waves 0-3 issue the DMA
-constexpr int kDmaPerWave = 5;                // 9 K + 9 V^T + 2 spare blocks over 4 waves
-constexpr int kMaxBlocks = 256;               // kv_len <= 16384 (the 2048px token count)
-constexpr float kRescaleThreshold = 8.0f;     // log2 units
-
-struct Flash72Args {
-    const bf16_t* q;
-    const bf16_t* k;
-    const bf16_t* vt;
-    bf16_t* out;
-    const void* mask;
-    int64_t ld_q, ld_k, vt_ld, ld_o;
-    int B, H, Sq, Skv;
-    int mask_f32;
-    int qblocks;
-    float c;   // scale * log2(e)
-    // Split over keys (low-occupancy shapes): workgroup (b, h, query block, split) takes key
-    // blocks [split * nblk / splits, (split + 1) * nblk / splits) and, when `part` is set,
-    // writes its unnormalised partial instead of the output:
-    // part[((split * B + b) * H + h) * Sq + q][0..79] = O over dims 0..71, the row sum at 72, the
-    // running maximum (log2 units) at 73.
-    int splits = 1;
-    float* part = nullptr;
-};
-
-#pragma clang diagnostic push
-#pragma clang diagnostic ignored "-Winline-asm"
-// One global_load_lds_dwordx4: lane L's 16 bytes at `src` land at LDS address lds + 16 L (`lds`
-// wave-uniform). Inline assembly so that the compiler does not track the LDS writes (its
-// tracking is conservative at loop headers); the explicit vmcnt waits cover them.
-__device__ __forceinline__ void dma16(const void* src, const char* lds) {
-    const uint32_t l = static_cast<uint32_t>(
-        reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const char*)(lds)));
-    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
-                 :
-                 : "s"(l), "v"(src)
-                 : "memory", "m0");
-}
-// The same with a wave-uniform base address in SGPRs and this lane's 32-bit byte offset from it
-// (the saddr form: the per-lane address costs no vector instruction).
-__device__ __forceinline__ void dma16s(uint32_t voff, const void* base, const char* lds) {
-    const uint32_t l = static_cast<uint32_t>(
-        reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const char*)(lds)));
-    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
-                 :
-                 : "s"(l), "v"(voff), "s"(base)
-                 : "memory", "m0");
-}
-#pragma clang diagnostic pop
-
-// Waits until this wave has at most N DMA instructions outstanding and no LDS operation, then
-// joins the workgroup; the empty asm statements keep every LDS access on its side.
-template <int N>
-__device__ __forceinline__ void wait_and_join() {
-    // sched_barrier: no instruction, MFMAs included, is moved across (the memory clobbers only
-    // pin memory operations), so each phase's work stays between its two barriers
-    __builtin_amdgcn_sched_barrier(0);
-    asm volatile("" ::: "memory");
-    s_waitcnt<N, 0>();
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_sched_barrier(0);
-}
-
-// The key blocks stream into `stage` as K rows (144 bytes each, contiguous) in DMA blocks 0..8
-// and V^T rows 0..71 (128 bytes = the block's 64 keys, 16-byte chunk c of row d stored at slot
-// c ^ ((d >> 1) & 7)) in blocks 9..17, spread over the four DMA waves: instruction i of DMA wave
-// w carries block 4i + w. Blocks 18-19 re-load block 0 into the spare area so every wave issues
-// exactly kDmaPerWave instructions. Which kind an instruction is depends only on (i, wave), so
-// the branch on it is scalar. DmaPlan holds this lane's byte offset for each instruction from the
-// block's first key row of K or V^T, in 32 bits (the launcher checks that one (b, h) slice spans
-// fewer than 2^31 elements); a block's DMA then needs only its two scalar base addresses.
-struct DmaPlan {
-    uint32_t off[kDmaPerWave];
-};
-
-__device__ __forceinline__ bool dma_is_v(int i, int wave) {
-    const int item = i * kDmaWaves + wave;
-    return item >= 9 && item < 18;
-}
-__device__ __forceinline__ int dma_dst(int i, int wave) {
-    const int item = i * kDmaWaves + wave;
-    return item < 9 ? item * 1024 : item < 18 ? kKBytes + (item - 9) * 1024
-                                              : kKBytes + kVBytes + (item - 18) * 1024;
-}
-// K items: this lane's row within the block
-__device__ __forceinline__ int dma_krow(int i, int wave, int lane) {
-    const int item = i * kDmaWaves + wave;
-    return ((item < 9 ? item : 0) * 64 + lane) / 9;
-}
-
-__device__ __forceinline__ DmaPlan dma_plan(const Flash72Args& a, int wave, int lane) {
-    DmaPlan p;
-#pragma unroll
-    for (int i = 0; i < kDmaPerWave; ++i) {
-        const int item = i * kDmaWaves + wave;
-        if (dma_is_v(i, wave)) {
-            const int d = (item - 9) * 8 + (lane >> 3);
-            const int c = (lane & 7) ^ ((d >> 1) & 7);
-            p.off[i] = 2u * static_cast<uint32_t>(d * static_cast<int>(a.vt_ld) + c * 8);
-        } else {
-            const int lg = (item < 9 ? item : 0) * 64 + lane;   // spares (18, 19) re-load block 0
-            const int row = lg / 9, ch = lg - row * 9;
-            p.off[i] = 2u * static_cast<uint32_t>(row * static_cast<int>(a.ld_k) + ch * 8);
-        }
-    }
-    return p;
-}
-
-// Key block starting at key kv0 (wave-uniform) into `stage`. `partial`: the block runs past the
-// last key, whose row then stands in for the missing ones (their scores are masked).
-__device__ __forceinline__ void dma_block(char* stage, const Flash72Args& a, const DmaPlan& p,
-                                          const bf16_t* kbh, const bf16_t* vbh, int wave, int lane,
-                                          int kv0, bool partial) {
-    const bf16_t* kb = kbh + static_cast<int64_t>(kv0) * a.ld_k;
-    const bf16_t* vb = vbh + kv0;
-#pragma unroll
-    for (int i = 0; i < kDmaPerWave; ++i) {
-        char* dst = stage + dma_dst(i, wave);
-        if (dma_is_v(i, wave)) {
-            dma16s(p.off[i], vb, dst);
-        } else if (!partial) {
-            dma16s(p.off[i], kb, dst);
-        } else {
-            const int row = dma_krow(i, wave, lane);
-            const int key = min(kv0 + row, a.Skv - 1);   // from kb: key - kv0 - row <= 0 rows
-            dma16(kb + (static_cast<int>(p.off[i] / 2u) + (key - kv0 - row) * static_cast<int>(a.ld_k)), dst);
-        }
-    }
-}
-
-// DMA item `item` (0..19) of the key block at kv0 into `stage`, any wave: items 0..8 are K, 9..17
-// V^T, 18..19 spares (see dma_block). Used by the resident variant's one-time prologue.
-__device__ __forceinline__ void dma_item(char* stage, const Flash72Args& a, const bf16_t* kbh,
-                                         const bf16_t* vbh, int item, int lane, int kv0,
-                                         bool partial) {
-    const bf16_t* src;
-    int dst;
-    if (item >= 9 && item < 18) {
-        const int d = (item - 9) * 8 + (lane >> 3);
-        const int c = (lane & 7) ^ ((d >> 1) & 7);
-        src = vbh + (d * static_cast<int>(a.vt_ld) + c * 8 + kv0);
-        dst = kKBytes + (item - 9) * 1024;
-    } else {
-        const int lg = (item < 9 ? item : 0) * 64 + lane;
-        const int row = lg / 9, ch = lg - row * 9;
-        const int key = partial ? min(kv0 + row, a.Skv - 1) : kv0 + row;
-        src = kbh + (key * static_cast<int>(a.ld_k) + ch * 8);
-        dst = item < 9 ? item * 1024 : kKBytes + kVBytes + (item - 18) * 1024;
-    }
-    dma16(src, stage + dst);
-}
-
-// This file is compiled with -fno-honor-nans: with IEEE NaN rules the compiler would first quiet
-// every MFMA result with an extra v_max before each maximum. Scores here are finite, or -inf for
-// masked keys.
-__device__ __forceinline__ bf16x8_t ld_frag(const char* p) {
-    return *reinterpret_cast<const bf16x8_t*>(p);
-}
-
-// Per-wave state of the pipeline.
-typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16_t;
-
-struct WaveState {
-    bf16x8_t qf[kST][kSSteps]; // Q fragments: query 32 qt + l%32, dims 16 s + 8 h .. +7 (h = l/32);
-                               // lanes h = 1 of step 4 hold (-m, 0, ..., 0) for dims 72..79
-    f32x4_t o[5][kQT];         // O^T accumulators: rows 16e + 4g .. +3 (row 72 = denominator)
-    f32x16_t s[kSK][kST];      // S^T of the current block: element r is key 32 kt + 8 (r/4) + 4 h + r%4,
-                               // query 32 qt + l%32
-    bf16x8_t pf[kQT][2];       // P of the previous block, as the second product's B operand
-    float mc[kST];             // running maximum (scaled, log2 units, a bf16 value) of query 32 qt + l%32
-};
-
-// The matrix phase: O^T += V^T P^T for the block whose P is in w.pf (OUT: 40 MFMAs 16x16x32,
-// V^T from `vstage`), then the scores of the next block (SCORES: 20 MFMAs 32x32x16, K from
-// `kstage`) into w.s.
-//   output: for each V^T fragment (row block e, 32-key chunk cc), four MFMAs (query tiles u);
-//           `vbase[cc]`: this lane's byte offset of its V^T chunk at row block 0 (e adds 16 rows).
-//   scores: five K=16 steps over dims 0..79, step-outer so that four independent MFMAs separate
-//           the dependent ones. `kb[0]`: this lane's byte offset of its K chunk (row l%32, dims
-//           8h..8h+7) at key tile 0 and step 0 (key tile kt adds 32 rows, step s 32 bytes);
-//           `kb[1 + kt]`: the offset for step 4 -- dims 64..71 of its row for h = 0, the ones row
-//           (kOnesOff) for h = 1, which pairs with -m in Q's dim 72.
-// Fragments are read ahead of their MFMAs: V^T three fragments ahead, K two ahead, the first two
-// K fragments during the last output MFMAs. The sched_group_barrier sequence pins that order (left
-// alone, the scheduler sinks each read next to its first use and the wave waits out the LDS
-// latency in front of every group).
-constexpr int kVAhead = 3;   // V^T fragments read ahead of their MFMAs
-constexpr int kKAhead = 2;   // K fragments read ahead of their MFMAs
-template <bool OUT, bool SCORES>
-__device__ __forceinline__ void matrix_phase(WaveState& w, const char* vstage, const int (&vbase)[2],
-                                             const char* kstage, const int (&kb)[3]) {
-    constexpr int kVF = 10;                // V^T fragments (e, cc)
-    constexpr int kKF = kSSteps * kSK;     // K fragments in MFMA order: p = 2 s + kt
-    bf16x8_t vf[kVF];
-    bf16x8_t kf[kKF];
-    auto read_v = [&](int i) { vf[i] = ld_frag(vstage + vbase[i & 1] + (i >> 1) * 16 * 128); };
-    auto read_k = [&](int p) {
-        const int kt = p % kSK, st = p / kSK;
-        kf[p] = ld_frag(kstage + (st < kSSteps - 1 ? kb[0] + kt * 32 * kKRow + st * 32 : kb[1 + kt]));
-    };
-    if (OUT) {
-#pragma unroll
-        for (int i = 0; i < kVAhead; ++i) read_v(i);
-#pragma unroll
-        for (int i = 0; i < kVF; ++i) {
-#pragma unroll
-            for (int u = 0; u < kQT; ++u)
-                w.o[i >> 1][u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf[i], w.pf[u][i & 1], w.o[i >> 1][u], 0, 0, 0);
-            if (i + kVAhead < kVF) read_v(i + kVAhead);
-            else if (SCORES && i >= kVF - kKAhead) read_k(i - (kVF - kKAhead));
-        }
-    } else if (SCORES) {
-#pragma unroll
-        for (int p = 0; p < kKAhead; ++p) read_k(p);
-    }
-    if (SCORES) {
-        const f32x16_t zero = {};
-#pragma unroll
-        for (int p = 0; p < kKF; ++p) {
-            const int kt = p % kSK, st = p / kSK;
-#pragma unroll
-            for (int qt = 0; qt < kST; ++qt)
-                w.s[kt][qt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-                    kf[p], w.qf[qt][st], st == 0 ? zero : w.s[kt][qt], 0, 0, 0);
-            if (p + kKAhead < kKF) read_k(p + kKAhead);
-        }
-    }
-    // the issue order
-    if (OUT) {
-        __builtin_amdgcn_sched_group_barrier(0x100, kVAhead, 0);
-#pragma unroll
-        for (int i = 0; i < kVF; ++i) {
-            __builtin_amdgcn_sched_group_barrier(0x008, kQT, 0);
-            if (i + kVAhead < kVF || (SCORES && i >= kVF - kKAhead)) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-        }
-    } else if (SCORES) {
-        __builtin_amdgcn_sched_group_barrier(0x100, kKAhead, 0);
-    }
-    if (SCORES) {
-#pragma unroll
-        for (int p = 0; p < kKF; ++p) {
-            __builtin_amdgcn_sched_group_barrier(0x008, kST, 0);
-            if (p + kKAhead < kKF) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-        }
-    }
-}
-
-__device__ __forceinline__ float lane_max2(float m, bool swap32) {
-    const uint32_t x = __float_as_uint(m);
-    const auto r = swap32 ? __builtin_amdgcn_permlane32_swap(x, x, false, false)
-                          : __builtin_amdgcn_permlane16_swap(x, x, false, false);
-    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
-}
-
-// Maxima of the 32 scores this lane holds for each query tile qt (its query's keys 8j + 4h + i of
-// both key tiles): four chains of v_max3 (one per tile), each link taking two new values,
-// interleaved so that no link waits on the one before it (a dependent VALU operand needs two
-// instructions between producer and consumer here). The empty asm makes each link opaque:
-// otherwise the compiler, with NaNs ignored, rebalances the chains into trees of two-input maxima
-// (~50 instructions per 64 values instead of 34).
-__device__ __forceinline__ float max3_link(float m, float a, float b) {
-    m = __builtin_fmaxf(__builtin_fmaxf(m, a), b);
-    asm("" : "+v"(m));
-    return m;
-}
-__device__ __forceinline__ void tile_max(const WaveState& w, float (&tm)[kST]) {
-    float c[kSK][kST];
-#pragma unroll
-    for (int kt = 0; kt < kSK; ++kt)
-#pragma unroll
-        for (int qt = 0; qt < kST; ++qt) c[kt][qt] = max3_link(w.s[kt][qt][0], w.s[kt][qt][1], w.s[kt][qt][2]);
-#pragma unroll
-    for (int i = 3; i < 15; i += 2)
-#pragma unroll
-        for (int kt = 0; kt < kSK; ++kt)
-#pragma unroll
-            for (int qt = 0; qt < kST; ++qt) c[kt][qt] = max3_link(c[kt][qt], w.s[kt][qt][i], w.s[kt][qt][i + 1]);
-#pragma unroll
-    for (int qt = 0; qt < kST; ++qt)
-        tm[qt] = __builtin_fmaxf(__builtin_fmaxf(c[0][qt], w.s[0][qt][15]),
-                                 __builtin_fmaxf(c[1][qt], w.s[1][qt][15]));
-}
-
-// Q's dim 72 := -m (lanes h = 1 of the last K step; their dims 73..79 stay zero).
-__device__ __forceinline__ void set_neg_max(WaveState& w, int h) {
-#pragma unroll
-    for (int qt = 0; qt < kST; ++qt) {
-        bf16x8_t f = {};
-        f[0] = static_cast<__bf16>(-w.mc[qt]);   // exact: m is a bf16 value
-        if (h) w.qf[qt][kSSteps - 1] = f;
-    }
-}
-
-// The smallest bf16 value not below x (x finite or -inf). Applied to integers it gives integers:
-// below 256 every integer is a bf16 value, from 256 up every bf16 value is an integer.
-__device__ __forceinline__ float ceil_bf16(float x) {
-    const uint32_t t = __float_as_uint(x) & 0xffff0000u;
-    return __uint_as_float(__uint_as_float(t) < x ? t + 0x10000u : t);
-}
-
-// P in w.pf times a power of two, per query: pf[u] holds query 16 u + l%16 in every lane row, so
-// tile u takes the factor of the lane that holds that query in the score layout. Exact (the
-// factor is 2^-k) unless a product falls below the normal range.
-__device__ __forceinline__ void scale_p(bf16x8_t& f, float s) {
-    uint32_t x[4];
-    __builtin_memcpy(x, &f, sizeof x);
-#pragma unroll
-    for (int v = 0; v < 4; ++v) {
-        bf16x2_t p;
-        p[0] = static_cast<__bf16>(__uint_as_float(x[v] << 16) * s);
-        p[1] = static_cast<__bf16>(__uint_as_float(x[v] & 0xffff0000u) * s);
-        x[v] = __builtin_bit_cast(uint32_t, p);
-    }
-    __builtin_memcpy(&f, x, sizeof x);
-}
-
-// P = exp2(x) of the scores in w.s into w.pf. Element r = 4j + i of tile (kt, qt) is key
-// 32 kt + 8j + 4h + i. Pairs pk[2j + v] hold keys (8j + 4h + 2v, +1). X = pk[0..3] (j = 0, 1) and
-// Y = pk[4..7] (j = 2, 3); swapping X's odd lane rows with Y's even ones leaves in X queries
-// 32 qt + 0..15 and in Y queries 32 qt + 16..31, lane row r holding keys
-// 16 (r & 1) + 4 (r >> 1) + {0..3, 8..11}: the eight keys at V^T slots 8r..8r+7 of the chunk
-// (vt_pos).
-__device__ __forceinline__ void form_p(WaveState& w) {
-#pragma unroll
-    for (int qt = 0; qt < kST; ++qt)
-#pragma unroll
-        for (int kt = 0; kt < kSK; ++kt) {
-            uint32_t pk[8];
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-#pragma unroll
-                for (int v = 0; v < 2; ++v) {
-                    bf16x2_t p;   // v_cvt_pk_bf16_f32: round to nearest even (P is finite)
-                    p[0] = static_cast<__bf16>(__builtin_amdgcn_exp2f(w.s[kt][qt][4 * j + 2 * v]));
-                    p[1] = static_cast<__bf16>(__builtin_amdgcn_exp2f(w.s[kt][qt][4 * j + 2 * v + 1]));
-                    pk[2 * j + v] = __builtin_bit_cast(uint32_t, p);
-                }
-#pragma unroll
-            for (int v = 0; v < 4; ++v) {
-                const auto r = __builtin_amdgcn_permlane16_swap(pk[v], pk[4 + v], false, false);
-                pk[v] = r[0];
-                pk[4 + v] = r[1];
-            }
-            const uint4 x = make_uint4(pk[0], pk[1], pk[2], pk[3]);
-            const uint4 y = make_uint4(pk[4], pk[5], pk[6], pk[7]);
-            w.pf[2 * qt][kt] = *reinterpret_cast<const bf16x8_t*>(&x);
-            w.pf[2 * qt + 1][kt] = *reinterpret_cast<const bf16x8_t*>(&y);
-        }
-}
-
-// Softmax of the block whose scores are in w.s: masking, the block maximum (the 64 keys of a
-// query sit in lanes l and l ^ 32), P = exp2(s c - m) in bf16 regrouped into w.pf, the lazy
-// rescale. The running maximum m is an integer-valued bf16 number: -m in Q's dim 72 is exact and
-// a rescale moves it by an integer k, so a rescale multiplies P and O by 2^-k exactly, and P is
-// formed before the decision (the maximum and the exponentials interleave; the scores die as
-// they are used).
-template <bool MASKED, bool FIRST>
-__device__ __forceinline__ void softmax(WaveState& w, const Flash72Args& a, int blk,
-                                        unsigned long long bits_all, bool all_masked, int h) {
-    if (MASKED) {
-        const unsigned long long bits = bits_all >> (4 * h);
-        const unsigned long long inrange =
-            (blk * kKV + kKV <= a.Skv) ? ~0ull : (((1ull << (a.Skv - blk * kKV)) - 1ull) >> (4 * h));
-#pragma unroll
-        for (int kt = 0; kt < kSK; ++kt)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int bit = 32 * kt + 8 * (r >> 2) + (r & 3);
-                const bool ok = all_masked ? ((inrange >> bit) & 1ull) : ((bits >> bit) & 1ull);
-#pragma unroll
-                for (int qt = 0; qt < kST; ++qt) {
-                    const float v = all_masked ? 0.0f : w.s[kt][qt][r];
-                    w.s[kt][qt][r] = ok ? v : -INFINITY;
-                }
-            }
-    }
-    float tm[kST];
-    tile_max(w, tm);
-    if constexpr (FIRST) {
-        // The first block sets the maximum, per query over its 64 keys (lanes l, l ^ 32), rounded
-        // up to an integer-valued bf16 number; its scores were formed against m = 0, so x = s c - m
-        // is formed here (later blocks' scores arrive as s c - m from the matrix cores).
-#pragma unroll
-        for (int qt = 0; qt < kST; ++qt) w.mc[qt] = ceil_bf16(ceilf(lane_max2(tm[qt], true)));
-#pragma unroll
-        for (int kt = 0; kt < kSK; ++kt)
-#pragma unroll
-            for (int qt = 0; qt < kST; ++qt)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) w.s[kt][qt][r] -= w.mc[qt];
-        set_neg_max(w, h);
-        form_p(w);
-    } else {
-        // Later blocks move the maximum only when one of their scores exceeds it by more than
-        // the threshold: one maximum over this lane's 64 values and a wave vote decide; the exact
-        // per-query maxima (across lanes) are formed only then.
-        form_p(w);
-        if (__any(fmaxf(tm[0], tm[1]) > kRescaleThreshold)) {
-            const int lr = __lane_id() & 15;
-#pragma unroll
-            for (int qt = 0; qt < kST; ++qt) {
-                const float m = lane_max2(tm[qt], true);
-                // the query's new maximum, an integer-valued bf16 number not below the old one
-                const float mnew = ceil_bf16(w.mc[qt] + ceilf(fmaxf(m, 0.0f)));
-                const float alpha = __builtin_ldexpf(1.0f, -static_cast<int>(mnew - w.mc[qt]));
-                w.mc[qt] = mnew;
-                // O^T tile u = 2 qt + t and P tile u hold query 32 qt + 16 t + l%16
-#pragma unroll
-                for (int t = 0; t < 2; ++t) {
-                    const float au = __shfl(alpha, 16 * t + lr, 64);
-#pragma unroll
-                    for (int e = 0; e < 5; ++e)
-#pragma unroll
-                        for (int r = 0; r < 4; ++r) w.o[e][2 * qt + t][r] *= au;
-#pragma unroll
-                    for (int cc = 0; cc < 2; ++cc) scale_p(w.pf[2 * qt + t][cc], au);
-                }
-            }
-            set_neg_max(w, h);
-        }
-    }
-}
+#include "flash72_core.inc"
+using namespace fk;
 
 // RESIDENT (kv_len <= 448): every key block is loaded once, up front, into a stage of its own;
 // after one barrier each wave runs its blocks through without further synchronisation (the two

@@ -127,6 +127,38 @@ def test_packed_and_scattered_weights_agree(hip):
         scattered.close()
 
 
+def test_fused_cross_attention_equals_opwise_plan_1024px(hip):
+    # At 1024px the fused plan runs each block's cross-attention Q projection and attention as one
+    # kernel (cross_fused.hip); it must equal the op-by-op plan's GEMM + attention bit for bit:
+    # with the workload's prefix masks (2 and 3 live key blocks of 5), with every key live (5
+    # blocks: two resident chunks per head) and with every key masked (the uniform average).
+    import torch
+    wl = make_workload(PIXART_SIGMA, batch=2, latent_hw=128, caption_len=300, layers=2)
+    a, b = Engine(wl, 0), Engine(wl, 1)
+    try:
+        for name, mask in (("prefix", None), ("all live", torch.ones_like(a.mask)),
+                           ("all masked", torch.zeros_like(a.mask))):
+            print(f"cross-attention mask: {name}", flush=True)
+            assert np.array_equal(a.forward(mask=mask), b.forward(mask=mask)), name
+    finally:
+        a.close()
+        b.close()
+
+
+def test_row_schedules_are_bit_identical_1024px(hip):
+    # The joined schedule runs the fused cross-attention kernel over both rows; each row of the
+    # split schedule is too few tiles for it and runs the GEMM and the attention kernel.
+    import burnisher_amd as bh
+    wl = make_workload(PIXART_SIGMA, batch=2, latent_hw=128, caption_len=300, layers=2)
+    e = Engine(wl, 0)
+    try:
+        joined = e.forward()
+        bh.call("bh_dit_set_rows", e.handle, bh.ROWS_SPLIT)
+        assert np.array_equal(e.forward(), joined)
+    finally:
+        e.close()
+
+
 def test_fused_plan_equals_opwise_plan(hip):
     # Fusion moves no rounding point, so the two plans agree bit for bit.
     wl = make_workload(PIXART_SIGMA, batch=2, latent_hw=64, caption_len=300, layers=2)
