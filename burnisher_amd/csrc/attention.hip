@@ -487,8 +487,8 @@ int64_t attention_part_floats(const bf16_t* q, const bf16_t* k, const bf16_t* v,
                               const AttnShape& sh, const void* key_mask, const bf16_t* bias) {
     if (sh.batch * sh.heads * sh.q_len == 0) return 0;
     if (plan_attention(q, k, v, out, sh, key_mask, bias).kind != AttnPlan::FLASH72) return 0;
-    const int splits = flash72_splits(sh.batch, sh.heads, sh.q_len, sh.kv_len, out, sh.ld_o);
-    return flash72_part_floats(sh.batch, sh.heads, sh.q_len, splits);
+    return flash72_plan_floats(sh.batch, sh.heads, sh.q_len,
+                               flash72_plan(sh.batch, sh.heads, sh.q_len, sh.kv_len, out, sh.ld_o));
 }
 
 bf16_t* noalloc_scratch() {
@@ -510,7 +510,7 @@ bf16_t* noalloc_scratch() {
 void launch_attention_bf16(const bf16_t* q, const bf16_t* k, const bf16_t* v, bf16_t* out,
                            const AttnShape& sh, const void* key_mask, bool mask_f32,
                            hipStream_t s, const bf16_t* bias, bf16_t* vt_buf, int64_t vt_buf_elems,
-                           int splits, float* part, int64_t part_floats) {
+                           int splits, float* part, int64_t part_floats, int qb0) {
     if (sh.batch * sh.heads * sh.q_len == 0) return;
     const AttnPlan plan = plan_attention(q, k, v, out, sh, key_mask, bias);
     // V^T goes to the caller's buffer when one is given (it must be large enough), else to the
@@ -535,7 +535,7 @@ void launch_attention_bf16(const bf16_t* q, const bf16_t* k, const bf16_t* v, bf
         launch_transpose_v72(v, sh.ld_kv, sh.batch, sh.heads, sh.kv_len, vt, vt_ld, s);
         launch_flash72(q, sh.ld_q, k, sh.ld_kv, vt, vt_ld, out, sh.ld_o, sh.batch, sh.heads,
                        sh.q_len, sh.kv_len, sh.scale, key_mask, mask_f32, s, splits, part,
-                       part_floats);
+                       part_floats, qb0);
         return;
     }
     require(sh.kv_len > 0, "attention: kv_len must be positive");

@@ -332,13 +332,13 @@ struct AttnShape {
 // The head_dim-72 and -512 kernels read V transposed: into `vt_buf` (vt_buf_elems elements, at
 // least attention_vt_elems of the call, else an error) when given, else into a per-device
 // workspace that grows on demand and that calls overlapping on one device share.
-// `splits`, `part`, `part_floats`: the head_dim-72 kernel's key splits and their fp32 partials,
-// as launch_flash72 takes them (other kernels ignore them).
+// `splits`, `part`, `part_floats`, `qb0`: the head_dim-72 kernel's key splits and their fp32
+// partials, as launch_flash72 takes them (other kernels ignore them).
 void launch_attention_bf16(const bf16_t* q, const bf16_t* k, const bf16_t* v, bf16_t* out,
                            const AttnShape& sh, const void* key_mask, bool mask_f32,
                            hipStream_t s, const bf16_t* bias = nullptr, bf16_t* vt_buf = nullptr,
                            int64_t vt_buf_elems = 0, int splits = 0, float* part = nullptr,
-                           int64_t part_floats = 0);
+                           int64_t part_floats = 0, int qb0 = 0);
 // The V^T elements launch_attention_bf16 needs for these operands (0: the kernel reads V as is).
 int64_t attention_vt_elems(const bf16_t* q, const bf16_t* k, const bf16_t* v, const bf16_t* out,
                            const AttnShape& sh, const void* key_mask, const bf16_t* bias);
@@ -354,14 +354,15 @@ bf16_t* noalloc_scratch();
 // Flash attention at head_dim 72 with V supplied transposed (flash72.hip): vt holds, for each
 // (b, h, d), a row of vt_ld >= flash72_vt_ld(kv_len) keys, zero past kv_len.
 int64_t flash72_vt_ld(int64_t kv_len);
-// `splits`: key splits (0: flash72_splits decides, 1: none). A split launch writes fp32
-// partials to `part` (part_floats floats, at least flash72_part_floats) or, when it is null, to a
-// per-device library buffer grown on demand, and a second kernel combines them into `out`.
+// `splits`: key splits (0: flash72_plan decides, 1: none), for query blocks qb0 and up (the ones
+// below run whole). A split launch writes fp32 partials to `part` (part_floats floats, at least
+// flash72_plan_floats) or, when it is null, to a per-device library buffer grown on demand, and a
+// last kernel combines them into `out`.
 void launch_flash72(const bf16_t* q, int64_t ld_q, const bf16_t* k, int64_t ld_k,
                     const bf16_t* vt, int64_t vt_ld, bf16_t* out, int64_t ld_o, int64_t batch,
                     int64_t heads, int64_t q_len, int64_t kv_len, float scale,
                     const void* key_mask, bool mask_f32, hipStream_t s, int splits = 0,
-                    float* part = nullptr, int64_t part_floats = 0);
+                    float* part = nullptr, int64_t part_floats = 0, int qb0 = 0);
 // Key splits for a head_dim-72 attention whose workgroups (512 queries of one batch row and head
 // each) would fill at most half the CUs: as many as still fit at once, at least two key blocks
 // each; 1 for the resident (kv_len <= 448) kernel and for an output whose rows are not 16-byte
@@ -379,6 +380,16 @@ void launch_cross_fused(const bf16_t* x, const bf16_t* wq, const bf16_t* bq, int
 int flash72_splits(int64_t batch, int64_t heads, int64_t q_len, int64_t kv_len,
                    const void* out = nullptr, int64_t ld_o = 8);
 int64_t flash72_part_floats(int64_t batch, int64_t heads, int64_t q_len, int splits);
+// The key splits launch_flash72 picks with splits = 0: `splits` ways for the query blocks from
+// qb0 on (all of them when qb0 == 0), query blocks below qb0 whole. Besides flash72_splits' case,
+// it splits the query blocks of a last, at most half-full round of workgroups (qb0 > 0).
+struct Flash72Plan {
+    int splits;
+    int qb0;
+};
+Flash72Plan flash72_plan(int64_t batch, int64_t heads, int64_t q_len, int64_t kv_len,
+                         const void* out = nullptr, int64_t ld_o = 8);
+int64_t flash72_plan_floats(int64_t batch, int64_t heads, int64_t q_len, const Flash72Plan& p);
 // V [batch, kv_len, ld_v] (head-last, head_dim 72) -> the V^T rows launch_flash72 reads.
 void launch_transpose_v72(const bf16_t* v, int64_t ld_v, int64_t batch, int64_t heads,
                           int64_t kv_len, bf16_t* vt, int64_t vt_ld, hipStream_t s);

@@ -140,7 +140,7 @@ struct bh_dit {
     hipEvent_t fork_ev = nullptr, join_ev = nullptr;
     DevBuf splitk;                    // fp32 split-K partials of the fused plan's long-K GEMMs
     int64_t splitk_floats = 0;
-    int splits_self = 1, splits_cross = 1;   // key splits of the head_dim-72 attentions (full batch)
+    Flash72Plan plan_self{1, 0}, plan_cross{1, 0};   // key splits of the head_dim-72 attentions (full batch)
     DevBuf attn_part;                 // their fp32 partials, a row group's slice at its batch offset
 
     ~bh_dit() {
@@ -298,13 +298,13 @@ void gemm(bh_dit& e, const bf16_t* a, const void* w, const void* b, bf16_t* out,
 // the engine's buffer at that row group's offset (null when the attention does not split). The
 // splits are fixed at create on the full batch, so row groups and the joined batch agree bit for
 // bit and a captured forward holds no library-owned pointer.
-float* attn_part(bh_dit& e, int splits, int64_t b0, int64_t nb, int64_t q_len) {
-    if (splits <= 1) return nullptr;
+float* attn_part(bh_dit& e, const Flash72Plan& plan, int64_t b0, int64_t nb, int64_t q_len) {
+    if (plan.splits <= 1) return nullptr;
     const int64_t heads = e.cfg.num_heads;
     require(e.attn_part.p != nullptr &&
-                flash72_part_floats(b0 + nb, heads, q_len, splits) * sizeof(float) <= e.attn_part.bytes,
+                flash72_plan_floats(b0 + nb, heads, q_len, plan) * sizeof(float) <= e.attn_part.bytes,
             "dit: the engine's attention partial buffer is smaller than this call needs");
-    return static_cast<float*>(e.attn_part.p) + flash72_part_floats(b0, heads, q_len, splits);
+    return static_cast<float*>(e.attn_part.p) + flash72_plan_floats(b0, heads, q_len, plan);
 }
 
 // The MI355X plan.
@@ -424,18 +424,18 @@ void forward_fused(bh_dit& e, const void* latent, double t, const void* caption,
     auto self_attention = [&](const Rows& g) {
         const bf16_t* q = e.qkv.bf() + g.b0 * N * qkv_ld;
         bf16_t* ctx = e.ctx.bf() + g.b0 * N * d;
-        const int sp = e.splits_self;
+        const Flash72Plan& sp = e.plan_self;
         float* part = attn_part(e, sp, g.b0, g.nb, N);
-        const int64_t pf = flash72_part_floats(g.nb, H, N, sp);
+        const int64_t pf = flash72_plan_floats(g.nb, H, N, sp);
         if (e.vt72) {
             launch_flash72(q, qkv_ld, q + d, qkv_ld, e.vt_self.bf() + g.b0 * H * Dh * e.vt_ld_self,
-                           e.vt_ld_self, ctx, d, g.nb, H, N, N, scale, nullptr, false, g.s, sp,
-                           part, pf);
+                           e.vt_ld_self, ctx, d, g.nb, H, N, N, scale, nullptr, false, g.s, sp.splits,
+                           part, pf, sp.qb0);
         } else {
             const int64_t vo = vt_op_offset(g, N);
             launch_attention_bf16(q, q + d, q + 2 * d, ctx, AttnShape{g.nb, H, N, N, Dh, 3 * d, 3 * d, d, scale},
-                                  nullptr, false, g.s, nullptr, e.vt_op.bf() + vo, e.vt_op_elems - vo, sp,
-                                  part, pf);
+                                  nullptr, false, g.s, nullptr, e.vt_op.bf() + vo, e.vt_op_elems - vo,
+                                  sp.splits, part, pf, sp.qb0);
         }
     };
     // 1c-3. the gated out-projection, the cross-attention block and the feed-forward block
@@ -456,9 +456,9 @@ void forward_fused(bh_dit& e, const void* latent, double t, const void* caption,
         // 2. cross-attention (no norm before it: pixart_dit.cpp:251-253)
         const bf16_t* kv = e.kv_all.bf() + g.b0 * e.cap_len * L * 2 * d + l * 2 * d;
         const void* m = static_cast<const char*>(mask) + g.b0 * e.cap_len * mask_elem;
-        const int sp = e.splits_cross;
+        const Flash72Plan& sp = e.plan_cross;
         float* part = attn_part(e, sp, g.b0, g.nb, N);
-        const int64_t pf = flash72_part_floats(g.nb, H, N, sp);
+        const int64_t pf = flash72_plan_floats(g.nb, H, N, sp);
         if (e.cross_fused && g.nb >= e.cross_fused_min_rows) {
             // the Q projection and the attention in one launch, bit-identical with the two below
             launch_cross_fused(x, static_cast<const bf16_t*>(bw.attn2_q_w),
@@ -471,13 +471,14 @@ void forward_fused(bh_dit& e, const void* latent, double t, const void* caption,
             if (e.vt72) {
                 launch_flash72(q2, d, kv, L * 2 * d,
                                e.vt_cross.bf() + (l * B + g.b0) * H * Dh * e.vt_ld_cross, e.vt_ld_cross,
-                               ctx, d, g.nb, H, N, e.cap_len, scale, m, mask_f32, g.s, sp, part, pf);
+                               ctx, d, g.nb, H, N, e.cap_len, scale, m, mask_f32, g.s, sp.splits, part,
+                               pf, sp.qb0);
             } else {
                 const int64_t vo = vt_op_offset(g, e.cap_len);
                 launch_attention_bf16(q2, kv, kv + d, ctx,
                                       AttnShape{g.nb, H, N, e.cap_len, Dh, d, L * 2 * d, d, scale}, m,
-                                      mask_f32, g.s, nullptr, e.vt_op.bf() + vo, e.vt_op_elems - vo, sp,
-                                      part, pf);
+                                      mask_f32, g.s, nullptr, e.vt_op.bf() + vo, e.vt_op_elems - vo,
+                                      sp.splits, part, pf, sp.qb0);
             }
         }
         {
@@ -728,10 +729,10 @@ int bh_dit_create(const bh_dit_config* cfg, const bh_dit_weights* w, int64_t bat
             }
             if (c.head_dim == 72) {   // key splits of the attentions, decided on the full batch
                 const int64_t H = c.num_heads;
-                e->splits_self = flash72_splits(B, H, e->N, e->N);
-                e->splits_cross = flash72_splits(B, H, e->N, caption_len);
-                const int64_t floats = std::max(flash72_part_floats(B, H, e->N, e->splits_self),
-                                                flash72_part_floats(B, H, e->N, e->splits_cross));
+                e->plan_self = flash72_plan(B, H, e->N, e->N);
+                e->plan_cross = flash72_plan(B, H, e->N, caption_len);
+                const int64_t floats = std::max(flash72_plan_floats(B, H, e->N, e->plan_self),
+                                                flash72_plan_floats(B, H, e->N, e->plan_cross));
                 if (floats > 0) e->attn_part = e->make_f32(floats);
             }
             if (batch >= 2) {   // the row-split schedule's second stream (default priority)

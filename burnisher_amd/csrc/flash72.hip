@@ -106,7 +106,7 @@ __global__ void __launch_bounds__(WAVES * 64, 1) k_flash72(Flash72Args a) {
         h = bh - b * a.H;
         qblk = bid - bh * a.qblocks;
     }
-    const int q_base = qblk * (WAVES * kQPerWave) + wave * kQPerWave;
+    const int q_base = (a.qb0 + qblk) * (WAVES * kQPerWave) + wave * kQPerWave;
     const int nblk = (a.Skv + kKV - 1) / kKV;
     const int kb0 = SPLIT ? split * nblk / splits : 0;
     const int kb1 = SPLIT ? (split + 1) * nblk / splits : nblk;
@@ -300,8 +300,9 @@ __global__ void __launch_bounds__(WAVES * 64, 1) k_flash72(Flash72Args a) {
         for (int u = 0; u < kQT; ++u) {
             const int q = q_base + u * 16 + lr;
             if (q >= a.Sq) continue;
-            float* dst = a.part + ((static_cast<int64_t>(split) * a.B + b) * a.H + h) * a.Sq * 80 +
-                         static_cast<int64_t>(q) * 80;
+            const int q0 = a.qb0 * kQPerWg;
+            float* dst = a.part + ((static_cast<int64_t>(split) * a.B + b) * a.H + h) * (a.Sq - q0) * 80 +
+                         static_cast<int64_t>(q - q0) * 80;
 #pragma unroll
             for (int e = 0; e < 5; ++e) {
                 const int d = e * 16 + g * 4;
@@ -365,15 +366,17 @@ __global__ void __launch_bounds__(256) k_transpose_v72(const bf16_t* __restrict_
 
 // The key splits' partials into the output: per (b, h, q), M = the largest running maximum,
 // out = sum_s O_s 2^(m_s - M) / sum_s l_s 2^(m_s - M), in split order. One thread per 8 dims.
+// The partials cover queries q0 .. Sq - 1 of every (b, h).
 __global__ void __launch_bounds__(256) k_flash72_combine(const float* __restrict__ part, int splits,
-                                                         int B, int H, int Sq, bf16_t* out,
+                                                         int B, int H, int Sq, int q0, bf16_t* out,
                                                          int64_t ld_o) {
     constexpr int kChunks = D / 8;   // 9
-    const int64_t rows = static_cast<int64_t>(B) * H * Sq;
+    const int Sp = Sq - q0;
+    const int64_t rows = static_cast<int64_t>(B) * H * Sp;
     const int64_t split_stride = rows * 80;
     for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < rows * kChunks;
          i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-        const int64_t row = i / kChunks;   // ((b * H + h) * Sq + q)
+        const int64_t row = i / kChunks;   // ((b * H + h) * Sp + q - q0)
         const int c = static_cast<int>(i - row * kChunks);
         const float* p = part + row * 80;
         float mx = -INFINITY;
@@ -395,7 +398,7 @@ __global__ void __launch_bounds__(256) k_flash72_combine(const float* __restrict
         float v[8];
 #pragma unroll
         for (int r = 0; r < 8; ++r) v[r] = o[r] * rl;
-        const int64_t q = row % Sq, bh = row / Sq;
+        const int64_t q = q0 + row % Sp, bh = row / Sp;
         const int64_t b = bh / H, h = bh - b * H;
         uint32_t wv[4];
 #pragma unroll
@@ -464,6 +467,39 @@ int64_t flash72_part_floats(int64_t batch, int64_t heads, int64_t q_len, int spl
     return splits > 1 ? static_cast<int64_t>(splits) * batch * heads * q_len * 80 : 0;
 }
 
+// A grid of W = batch x heads x query blocks whole workgroups over C CUs runs ceil(W / C) rounds;
+// when the last one is at most half full (1152px: 352 workgroups, a last round of 96), the query
+// blocks past the whole rounds split their keys instead, as many ways as still fit in one round,
+// so that round takes a fraction of a query block's time. The blocks of the whole rounds stay
+// unsplit: query blocks qb0 and up of every (b, h) are split, qb0 = whole rounds x C / (b x h).
+Flash72Plan flash72_plan(int64_t batch, int64_t heads, int64_t q_len, int64_t kv_len,
+                         const void* out, int64_t ld_o) {
+    const int sp = flash72_splits(batch, heads, q_len, kv_len, out, ld_o);
+    if (sp > 1) return {sp, 0};
+    if (kv_len <= kResidentBlocks * kKV) return {1, 0};
+    if (ld_o % 8 != 0 || reinterpret_cast<uintptr_t>(out) % 16 != 0) return {1, 0};
+    int cus = 0, dev = 0;
+    hip_check(hipGetDevice(&dev), "hipGetDevice");
+    hip_check(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev), "hipDeviceGetAttribute");
+    const int64_t bh = batch * heads;
+    const int64_t qblocks = (q_len + kQPerWg - 1) / kQPerWg;
+    const int64_t wgs = bh * qblocks;
+    const int64_t rounds = wgs / cus;
+    if (rounds == 0 || wgs % cus == 0 || (wgs % cus) * 2 > cus) return {1, 0};
+    const int64_t qb0 = rounds * cus / bh;
+    const int64_t tail = bh * (qblocks - qb0);
+    const int64_t nblk = (kv_len + kKV - 1) / kKV;
+    int best = 1;
+    for (int s2 = 2; s2 <= 8; ++s2)
+        if (tail * s2 <= cus && nblk >= 2 * s2) best = s2;
+    if (best == 1 || qb0 <= 0 || qb0 >= qblocks) return {1, 0};
+    return {best, static_cast<int>(qb0)};
+}
+
+int64_t flash72_plan_floats(int64_t batch, int64_t heads, int64_t q_len, const Flash72Plan& p) {
+    return flash72_part_floats(batch, heads, q_len - static_cast<int64_t>(p.qb0) * kQPerWg, p.splits);
+}
+
 // The same with 16-byte accesses (V and V^T 16-byte aligned, ld_v % 8 == 0, vt_ld % 64 == 0):
 // a thread loads 8 dims of one key, then stores the 8 keys of one dim that sit at V^T slots
 // 8q..8q+7 of the block. Those are two runs of four keys (vt_pos keeps runs of four):
@@ -521,7 +557,7 @@ void launch_flash72(const bf16_t* q, int64_t ld_q, const bf16_t* k, int64_t ld_k
                     const bf16_t* vt, int64_t vt_ld, bf16_t* out, int64_t ld_o, int64_t batch,
                     int64_t heads, int64_t q_len, int64_t kv_len, float scale,
                     const void* key_mask, bool mask_f32, hipStream_t s, int splits,
-                    float* part, int64_t part_floats) {
+                    float* part, int64_t part_floats, int qb0) {
     if (batch * heads * q_len == 0) return;
     require(kv_len > 0, "attention: kv_len must be positive");
     require(kv_len <= kMaxBlocks * kKV, "attention (head_dim 72): kv_len above 16384");
@@ -559,13 +595,20 @@ void launch_flash72(const bf16_t* q, int64_t ld_q, const bf16_t* k, int64_t ld_k
         while (waves > 1 && wgs(waves) < cus) waves /= 2;
     }
     a.qblocks = static_cast<int>((q_len + waves * kQPerWave - 1) / (waves * kQPerWave));
-    if (splits <= 0) splits = flash72_splits(batch, heads, q_len, kv_len, out, ld_o);
+    if (splits <= 0) {
+        const Flash72Plan p = flash72_plan(batch, heads, q_len, kv_len, out, ld_o);
+        splits = p.splits;
+        qb0 = p.qb0;
+    }
     const int64_t nblk = (kv_len + kKV - 1) / kKV;
     require(splits >= 1 && splits <= 8 && (splits == 1 || (!resident && nblk >= splits)),
             "attention (head_dim 72): " + std::to_string(splits) + " key splits of " +
                 std::to_string(nblk) + " key blocks");
+    require(qb0 >= 0 && (qb0 == 0 || (splits > 1 && qb0 < a.qblocks)),
+            "attention (head_dim 72): key splits from query block " + std::to_string(qb0) + " of " +
+                std::to_string(a.qblocks));
     if (splits > 1) {
-        const int64_t floats = flash72_part_floats(batch, heads, q_len, splits);
+        const int64_t floats = flash72_plan_floats(batch, heads, q_len, Flash72Plan{splits, qb0});
         if (part) {
             require(part_floats >= floats && reinterpret_cast<uintptr_t>(part) % 16 == 0,
                     "attention (head_dim 72): the partial buffer holds " + std::to_string(part_floats) +
@@ -578,9 +621,21 @@ void launch_flash72(const bf16_t* q, int64_t ld_q, const bf16_t* k, int64_t ld_k
         a.splits = splits;
         a.part = part;
     }
-    const int grid = a.B * a.H * a.qblocks * a.splits;
     const double flops = 4.0 * batch * heads * static_cast<double>(q_len) * kv_len * D;
     ProfileScope ps(q_len == kv_len ? K_ATTN_SELF : K_ATTN_CROSS, s, flops);
+    if (qb0 > 0) {   // query blocks below qb0 whole, then the rest split over keys
+        Flash72Args w = a;
+        w.qblocks = qb0;
+        w.splits = 1;
+        w.part = nullptr;
+        const int grid0 = w.B * w.H * w.qblocks;
+        if (masked) k_flash72<true, false, false><<<grid0, kThreads, 0, s>>>(w);
+        else k_flash72<false, false, false><<<grid0, kThreads, 0, s>>>(w);
+        launch_check("attention (flash, head_dim 72)");
+        a.qb0 = qb0;
+        a.qblocks -= qb0;
+    }
+    const int grid = a.B * a.H * a.qblocks * a.splits;
     if (a.splits > 1 && masked) k_flash72<true, false, true><<<grid, kThreads, 0, s>>>(a);
     else if (a.splits > 1) k_flash72<false, false, true><<<grid, kThreads, 0, s>>>(a);
     else if (resident) launch_resident(masked, waves, grid, a, s);
@@ -588,9 +643,10 @@ void launch_flash72(const bf16_t* q, int64_t ld_q, const bf16_t* k, int64_t ld_k
     else k_flash72<false, false, false><<<grid, kThreads, 0, s>>>(a);
     launch_check("attention (flash, head_dim 72)");
     if (a.splits > 1) {
-        const int64_t threads = batch * heads * q_len * (D / 8);
+        const int q0 = a.qb0 * kQPerWg;
+        const int64_t threads = batch * heads * (q_len - q0) * (D / 8);
         k_flash72_combine<<<static_cast<int>(std::min<int64_t>((threads + 255) / 256, 8192)), 256, 0, s>>>(
-            a.part, a.splits, a.B, a.H, a.Sq, out, ld_o);
+            a.part, a.splits, a.B, a.H, a.Sq, q0, out, ld_o);
         launch_check("attention (head_dim 72, key-split combine)");
     }
 }

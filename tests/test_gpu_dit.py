@@ -174,7 +174,8 @@ def test_fused_plan_equals_opwise_plan(hip):
     (PIXART_SIGMA, 2, 64, 300, 2),   # the CFG pair at 512px: one row per stream, head_dim 72
     (SMALL, 3, 8, 5, None),          # groups of two rows and one, the generic attention
     (ODD72, 2, 16, 20, None),        # head_dim 72, V transposed per row group by the attention op
-], ids=["512px_b2", "small_b3", "odd72_b2"])
+    (PIXART_SIGMA, 2, 144, 128, 1),  # 1152px: the self-attention's last-round query blocks split
+], ids=["512px_b2", "small_b3", "odd72_b2", "1152px_b2"])
 def test_row_schedules_are_bit_identical(hip, cfg, batch, hw, cap, layers):
     # Rows never mix, so running the two row groups on two streams changes no bit of the output,
     # forward after forward.

@@ -128,3 +128,34 @@ def test_attention_1024px_shapes(hip, cross):
     print(s, "worst head", (b, h), ws)
     assert ws["max_abs"] <= tol["max_abs"] and ws["rel_l2"] <= tol["rel_l2"] and ws["cosine"] >= tol["cosine"], \
         f"head {(b, h)}: {ws} vs {tol}"
+
+
+def test_attention_1152px_self_ragged_round(hip):
+    # The held-out 1152px self-attention: 2 x 16 heads x 11 query blocks = 352 workgroups on the
+    # 256 CUs. Query blocks 0-7 of every head run whole, blocks 8-10 (the last one 64 queries)
+    # split their 81 key blocks two ways and are combined: every path of that plan is held to
+    # the gate, per head too.
+    import burnisher_amd as bh
+    import torch
+    B, S2 = 2, 5184
+    q = randn_bf16(RNG, (B, S2, H, DH))
+    k = randn_bf16(RNG, (B, S2, H, DH))
+    v = randn_bf16(RNG, (B, S2, H, DH))
+    want = np.zeros((B, S2, H, DH), np.uint16)
+    st("stock_attention", addr(q), addr(k), addr(v), addr(want), B, H, S2, S2, DH, 0.0, None,
+       None, F32, BF16, 0, 0)
+    dq, dk, dv = dev(q), dev(k), dev(v)   # held: a freed operand's memory could be reused
+    out = torch.zeros((B, S2, H, DH), dtype=torch.bfloat16, device="cuda")
+    print(f"bh_attention B{B} H{H} {S2}x{S2} d{DH}", flush=True)
+    bh.call("bh_attention", dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), out.data_ptr(), B, H,
+            S2, S2, DH, 0.0, None, None, F32, BF16, None)
+    got = back(out)
+    s = assert_within(from_bf16(got), from_bf16(want), "attention", f"{S2}x{S2}")
+    (b, h), ws = per_head_worst(got, want, B, S2)
+    tol = TOLERANCE["ops"]["attention"]
+    print(s, "worst head", (b, h), ws)
+    assert ws["max_abs"] <= tol["max_abs"] and ws["rel_l2"] <= tol["rel_l2"] and ws["cosine"] >= tol["cosine"], \
+        f"head {(b, h)}: {ws} vs {tol}"
+    # the split query rows and the whole ones, each against the oracle on its own
+    for lo, hi in ((0, 8 * 512), (8 * 512, S2)):
+        assert_within(from_bf16(got[:, lo:hi]), from_bf16(want[:, lo:hi]), "attention", f"queries {lo}..{hi - 1}")
