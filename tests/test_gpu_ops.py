@@ -268,6 +268,20 @@ def test_attention_key_splits_masked(hip):
     assert_within(from_bf16(g), from_bf16(want), "attention", "key splits, ragged")
 
 
+def test_attention_ragged_last_round_masked(hip):
+    # 16 heads x 17 query blocks = 272 workgroups of 512 queries on 256 CUs: query blocks 0-15
+    # run whole and block 16 (508 queries) splits its 136 key blocks 8 ways. Masked: a key count
+    # that is not a multiple of 64 and holes, one of them covering whole splits.
+    B, S, KV, H, D = 1, 8700, 8699, 16, 72
+    mask = np.ones((B, KV), np.float32)
+    mask[0, 1000:3000] = 0.0
+    mask[0, 5000:8000:7] = 0.0
+    g, want = attention_case(B, S, KV, H, D, mask=mask)
+    assert_within(from_bf16(g), from_bf16(want), "attention", "ragged last round, masked")
+    lo = 16 * 512   # the split query block on its own
+    assert_within(from_bf16(g[:, lo:]), from_bf16(want[:, lo:]), "attention", "the split query block")
+
+
 def test_launch_profiler_sampling(hip):
     import ctypes
     # bh_profile_sample(3) brackets launches 0, 3 and 6 of seven; every launch after sample(1)
