@@ -174,30 +174,17 @@ __global__ void __launch_bounds__(256) k_gemm_fused_small(const bf16_t* __restri
     out[m * e.ld_out + n] = f2bf(finish(e, mode, act_exact(e.act, acc), m, n, N));
 }
 
-// Small K (the patch embedding's K = in_channels * patch^2 = 16): one thread per 8 consecutive
-// output columns of one row, the reference's sequential k order, 16-byte loads and stores. Needs
-// K % 8 == 0, N % 8 == 0 and 16-byte aligned operands.
-__global__ void __launch_bounds__(256) k_gemm_smallk(const bf16_t* __restrict__ A,
-                                                     const bf16_t* __restrict__ B, bf16_t* out,
-                                                     int M, int N, int K, Epi e, int mode) {
-    const int groups = N >> 3;
-    const int idx = blockIdx.x * blockDim.x + threadIdx.x;
-    if (idx >= M * groups) return;
-    const int m = idx / groups, n0 = (idx - m * groups) * 8;
-    float acc[8];
-#pragma unroll
-    for (int r = 0; r < 8; ++r) acc[r] = 0.f;
-    for (int k0 = 0; k0 < K; k0 += 8) {
-        float a[8];
-        unpack8(*reinterpret_cast<const uint4*>(A + static_cast<int64_t>(m) * K + k0), a);
-#pragma unroll
-        for (int r = 0; r < 8; ++r) {
-            float w[8];
-            unpack8(*reinterpret_cast<const uint4*>(B + static_cast<int64_t>(n0 + r) * K + k0), w);
-#pragma unroll
-            for (int t = 0; t < 8; ++t) acc[r] = __fadd_rn(acc[r], __fmul_rn(a[t], w[t]));
-        }
-    }
+// Small K (the patch embedding's K = in_channels * patch^2 = 16): each thread owns 8 consecutive
+// output columns and walks kSmallKRows consecutive rows with them, the reference's sequential k
+// order, 16-byte loads and stores. With K = 8 KC fixed (KC > 0) the thread's 8 x K weights are
+// read once into registers: the weight rows of neighbouring threads lie 8 rows apart, so every
+// 16-byte weight load touches a different cache line per lane, and reading them per output row
+// made the patch embedding (8192 x 1152 x 16) take ~47 us. KC = 0 is any K % 8 == 0 up to 256,
+// weights read per row. Needs N % 8 == 0 and 16-byte aligned operands.
+constexpr int kSmallKRows = 8;
+
+__device__ __forceinline__ void smallk_store(const Epi& e, int mode, const float (&acc)[8], int m,
+                                             int n0, int N, bf16_t* out) {
     float v[8], t[8];
     if (e.bias) {
         unpack8(*reinterpret_cast<const uint4*>(e.bias + n0), t);
@@ -232,6 +219,67 @@ __global__ void __launch_bounds__(256) k_gemm_smallk(const bf16_t* __restrict__ 
         }
     }
     *reinterpret_cast<uint4*>(out + static_cast<int64_t>(m) * e.ld_out + n0) = pack8(v);
+}
+
+template <int KC>
+__global__ void __launch_bounds__(256) k_gemm_smallk(const bf16_t* __restrict__ A,
+                                                     const bf16_t* __restrict__ B, bf16_t* out,
+                                                     int M, int N, int K, Epi e, int mode) {
+    const int groups = N >> 3;
+    const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+    const int band = idx / groups;
+    if (band >= (M + kSmallKRows - 1) / kSmallKRows) return;
+    const int n0 = (idx - band * groups) * 8;
+    const int m0 = band * kSmallKRows, m1 = min(M, m0 + kSmallKRows);
+    if constexpr (KC > 0) {
+        constexpr int kK = 8 * KC;
+        float w[8][kK];
+#pragma unroll
+        for (int r = 0; r < 8; ++r)
+#pragma unroll
+            for (int c = 0; c < KC; ++c) {
+                float f[8];
+                unpack8(*reinterpret_cast<const uint4*>(B + static_cast<int64_t>(n0 + r) * kK + 8 * c), f);
+#pragma unroll
+                for (int t = 0; t < 8; ++t) w[r][8 * c + t] = f[t];
+            }
+        for (int m = m0; m < m1; ++m) {
+            float a[kK];
+#pragma unroll
+            for (int c = 0; c < KC; ++c) {
+                float f[8];
+                unpack8(*reinterpret_cast<const uint4*>(A + static_cast<int64_t>(m) * kK + 8 * c), f);
+#pragma unroll
+                for (int t = 0; t < 8; ++t) a[8 * c + t] = f[t];
+            }
+            float acc[8];
+#pragma unroll
+            for (int r = 0; r < 8; ++r) {
+                acc[r] = 0.f;
+#pragma unroll
+                for (int t = 0; t < kK; ++t) acc[r] = __fadd_rn(acc[r], __fmul_rn(a[t], w[r][t]));
+            }
+            smallk_store(e, mode, acc, m, n0, N, out);
+        }
+    } else {
+        for (int m = m0; m < m1; ++m) {
+            float acc[8];
+#pragma unroll
+            for (int r = 0; r < 8; ++r) acc[r] = 0.f;
+            for (int k0 = 0; k0 < K; k0 += 8) {
+                float a[8];
+                unpack8(*reinterpret_cast<const uint4*>(A + static_cast<int64_t>(m) * K + k0), a);
+#pragma unroll
+                for (int r = 0; r < 8; ++r) {
+                    float w[8];
+                    unpack8(*reinterpret_cast<const uint4*>(B + static_cast<int64_t>(n0 + r) * K + k0), w);
+#pragma unroll
+                    for (int t = 0; t < 8; ++t) acc[r] = __fadd_rn(acc[r], __fmul_rn(a[t], w[t]));
+                }
+            }
+            smallk_store(e, mode, acc, m, n0, N, out);
+        }
+    }
 }
 
 // Compute units of the current device, looked up once per device.
@@ -493,9 +541,12 @@ void launch_gemm_bf16(const bf16_t* a, const bf16_t* b, const bf16_t* bias, bf16
     if (k8 && k % BK != 0 && vec && k <= 256 && m * (n / 8) < (int64_t{1} << 31) &&
         e.row_add_period < (int64_t{1} << 31) && e.gate_rows < (int64_t{1} << 31)) {
         ProfileScope ps(K_GEMM, s, flops);
-        const int64_t threads = m * (n / 8);
-        k_gemm_smallk<<<static_cast<int>((threads + 255) / 256), 256, 0, s>>>(
-            a, b, out, static_cast<int>(m), static_cast<int>(n), static_cast<int>(k), e, mode);
+        const int64_t threads = (m + kSmallKRows - 1) / kSmallKRows * (n / 8);
+        const int blocks = static_cast<int>((threads + 255) / 256);
+        const int mi = static_cast<int>(m), ni = static_cast<int>(n), ki = static_cast<int>(k);
+        if (k == 8) k_gemm_smallk<1><<<blocks, 256, 0, s>>>(a, b, out, mi, ni, ki, e, mode);
+        else if (k == 16) k_gemm_smallk<2><<<blocks, 256, 0, s>>>(a, b, out, mi, ni, ki, e, mode);
+        else k_gemm_smallk<0><<<blocks, 256, 0, s>>>(a, b, out, mi, ni, ki, e, mode);
         launch_check("gemm (small K)");
         return;
     }
