@@ -518,7 +518,8 @@ void launch_gemm_bf16(const bf16_t* a, const bf16_t* b, const bf16_t* bias, bf16
                     ep.vt_col0 < ep.vt_period && ep.vt_seq > 0 && m % ep.vt_seq == 0 &&
                     ep.vt_ld >= ep.vt_seq && ep.vt_heads > 0 && ep.vt_dim > 0 &&
                     ep.vt_dim == 72 && (ep.vt_period - ep.vt_col0) == int64_t{ep.vt_heads} * 72 &&
-                    ep.vt_ld % 32 == 0 && ep.vt_seq % 4 == 0 && aligned(ep.vt, 16),
+                    ep.vt_ld % 32 == 0 && ep.vt_seq % 4 == 0 && aligned(ep.vt, 16) &&
+                    m < (int64_t{1} << 31) && n < (int64_t{1} << 31),
                 "gemm: transposed V store geometry");
     }
     const int mode = ep.residual ? (ep.gate ? EPI_GATED : EPI_RESIDUAL)
