@@ -559,6 +559,10 @@ void launch_gemm_bf16(const bf16_t* a, const bf16_t* b, const bf16_t* bias, bf16
         launch_check("gemm (reference order, fused epilogue)");
         return;
     }
+    // the MFMA kernel's epilogues index rows, gate rows and row-add rows in 32 bits
+    require(m < (int64_t{1} << 31) && n < (int64_t{1} << 31) && e.gate_rows < (int64_t{1} << 31) &&
+                e.row_add_period < (int64_t{1} << 31),
+            "gemm: M, N, the gate's row count and the row-add period must be below 2^31");
     const int splits = ep.splitk > 0 ? ep.splitk : gemm_splits(m, n, k, ep);
     if (splits > 1) {
         require(k % (BK * splits) == 0 && !ep.vt && mode != EPI_ROW_ADD && splits <= 16,
