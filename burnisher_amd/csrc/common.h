@@ -433,11 +433,15 @@ void launch_chunk_all(const bf16_t* mod, const bf16_t* const* tables_dev, bf16_t
                       float* out_f32, int64_t layers, int64_t batch, int64_t channels,
                       hipStream_t s);
 // LayerNorm + modulate with float shift and 1 + scale rows ([batch, channels], as k_chunk_all
-// writes them); channels a multiple of 128, at most 4096.
+// writes them); channels a multiple of 128, at most 4096. `warm` (device memory, or null): the
+// kernel also reads 4 bytes of each 128-byte line of those `warm_bytes` (at most 8 KiB per row)
+// and discards them, so that the weights of the GEMM after the norm come from the memory-side
+// cache instead of HBM.
 bool norm_modulate_f32_supported(int64_t channels);
 void launch_norm_modulate_f32(const bf16_t* x, const float* shift, const float* scale1,
                               bf16_t* out, int64_t batch, int64_t tokens, int64_t channels,
-                              float eps, hipStream_t s);
+                              float eps, hipStream_t s, const void* warm = nullptr,
+                              int64_t warm_bytes = 0);
 void launch_patch(const void* in, void* out, int64_t batch, int64_t channels, int64_t grid,
                   int64_t patch, bool inverse, bool f32, hipStream_t s);
 // Cos-first sinusoidal timestep embedding, fp64, rounded to bf16, broadcast to `batch` rows

@@ -334,7 +334,8 @@ struct NormRow {
 template <int NV, int NP>
 __global__ void __launch_bounds__(256) k_norm_mod_dense(
     const bf16_t* __restrict__ x, const float* __restrict__ shift, const float* __restrict__ scale1,
-    bf16_t* __restrict__ out, int64_t rows, int64_t tokens, int cols, float eps) {
+    bf16_t* __restrict__ out, int64_t rows, int64_t tokens, int cols, float eps,
+    const uint32_t* __restrict__ warm, int64_t warm_lines) {
     using Row = NormRow<NV, NP>;
     constexpr int kE = Row::kE;
     constexpr int pair0 = NV * 8 * kWave;   // first channel of the pairs
@@ -373,6 +374,15 @@ __global__ void __launch_bounds__(256) k_norm_mod_dense(
             sh[8 * NV + 2 * p] = a.x; sh[8 * NV + 2 * p + 1] = a.y;
             sc[8 * NV + 2 * p] = m.x; sc[8 * NV + 2 * p + 1] = m.y;
         }
+        // The weights of the GEMM that reads this kernel's output: one 4-byte read per 128-byte
+        // line, so that they are in the memory-side cache when that GEMM starts instead of
+        // meeting it cold from HBM. Line lane * rows + row: the lines spread evenly over the
+        // rows (the first few lanes of every wave); lanes past the range all read its last line.
+        // Issued after the row, shift and scale loads (the scheduling barrier keeps it there), so
+        // no wait for them waits for it, and consumed only after the stores, so its latency hides
+        // under the statistics.
+        const uint32_t touched = warm[min(lane * rows + row, warm_lines - 1) * 32];
+        __builtin_amdgcn_sched_barrier(0);
         float v[kE];
 #pragma unroll
         for (int i = 0; i < kE / 2; ++i) {
@@ -416,6 +426,8 @@ __global__ void __launch_bounds__(256) k_norm_mod_dense(
 #pragma unroll
         for (int p = 0; p < NP; ++p)
             *reinterpret_cast<uint32_t*>(orow + pair0 + (p * kWave + lane) * 2) = o[4 * NV + p];
+        __builtin_amdgcn_sched_barrier(0);
+        asm volatile("" ::"v"(touched));
     }
 }
 
@@ -827,7 +839,7 @@ void launch_norm_modulate_pre(const bf16_t* x, const bf16_t* shift, const bf16_t
 
 void launch_norm_modulate_f32(const bf16_t* x, const float* shift, const float* scale1,
                               bf16_t* out, int64_t batch, int64_t tokens, int64_t channels,
-                              float eps, hipStream_t s) {
+                              float eps, hipStream_t s, const void* warm, int64_t warm_bytes) {
     const int64_t rows = batch * tokens;
     if (rows == 0) return;
     require(norm_modulate_f32_supported(channels),
@@ -838,8 +850,19 @@ void launch_norm_modulate_f32(const bf16_t* x, const float* shift, const float* 
     const int nv = static_cast<int>(channels / 512), np = static_cast<int>(channels % 512 / 128);
     const int grid = static_cast<int>((rows + 3) / 4);
     const int c = static_cast<int>(channels);
+    // the 128-byte lines the warm range touches (its first one starts at or before it, inside the
+    // same allocation, whose base is aligned further), at most one per lane of the launch; with
+    // no range, every lane reads the first 4 bytes of x (the kernel's read is unconditional)
+    const uintptr_t w0 = reinterpret_cast<uintptr_t>(warm) & ~uintptr_t{127};
+    const bool warm_ok = warm && warm_bytes > 0;
+    const int64_t warm_lines =
+        warm_ok ? std::min<int64_t>((reinterpret_cast<uintptr_t>(warm) + warm_bytes - w0 + 127) / 128,
+                                    rows * kWave)
+                : 1;
+    const uint32_t* wl = warm_ok ? reinterpret_cast<const uint32_t*>(w0) : reinterpret_cast<const uint32_t*>(x);
 #define BH_ND(NV, NP)                                                                         \
-    k_norm_mod_dense<NV, NP><<<grid, 256, 0, s>>>(x, shift, scale1, out, rows, tokens, c, eps)
+    k_norm_mod_dense<NV, NP><<<grid, 256, 0, s>>>(x, shift, scale1, out, rows, tokens, c, eps, \
+                                                  wl, warm_lines)
     switch (nv * 4 + np) {
 #define BH_NV(NV) \
         case NV * 4 + 0: BH_ND(NV, 0); break; \
