@@ -309,7 +309,7 @@ __global__ void __launch_bounds__(256) k_norm_modulate(
 // alone would leave three quarters of the lanes idle in the third vector). Shift and 1 + scale
 // arrive as floats (k_chunk_all), so per channel the output costs only the oracle's own
 // operations. One row per wave: all rows are in flight at once (a wave walking two rows with the
-// next one prefetched measured slower).
+// next one prefetched measured slower), which needs at most 64 VGPRs a wave.
 
 template <int NV, int NP>
 struct NormRow {
@@ -350,85 +350,88 @@ __global__ void __launch_bounds__(256) k_norm_mod_dense(
     if (row >= rows) return;
     Row cur;
     cur.load(x + row * cols, lane);
-    {
-        const int64_t b = static_cast<int>(row) / static_cast<int>(tokens);   // rows < 2^31
-        float sh[kE], sc[kE];
+    const int64_t b = static_cast<int>(row) / static_cast<int>(tokens);   // rows < 2^31
+    const float* shb = shift + b * cols;
+    const float* scb = scale1 + b * cols;
+    // The weights of the GEMM that reads this kernel's output: one 4-byte read per 128-byte line,
+    // so that they are in the memory-side cache when that GEMM starts instead of meeting it cold
+    // from HBM. Line lane * rows + row: the lines spread evenly over the rows (the first few lanes
+    // of every wave); lanes past the range all read its last line. Issued after the row load (the
+    // scheduling barrier keeps it there), so no wait for the row waits for it, and consumed only
+    // after the stores, so its latency hides under the statistics.
+    const uint32_t touched = warm[min(lane * rows + row, warm_lines - 1) * 32];
+    __builtin_amdgcn_sched_barrier(0);
+    // channel e of this lane, widened from the raw row where it is used (kept as bf16 pairs, the
+    // row costs kE / 2 registers: few registers per wave keep every row of a SIMD in flight at once)
+    auto val = [&](int e) -> float {
+        const uint32_t w = cur.raw[e >> 1];
+        return (e & 1) ? __uint_as_float(w & 0xffff0000u) : __uint_as_float(w << 16);
+    };
+    // The deviations' pass widens the row again: the empty asm makes the raw words opaque, so the
+    // compiler cannot keep the mean pass's 2 kE fp64 registers alive for it (63 instead of 85
+    // VGPRs at 1152 channels: eight waves per SIMD, every row of a SIMD in flight at once;
+    // making the output pass re-widen too saves registers the occupancy no longer needs and
+    // costs 18 instructions).
+    auto reload = [&]() {
 #pragma unroll
-        for (int j = 0; j < NV; ++j) {
+        for (int i = 0; i < kE / 2; ++i) asm volatile("" : "+v"(cur.raw[i]));
+    };
+    // statistics exactly as the oracle forms them: fp64 mean, fp64 sum of squared deviations
+    double sum = 0.0;
 #pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                const int c = (lane + j * kWave) * 8 + 4 * h;
-                const float4 a = *reinterpret_cast<const float4*>(shift + b * cols + c);
-                const float4 m = *reinterpret_cast<const float4*>(scale1 + b * cols + c);
-                sh[8 * j + 4 * h] = a.x; sh[8 * j + 4 * h + 1] = a.y;
-                sh[8 * j + 4 * h + 2] = a.z; sh[8 * j + 4 * h + 3] = a.w;
-                sc[8 * j + 4 * h] = m.x; sc[8 * j + 4 * h + 1] = m.y;
-                sc[8 * j + 4 * h + 2] = m.z; sc[8 * j + 4 * h + 3] = m.w;
-            }
-        }
+    for (int e = 0; e < kE; ++e) sum += static_cast<double>(val(e));
+    const double mean = wave_sum(sum) / static_cast<double>(cols);
+    reload();
+    double q = 0.0;
 #pragma unroll
-        for (int p = 0; p < NP; ++p) {
-            const int c = pair0 + (p * kWave + lane) * 2;
-            const float2 a = *reinterpret_cast<const float2*>(shift + b * cols + c);
-            const float2 m = *reinterpret_cast<const float2*>(scale1 + b * cols + c);
-            sh[8 * NV + 2 * p] = a.x; sh[8 * NV + 2 * p + 1] = a.y;
-            sc[8 * NV + 2 * p] = m.x; sc[8 * NV + 2 * p + 1] = m.y;
-        }
-        // The weights of the GEMM that reads this kernel's output: one 4-byte read per 128-byte
-        // line, so that they are in the memory-side cache when that GEMM starts instead of
-        // meeting it cold from HBM. Line lane * rows + row: the lines spread evenly over the
-        // rows (the first few lanes of every wave); lanes past the range all read its last line.
-        // Issued after the row, shift and scale loads (the scheduling barrier keeps it there), so
-        // no wait for them waits for it, and consumed only after the stores, so its latency hides
-        // under the statistics.
-        const uint32_t touched = warm[min(lane * rows + row, warm_lines - 1) * 32];
-        __builtin_amdgcn_sched_barrier(0);
-        float v[kE];
-#pragma unroll
-        for (int i = 0; i < kE / 2; ++i) {
-            v[2 * i] = __uint_as_float(cur.raw[i] << 16);
-            v[2 * i + 1] = __uint_as_float(cur.raw[i] & 0xffff0000u);
-        }
-        // statistics exactly as the oracle forms them: fp64 mean, fp64 sum of squared deviations
-        double sum = 0.0;
-#pragma unroll
-        for (int e = 0; e < kE; ++e) sum += static_cast<double>(v[e]);
-        const double mean = wave_sum(sum) / static_cast<double>(cols);
-        double q = 0.0;
-#pragma unroll
-        for (int e = 0; e < kE; ++e) {
-            const double d = static_cast<double>(v[e]) - mean;
-            q += d * d;
-        }
-        const double var = wave_sum(q) / static_cast<double>(cols);
-        const float inv = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(static_cast<float>(var), eps)));
-        const float fmean = static_cast<float>(mean);
-        uint32_t o[kE / 2];
-#pragma unroll
-        for (int i = 0; i < kE / 2; ++i) {
-            // normed is stored (rounded) by the norm op before modulate reads it: both values of
-            // the pair rounded by one conversion, then widened back
-            bf16x2_t nb;
-            nb[0] = static_cast<__bf16>(__fmul_rn(__fsub_rn(v[2 * i], fmean), inv));
-            nb[1] = static_cast<__bf16>(__fmul_rn(__fsub_rn(v[2 * i + 1], fmean), inv));
-            const uint32_t nw = __builtin_bit_cast(uint32_t, nb);
-            const float n0 = __uint_as_float(nw << 16), n1 = __uint_as_float(nw & 0xffff0000u);
-            bf16x2_t rb;
-            rb[0] = static_cast<__bf16>(__fadd_rn(__fmul_rn(n0, sc[2 * i]), sh[2 * i]));
-            rb[1] = static_cast<__bf16>(__fadd_rn(__fmul_rn(n1, sc[2 * i + 1]), sh[2 * i + 1]));
-            o[i] = __builtin_bit_cast(uint32_t, rb);
-        }
-        bf16_t* orow = out + row * cols;
-#pragma unroll
-        for (int j = 0; j < NV; ++j)
-            *reinterpret_cast<uint4*>(orow + (lane + j * kWave) * 8) =
-                make_uint4(o[4 * j], o[4 * j + 1], o[4 * j + 2], o[4 * j + 3]);
-#pragma unroll
-        for (int p = 0; p < NP; ++p)
-            *reinterpret_cast<uint32_t*>(orow + pair0 + (p * kWave + lane) * 2) = o[4 * NV + p];
-        __builtin_amdgcn_sched_barrier(0);
-        asm volatile("" ::"v"(touched));
+    for (int e = 0; e < kE; ++e) {
+        const double d = static_cast<double>(val(e)) - mean;
+        q += d * d;
     }
+    const double var = wave_sum(q) / static_cast<double>(cols);
+    const float inv = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(static_cast<float>(var), eps)));
+    const float fmean = static_cast<float>(mean);
+    // normed is stored (rounded) by the norm op before modulate reads it: both values of a pair
+    // rounded by one conversion, then widened back
+    auto out2 = [&](int i, float s0, float s1, float c0, float c1) -> uint32_t {
+        bf16x2_t nb;
+        nb[0] = static_cast<__bf16>(__fmul_rn(__fsub_rn(val(2 * i), fmean), inv));
+        nb[1] = static_cast<__bf16>(__fmul_rn(__fsub_rn(val(2 * i + 1), fmean), inv));
+        const uint32_t nw = __builtin_bit_cast(uint32_t, nb);
+        const float n0 = __uint_as_float(nw << 16), n1 = __uint_as_float(nw & 0xffff0000u);
+        bf16x2_t rb;
+        rb[0] = static_cast<__bf16>(__fadd_rn(__fmul_rn(n0, c0), s0));
+        rb[1] = static_cast<__bf16>(__fadd_rn(__fmul_rn(n1, c1), s1));
+        return __builtin_bit_cast(uint32_t, rb);
+    };
+    // Shift and 1 + scale are read per 16-byte vector of the row, after the statistics (the
+    // scheduling barriers keep them there): 16 registers at a time instead of 4 kE.
+    bf16_t* orow = out + row * cols;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        __builtin_amdgcn_sched_barrier(0);
+        const int c = (lane + j * kWave) * 8;
+        const float4 a0 = *reinterpret_cast<const float4*>(shb + c);
+        const float4 a1 = *reinterpret_cast<const float4*>(shb + c + 4);
+        const float4 m0 = *reinterpret_cast<const float4*>(scb + c);
+        const float4 m1 = *reinterpret_cast<const float4*>(scb + c + 4);
+        uint4 o;
+        o.x = out2(4 * j, a0.x, a0.y, m0.x, m0.y);
+        o.y = out2(4 * j + 1, a0.z, a0.w, m0.z, m0.w);
+        o.z = out2(4 * j + 2, a1.x, a1.y, m1.x, m1.y);
+        o.w = out2(4 * j + 3, a1.z, a1.w, m1.z, m1.w);
+        *reinterpret_cast<uint4*>(orow + c) = o;
+    }
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+        __builtin_amdgcn_sched_barrier(0);
+        const int c = pair0 + (p * kWave + lane) * 2;
+        const float2 a = *reinterpret_cast<const float2*>(shb + c);
+        const float2 m = *reinterpret_cast<const float2*>(scb + c);
+        *reinterpret_cast<uint32_t*>(orow + c) = out2(4 * NV + p, a.x, a.y, m.x, m.y);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("" ::"v"(touched));
 }
 
 // LayerNorm / RMSNorm (NormArgs) in the same lane-dense layout (C = 512 NV + 128 NP channels: NV
