@@ -363,8 +363,8 @@ __global__ void __launch_bounds__(kThreads, 1) k_flash(AttnArgs a) {
             for (int r = 0; r < 4; ++r) v[r] = o[e][u][r] * rl;
             if (VEC) {
                 uint2 w;
-                w.x = static_cast<uint32_t>(f2bf(v[0])) | (static_cast<uint32_t>(f2bf(v[1])) << 16);
-                w.y = static_cast<uint32_t>(f2bf(v[2])) | (static_cast<uint32_t>(f2bf(v[3])) << 16);
+                w.x = f2bf2(v[0], v[1]);
+                w.y = f2bf2(v[2], v[3]);
                 *reinterpret_cast<uint2*>(dst + d) = w;
             } else {
 #pragma unroll

@@ -57,6 +57,16 @@ __host__ __device__ inline bf16_t f2bf(float f) {
 // What a store through the tensor dtype does to a float.
 __host__ __device__ inline float round_bf16(float f) { return bf2f(f2bf(f)); }
 
+// Two bf16 from one conversion (v_cvt_pk_bf16_f32, the same rounding as f2bf): a pair built from
+// two f2bf calls costs a conversion per value plus a mask, a shift and an or.
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+__device__ inline uint32_t f2bf2(float lo, float hi) {
+    bf16x2_t v;
+    v[0] = static_cast<__bf16>(lo);
+    v[1] = static_cast<__bf16>(hi);
+    return __builtin_bit_cast(uint32_t, v);
+}
+
 // bf16 of an fp64 value the way the reference's host code stores one: Tensor::set(static_cast<
 // float>(v)) rounds to float, then to bf16 (two roundings; the second one sees a tie when the
 // float lands exactly halfway between two bf16 values). The second rounding works on the float's

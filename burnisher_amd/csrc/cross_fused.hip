@@ -222,10 +222,8 @@ k_cross_fused(const bf16_t* __restrict__ X, const bf16_t* __restrict__ Wq, gk::E
             const int d = e5 * 16 + g * 4;
             if (d >= fk::D) continue;
             uint2 x;
-            x.x = static_cast<uint32_t>(f2bf(w.o[e5][u][0] * rl)) |
-                  (static_cast<uint32_t>(f2bf(w.o[e5][u][1] * rl)) << 16);
-            x.y = static_cast<uint32_t>(f2bf(w.o[e5][u][2] * rl)) |
-                  (static_cast<uint32_t>(f2bf(w.o[e5][u][3] * rl)) << 16);
+            x.x = f2bf2(w.o[e5][u][0] * rl, w.o[e5][u][1] * rl);
+            x.y = f2bf2(w.o[e5][u][2] * rl, w.o[e5][u][3] * rl);
             *reinterpret_cast<uint2*>(dst + d) = x;
         }
     }

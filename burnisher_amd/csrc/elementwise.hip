@@ -17,7 +17,6 @@
 namespace bh {
 namespace {
 
-typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));   // two bf16 from one conversion
 
 constexpr int kWave = 64;
 
@@ -94,8 +93,7 @@ __device__ __forceinline__ void store8(bf16_t* p, const V8& v) {
     uint32_t w[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        w[i] = static_cast<uint32_t>(f2bf(v.f[2 * i])) |
-               (static_cast<uint32_t>(f2bf(v.f[2 * i + 1])) << 16);
+        w[i] = f2bf2(v.f[2 * i], v.f[2 * i + 1]);
     }
     *reinterpret_cast<uint4*>(p) = make_uint4(w[0], w[1], w[2], w[3]);
 }

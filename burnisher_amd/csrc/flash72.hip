@@ -332,10 +332,8 @@ __global__ void __launch_bounds__(WAVES * 64, 1) k_flash72(Flash72Args a) {
             const int d = e * 16 + g * 4;
             if (d >= D) continue;
             uint2 x;
-            x.x = static_cast<uint32_t>(f2bf(w.o[e][u][0] * rl)) |
-                  (static_cast<uint32_t>(f2bf(w.o[e][u][1] * rl)) << 16);
-            x.y = static_cast<uint32_t>(f2bf(w.o[e][u][2] * rl)) |
-                  (static_cast<uint32_t>(f2bf(w.o[e][u][3] * rl)) << 16);
+            x.x = f2bf2(w.o[e][u][0] * rl, w.o[e][u][1] * rl);
+            x.y = f2bf2(w.o[e][u][2] * rl, w.o[e][u][3] * rl);
             *reinterpret_cast<uint2*>(dst + d) = x;
         }
     }
@@ -403,7 +401,7 @@ __global__ void __launch_bounds__(256) k_flash72_combine(const float* __restrict
         uint32_t wv[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r)
-            wv[r] = static_cast<uint32_t>(f2bf(v[2 * r])) | (static_cast<uint32_t>(f2bf(v[2 * r + 1])) << 16);
+            wv[r] = f2bf2(v[2 * r], v[2 * r + 1]);
         *reinterpret_cast<uint4*>(out + (b * Sq + q) * ld_o + h * D + c * 8) = make_uint4(wv[0], wv[1], wv[2], wv[3]);
     }
 }

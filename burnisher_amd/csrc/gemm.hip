@@ -379,7 +379,7 @@ __global__ void __launch_bounds__(256) k_splitk_residual(const float* __restrict
         for (int q = 0; q < 2; ++q) {
             const float lo = __fadd_rn(res[2 * q], round_bf16(acc[2 * q]));
             const float hi = __fadd_rn(res[2 * q + 1], round_bf16(acc[2 * q + 1]));
-            o[q] = static_cast<uint32_t>(f2bf(lo)) | (static_cast<uint32_t>(f2bf(hi)) << 16);
+            o[q] = f2bf2(lo, hi);
         }
         *reinterpret_cast<uint2*>(out + i) = make_uint2(o[0], o[1]);
     }

@@ -171,7 +171,7 @@ __global__ void __launch_bounds__(256) k_gn_apply(const bf16_t* x, bf16_t* out, 
                 if (SILU) v = silu_hw(round_bf16(v));
                 v2[h] = v;
             }
-            r4[q2] = static_cast<uint32_t>(f2bf(v2[0])) | (static_cast<uint32_t>(f2bf(v2[1])) << 16);
+            r4[q2] = f2bf2(v2[0], v2[1]);
         }
         dst[i] = make_uint4(r4[0], r4[1], r4[2], r4[3]);
     }
@@ -420,8 +420,8 @@ __global__ void __launch_bounds__(256, 1) k_flash512(A5Args a) {
     const float rl = __frcp_rn(l);   // one reciprocal per query, a multiply per output
 #pragma unroll
     for (int dt = 0; dt < 32; ++dt) {
-        const uint32_t lo = static_cast<uint32_t>(f2bf(o[dt][0] * rl)) | (static_cast<uint32_t>(f2bf(o[dt][1] * rl)) << 16);
-        const uint32_t hi2 = static_cast<uint32_t>(f2bf(o[dt][2] * rl)) | (static_cast<uint32_t>(f2bf(o[dt][3] * rl)) << 16);
+        const uint32_t lo = f2bf2(o[dt][0] * rl, o[dt][1] * rl);
+        const uint32_t hi2 = f2bf2(o[dt][2] * rl, o[dt][3] * rl);
         *reinterpret_cast<uint2*>(orow + 16 * dt) = make_uint2(lo, hi2);
     }
 }
