@@ -242,7 +242,9 @@ __global__ void __launch_bounds__(WAVES * 64, 1) k_flash72(Flash72Args a) {
         const int last_full = a.Skv / kKV;   // blocks below this one hold 64 real keys
         const DmaPlan plan = dma_plan(a, wave, lane);
         auto issue = [&](int j) {
-            const int blk = __builtin_amdgcn_readfirstlane(live[min(j, n - 1)]);
+            // unmasked, the live blocks are kb0, kb0 + 1, ...: no LDS read (and no wait for every
+            // LDS read in flight) in the middle of the matrix phase
+            const int blk = MASKED ? __builtin_amdgcn_readfirstlane(live[min(j, n - 1)]) : kb0 + min(j, n - 1);
             dma_block(stage_of(j), a, plan, kbh, vbh, wave, lane, blk * kKV, MASKED && blk >= last_full);
         };
         issue(0);
