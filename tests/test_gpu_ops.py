@@ -144,6 +144,40 @@ def test_gemm_fused_epilogues(hip):
     assert s1["mismatch_frac"] < 0.01
 
 
+@pytest.mark.parametrize("B,N_tok", [(2, 1024), (7, 143)], ids=["whole_bands", "ragged_band"])
+def test_gemm_small_k_fused_epilogues(hip, B, N_tok):
+    # K = 16, the patch embedding's in_channels * patch^2: the register-weight kernel. Whole bands
+    # of rows take the path that issues every load of the band before its first store (plain and
+    # row-add stores); M = 1001 leaves a ragged last band, which walks its rows one at a time, as
+    # do the residual epilogues.
+    import burnisher_amd as bh
+    import ctypes
+    d, K = 1152, 16
+    M = B * N_tok
+    a, w, bias = randn_bf16(RNG, (M, K)), randn_bf16(RNG, (d, K), 0.02), randn_bf16(RNG, (d,), 0.02)
+    x, gate, pos = randn_bf16(RNG, (M, d)), randn_bf16(RNG, (B, d), 0.5), randn_bf16(RNG, (N_tok, d))
+    zero = np.zeros((B, d), np.uint16)
+    proj = np.zeros((M, d), np.uint16)
+    st("stock_gemm", addr(a), addr(w), addr(bias), addr(proj), M, d, K, 1, 0, BF16, 0)
+    want_pos = np.zeros_like(proj)
+    st("stock_add", addr(proj), addr(pos), addr(want_pos), B, N_tok * d, 1.0, 1, BF16)
+    want_gated = x.copy()
+    st("stock_modulate", addr(proj), addr(zero), addr(zero), addr(want_gated), B, N_tok, d,
+       addr(want_gated), addr(gate), BF16)
+    da, dw, db, dpos, dgate = dev(a), dev(w), dev(bias), dev(pos), dev(gate)
+    out = empty((M, d))
+    f = bh.GemmFused(epilogue=0, round_mid=1, row_add=P(dpos), row_add_period=N_tok, ld_out=d)
+    call("bh_gemm_fused_run", P(da), P(dw), P(db), P(out), M, d, K, ctypes.byref(f), None)
+    assert_within(from_bf16(host(out, want_pos)), from_bf16(want_pos), "gemm_fused", f"row add M={M}")
+    plain = empty((M, d))
+    call("bh_gemm", P(da), P(dw), P(db), P(plain), M, d, K, 1, 0, BF16, None)
+    assert_within(from_bf16(host(plain, proj)), from_bf16(proj), "gemm", f"plain M={M}")
+    dx = dev(x)
+    f = bh.GemmFused(epilogue=0, round_mid=1, residual=P(dx), gate=P(dgate), gate_rows=N_tok, ld_out=d)
+    call("bh_gemm_fused_run", P(da), P(dw), P(db), P(dx), M, d, K, ctypes.byref(f), None)
+    assert_within(from_bf16(host(dx, want_gated)), from_bf16(want_gated), "gemm_fused", f"gated M={M}")
+
+
 def test_gemm_split_k_epilogues(hip):
     # A long-K GEMM with few output tiles (the 512px ff2 shape at 300 tokens per row: 24 tiles of
     # 256 x 144, 72 k-tiles) runs as K slices whose fp32 partials are summed in slice order by the
