@@ -306,7 +306,7 @@ typedef enum {
     BH_DIT_ROWS_JOINED = 0,
     /* The rows in two groups, each on its own stream from the block loop's start to the output
      * head, so one group's launch tails and epilogues can overlap the other group's work. At
-     * the current kernels it is slower than JOINED (15.12 against 13.93 ms per 1024px step: each
+     * the current kernels it is slower than JOINED (14.99 against 13.51 ms per 1024px step: each
      * group's GEMMs have half the tiles, and the two streams' persistent kernels contend for the
      * CUs), so it is not the default. The second stream is the engine's own (default
      * priority); it joins the caller's stream by events, so a forward on a capturing stream is
