@@ -368,7 +368,7 @@ void launch_tn(const bf16_t* a, const bf16_t* b, bf16_t* out, int64_t m, int64_t
     const int tiles = tiles_m * tiles_n;
     // One persistent workgroup per CU (the LDS stages allow no second one); with the tile count
     // a multiple of 8, so is the grid, which the XCD banding relies on. An XCD's band is walked
-    // 256 rows of M-tiles at a time whatever the tile height.
+    // 16 / MT M-tiles (1024 rows; 960 at the 192-row tile) at a time whatever the tile height.
     int grid = min(tiles, device_cus() & ~7);
     if (grid < 8) grid = min(tiles, device_cus());
     k_gemm_tn<ACT, MODE, CONV, MT><<<grid, kWgThreads, 0, s>>>(a, b, out, m, n, k, e, tiles_m, tiles_n,
@@ -386,7 +386,7 @@ int gemm_tile_mt(int64_t m, int64_t n) {
     const int64_t tiles_n = (n + BN - 1) / BN;
     int best = kMaxMT;
     int64_t best_cost = -1;
-    for (int mt = kMaxMT; mt >= 1; mt /= 2) {
+    for (int mt = kMaxMT; mt >= 1; --mt) {
         const int64_t bm = 64 * mt;
         const int64_t rounds = (((m + bm - 1) / bm) * tiles_n + cus - 1) / cus;
         const int64_t cost = rounds * (bm + BN);
@@ -536,6 +536,7 @@ void launch_tn_mt(int mt, int mode, const bf16_t* a, const bf16_t* b, bf16_t* ou
     switch (mt) {
         case 1: launch_tn_mode<ACT, 1>(mode, a, b, out, m, n, k, e, s); break;
         case 2: launch_tn_mode<ACT, 2>(mode, a, b, out, m, n, k, e, s); break;
+        case 3: launch_tn_mode<ACT, 3>(mode, a, b, out, m, n, k, e, s); break;
         default: launch_tn_mode<ACT, kMaxMT>(mode, a, b, out, m, n, k, e, s); break;
     }
 }

@@ -159,9 +159,11 @@ def test_row_schedules_are_bit_identical_1024px(hip):
         e.close()
 
 
-def test_fused_plan_equals_opwise_plan(hip):
-    # Fusion moves no rounding point, so the two plans agree bit for bit.
-    wl = make_workload(PIXART_SIGMA, batch=2, latent_hw=64, caption_len=300, layers=2)
+@pytest.mark.parametrize("hw,layers", [(64, 2), (96, 1)], ids=["512px", "768px"])
+def test_fused_plan_equals_opwise_plan(hip, hw, layers):
+    # Fusion moves no rounding point, so the two plans agree bit for bit (at 768px the fused QKV
+    # projection runs 256-row tiles and the separate Q, K and V projections 192-row ones).
+    wl = make_workload(PIXART_SIGMA, batch=2, latent_hw=hw, caption_len=300, layers=layers)
     a, b = Engine(wl, 0), Engine(wl, 1)
     try:
         assert np.array_equal(a.forward(), b.forward())

@@ -70,8 +70,10 @@ GEMM_SHAPES = [(13, 11, 40), (37, 150, 64), (2, 6912, 1152), (5, 1152, 256), (60
                (37, 152, 128), (777, 296, 320), (300, 1152, 64),
                # more tiles than CUs: the persistent loop, whole and ragged tile grids
                (3072, 3456, 128), (4100, 2312, 64),
-               # tile heights: 128 rows (96 tiles of 256 rows would fill 96 CUs), 64 rows
-               (2048, 1728, 256), (1000, 1160, 192)]
+               # tile heights: 128 rows (96 tiles of 256 rows would fill 96 CUs), 64 rows, 192 rows
+               # (the 768px N = 1152 shape: 144 tiles of 256 rows against 192 of 192), and 192
+               # rows with ragged M and N
+               (2048, 1728, 256), (1000, 1160, 192), (4608, 1152, 1152), (4500, 1160, 192)]
 
 
 @pytest.mark.parametrize("shape", GEMM_SHAPES, ids=lambda s: "x".join(map(str, s)))
@@ -88,6 +90,24 @@ def test_gemm_matches_oracle(hip, shape, epi):
     g = host(got, want)
     assert_within(from_bf16(g), from_bf16(want), "gemm", f"{shape} epi={epi}")
     assert np.array_equal(g, host(again, want)), "not byte-identical across two calls"
+
+
+@pytest.mark.parametrize("act", [0, 1], ids=["plain", "gelu"])
+def test_gemm_tile_heights_agree(hip, act):
+    # The tile height is chosen per launch from M and N (on 256 CUs: 64 rows at M = 2048, 128 at
+    # 4096, 192 at 4608 and 256 at 8192 for N = 1152); every height sums an output's k-tiles in the
+    # same order with the same MFMAs, so the rows a shorter launch shares with a taller one are
+    # bit-identical.
+    M, N, K = 8192, 1152, 1152
+    a, b, bias = randn_bf16(RNG, (M, K)), randn_bf16(RNG, (N, K), 0.02), randn_bf16(RNG, (N,), 0.02)
+    da, db, dbias = dev(a), dev(b), dev(bias)
+    full = empty((M, N))
+    call("bh_gemm", P(da), P(db), P(dbias), P(full), M, N, K, 1, act, BF16, None)
+    want = host(full, np.zeros((M, N), np.uint16))
+    for rows in (2048, 4096, 4608, 4500):
+        part = empty((rows, N))
+        call("bh_gemm", P(da), P(db), P(dbias), P(part), rows, N, K, 1, act, BF16, None)
+        assert np.array_equal(host(part, want[:rows]), want[:rows]), f"{rows} rows differ from {M}"
 
 
 def test_gemm_unaligned_k_and_plain_layouts(hip):
