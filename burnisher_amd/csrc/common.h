@@ -238,7 +238,7 @@ struct GemmEpilogue {
     int64_t vt_period = 0, vt_col0 = 0, vt_seq = 0, vt_ld = 0;
     int vt_heads = 0, vt_dim = 72;
     // Split-K (GEMMs with too few output tiles to fill the CUs): 0 lets the shape decide
-    // (gemm_splits), 1 never splits, n >= 2 sums exactly n K slices. The fp32 partials go to
+    // (gemm_splits), 1 never splits, 2 <= n <= 8 sums exactly n K slices. The fp32 partials go to
     // `splitk_ws` (splitk_ws_floats floats, at least splits * m * n) or, when it is null, to a
     // per-device library buffer grown on demand (calls that overlap on one device share it).
     int splitk = 0;

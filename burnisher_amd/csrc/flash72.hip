@@ -366,10 +366,13 @@ __global__ void __launch_bounds__(256) k_transpose_v72(const bf16_t* __restrict_
 
 // The key splits' partials into the output: per (b, h, q), M = the largest running maximum,
 // out = sum_s O_s 2^(m_s - M) / sum_s l_s 2^(m_s - M), in split order. One thread per 8 dims.
-// The partials cover queries q0 .. Sq - 1 of every (b, h).
-__global__ void __launch_bounds__(256) k_flash72_combine(const float* __restrict__ part, int splits,
-                                                         int B, int H, int Sq, int q0, bf16_t* out,
-                                                         int64_t ld_o) {
+// The partials cover queries q0 .. Sq - 1 of every (b, h). The split count is a template
+// argument so that a thread issues every load of its S partials before the first use: with a
+// run-time count each split's loads waited for the previous split's (2 S memory round trips per
+// thread, which set the launch's time, as every thread of the grid is resident at once).
+template <int S>
+__global__ void __launch_bounds__(256) k_flash72_combine(const float* __restrict__ part, int B, int H,
+                                                         int Sq, int q0, bf16_t* out, int64_t ld_o) {
     constexpr int kChunks = D / 8;   // 9
     const int Sp = Sq - q0;
     const int64_t rows = static_cast<int64_t>(B) * H * Sp;
@@ -379,19 +382,27 @@ __global__ void __launch_bounds__(256) k_flash72_combine(const float* __restrict
         const int64_t row = i / kChunks;   // ((b * H + h) * Sp + q - q0)
         const int c = static_cast<int>(i - row * kChunks);
         const float* p = part + row * 80;
-        float mx = -INFINITY;
-        for (int sp = 0; sp < splits; ++sp) mx = fmaxf(mx, p[sp * split_stride + 73]);
-        float l = 0.f, o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-        for (int sp = 0; sp < splits; ++sp) {
+        float2 lm[S];   // (l, m) of each split: floats 72 and 73 of its row
+        f32x4_t lo[S], hi[S];
+#pragma unroll
+        for (int sp = 0; sp < S; ++sp) {
             const float* ps = p + sp * split_stride;
-            const float wgt = __builtin_amdgcn_exp2f(ps[73] - mx);   // 0 for an empty split
-            l = __fmaf_rn(ps[72], wgt, l);
-            const f32x4_t lo = *reinterpret_cast<const f32x4_t*>(ps + c * 8);
-            const f32x4_t hi = *reinterpret_cast<const f32x4_t*>(ps + c * 8 + 4);
+            lm[sp] = *reinterpret_cast<const float2*>(ps + 72);
+            lo[sp] = *reinterpret_cast<const f32x4_t*>(ps + c * 8);
+            hi[sp] = *reinterpret_cast<const f32x4_t*>(ps + c * 8 + 4);
+        }
+        float mx = -INFINITY;
+#pragma unroll
+        for (int sp = 0; sp < S; ++sp) mx = fmaxf(mx, lm[sp].y);
+        float l = 0.f, o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int sp = 0; sp < S; ++sp) {
+            const float wgt = __builtin_amdgcn_exp2f(lm[sp].y - mx);   // 0 for an empty split
+            l = __fmaf_rn(lm[sp].x, wgt, l);
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                o[r] = __fmaf_rn(lo[r], wgt, o[r]);
-                o[4 + r] = __fmaf_rn(hi[r], wgt, o[4 + r]);
+                o[r] = __fmaf_rn(lo[sp][r], wgt, o[r]);
+                o[4 + r] = __fmaf_rn(hi[sp][r], wgt, o[4 + r]);
             }
         }
         const float rl = __frcp_rn(l);
@@ -406,6 +417,12 @@ __global__ void __launch_bounds__(256) k_flash72_combine(const float* __restrict
             wv[r] = f2bf2(v[2 * r], v[2 * r + 1]);
         *reinterpret_cast<uint4*>(out + (b * Sq + q) * ld_o + h * D + c * 8) = make_uint4(wv[0], wv[1], wv[2], wv[3]);
     }
+}
+
+template <int S>
+void launch_combine(const Flash72Args& a, int64_t threads, int q0, bf16_t* out, int64_t ld_o, hipStream_t s) {
+    k_flash72_combine<S><<<static_cast<int>(std::min<int64_t>((threads + 255) / 256, 8192)), 256, 0, s>>>(
+        a.part, a.B, a.H, a.Sq, q0, out, ld_o);
 }
 
 // Per-device partials for split calls that bring no buffer of their own, grown on demand.
@@ -645,8 +662,15 @@ void launch_flash72(const bf16_t* q, int64_t ld_q, const bf16_t* k, int64_t ld_k
     if (a.splits > 1) {
         const int q0 = a.qb0 * kQPerWg;
         const int64_t threads = batch * heads * (q_len - q0) * (D / 8);
-        k_flash72_combine<<<static_cast<int>(std::min<int64_t>((threads + 255) / 256, 8192)), 256, 0, s>>>(
-            a.part, a.splits, a.B, a.H, a.Sq, q0, out, ld_o);
+        switch (a.splits) {
+            case 2: launch_combine<2>(a, threads, q0, out, ld_o, s); break;
+            case 3: launch_combine<3>(a, threads, q0, out, ld_o, s); break;
+            case 4: launch_combine<4>(a, threads, q0, out, ld_o, s); break;
+            case 5: launch_combine<5>(a, threads, q0, out, ld_o, s); break;
+            case 6: launch_combine<6>(a, threads, q0, out, ld_o, s); break;
+            case 7: launch_combine<7>(a, threads, q0, out, ld_o, s); break;
+            default: launch_combine<8>(a, threads, q0, out, ld_o, s); break;
+        }
         launch_check("attention (head_dim 72, key-split combine)");
     }
 }

@@ -417,18 +417,26 @@ void launch_tn_splitk(const bf16_t* a, const bf16_t* b, float* partial, int64_t 
         a, b, reinterpret_cast<bf16_t*>(partial), m, n, k / splits, e, tiles_m, tiles_n, 4, ConvGeom{});
 }
 
+// The split-K reductions below take the slice count S as a template argument, so a thread issues
+// the loads of all S slices (and of the residual and gate) before the first addition: with a
+// run-time count each slice's load waited for the previous slice's sum, S + 1 memory round trips
+// per thread, which set the launch's time because every thread of the grid is resident at once.
+
 // out[m, n] = bf16(residual[m, n] + bf16(sum_s partial[s][m][n])), the slices summed in order.
-__global__ void __launch_bounds__(256) k_splitk_residual(const float* __restrict__ partial, int splits,
+template <int S>
+__global__ void __launch_bounds__(256) k_splitk_residual(const float* __restrict__ partial,
                                                          const bf16_t* residual, bf16_t* out, int64_t mn) {
     for (int64_t i = (blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x) * 4; i < mn;
          i += static_cast<int64_t>(gridDim.x) * blockDim.x * 4) {
-        f32x4_t acc = *reinterpret_cast<const f32x4_t*>(partial + i);
-        for (int sp = 1; sp < splits; ++sp) {
-            const f32x4_t p = *reinterpret_cast<const f32x4_t*>(partial + sp * mn + i);
+        f32x4_t p[S];
 #pragma unroll
-            for (int q = 0; q < 4; ++q) acc[q] = __fadd_rn(acc[q], p[q]);
-        }
+        for (int sp = 0; sp < S; ++sp) p[sp] = *reinterpret_cast<const f32x4_t*>(partial + sp * mn + i);
         const uint2 r = *reinterpret_cast<const uint2*>(residual + i);
+        f32x4_t acc = p[0];
+#pragma unroll
+        for (int sp = 1; sp < S; ++sp)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) acc[q] = __fadd_rn(acc[q], p[sp][q]);
         const float res[4] = {__uint_as_float(r.x << 16), __uint_as_float(r.x & 0xffff0000u),
                               __uint_as_float(r.y << 16), __uint_as_float(r.y & 0xffff0000u)};
         uint32_t o[2];
@@ -445,9 +453,9 @@ __global__ void __launch_bounds__(256) k_splitk_residual(const float* __restrict
 // The split-K epilogue: out[m, n8..n8+7] from the slices summed in order, then exactly the MFMA
 // kernel's epilogue (chunk_store): bias, activation, the mid rounding, residual or gated residual,
 // one rounding at the store. out may alias the residual (each element is read before written).
-template <int ACT, int MODE>
-__global__ void __launch_bounds__(256) k_splitk_epi(const float* __restrict__ partial, int splits,
-                                                    int64_t M, int64_t N, Epi e, bf16_t* out) {
+template <int ACT, int MODE, int S>
+__global__ void __launch_bounds__(256) k_splitk_epi(const float* __restrict__ partial, int64_t M,
+                                                    int64_t N, Epi e, bf16_t* out) {
     const int64_t per_row = N / 8;
     const int64_t groups = M * per_row;
     const int64_t mn = M * N;
@@ -455,32 +463,40 @@ __global__ void __launch_bounds__(256) k_splitk_epi(const float* __restrict__ pa
          g += static_cast<int64_t>(gridDim.x) * blockDim.x) {
         const int64_t m = g / per_row, n = (g - m * per_row) * 8;
         const float* p = partial + m * N + n;
-        f32x4_t lo = *reinterpret_cast<const f32x4_t*>(p), hi = *reinterpret_cast<const f32x4_t*>(p + 4);
-        for (int sp = 1; sp < splits; ++sp) {
-            const f32x4_t a = *reinterpret_cast<const f32x4_t*>(p + sp * mn);
-            const f32x4_t b = *reinterpret_cast<const f32x4_t*>(p + sp * mn + 4);
+        f32x4_t a[S], b[S];
+#pragma unroll
+        for (int sp = 0; sp < S; ++sp) {
+            a[sp] = *reinterpret_cast<const f32x4_t*>(p + sp * mn);
+            b[sp] = *reinterpret_cast<const f32x4_t*>(p + sp * mn + 4);
+        }
+        const uint4 braw = e.bias ? *reinterpret_cast<const uint4*>(e.bias + n) : uint4{};
+        uint4 rraw{}, graw{};
+        if (MODE == EPI_RESIDUAL || MODE == EPI_GATED) rraw = *reinterpret_cast<const uint4*>(e.residual + m * e.ld_out + n);
+        if (MODE == EPI_GATED) graw = *reinterpret_cast<const uint4*>(e.gate + (m / e.gate_rows) * N + n);
+        f32x4_t lo = a[0], hi = b[0];
+#pragma unroll
+        for (int sp = 1; sp < S; ++sp)
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
-                lo[q] = __fadd_rn(lo[q], a[q]);
-                hi[q] = __fadd_rn(hi[q], b[q]);
+                lo[q] = __fadd_rn(lo[q], a[sp][q]);
+                hi[q] = __fadd_rn(hi[q], b[sp][q]);
             }
-        }
         float x[8], bias[8], t[8];
-        bias_or_neg_zero(e, e.bias ? *reinterpret_cast<const uint4*>(e.bias + n) : uint4{}, bias);
+        bias_or_neg_zero(e, braw, bias);
 #pragma unroll
         for (int q = 0; q < 8; ++q) x[q] = act_fast<ACT>(__fadd_rn(q < 4 ? lo[q] : hi[q - 4], bias[q]));
         if (MODE != EPI_STORE && e.round_mid)
 #pragma unroll
             for (int q = 0; q < 8; ++q) x[q] = round_bf16(x[q]);
         if (MODE == EPI_RESIDUAL) {
-            unpack8(*reinterpret_cast<const uint4*>(e.residual + m * e.ld_out + n), t);
+            unpack8(rraw, t);
 #pragma unroll
             for (int q = 0; q < 8; ++q) x[q] = __fadd_rn(t[q], x[q]);
         }
         if (MODE == EPI_GATED) {
             float gq[8];
-            unpack8(*reinterpret_cast<const uint4*>(e.gate + (m / e.gate_rows) * N + n), gq);
-            unpack8(*reinterpret_cast<const uint4*>(e.residual + m * e.ld_out + n), t);
+            unpack8(graw, gq);
+            unpack8(rraw, t);
 #pragma unroll
             for (int q = 0; q < 8; ++q) x[q] = __fadd_rn(__fmul_rn(x[q], gq[q]), t[q]);
         }
@@ -507,15 +523,29 @@ float* splitk_workspace(int64_t floats) {
     return static_cast<float*>(ptr[dev]);
 }
 
-template <int ACT>
-void launch_splitk_epi(int mode, const float* partial, int splits, int64_t m, int64_t n, const Epi& e,
-                       bf16_t* out, hipStream_t s) {
+template <int ACT, int S>
+void launch_splitk_epi_s(int mode, const float* partial, int64_t m, int64_t n, const Epi& e, bf16_t* out,
+                         hipStream_t s) {
     const int64_t groups = m * (n / 8);
     const int blocks = static_cast<int>(std::min<int64_t>((groups + 255) / 256, 8192));
     switch (mode) {
-        case EPI_STORE: k_splitk_epi<ACT, EPI_STORE><<<blocks, 256, 0, s>>>(partial, splits, m, n, e, out); break;
-        case EPI_RESIDUAL: k_splitk_epi<ACT, EPI_RESIDUAL><<<blocks, 256, 0, s>>>(partial, splits, m, n, e, out); break;
-        default: k_splitk_epi<ACT, EPI_GATED><<<blocks, 256, 0, s>>>(partial, splits, m, n, e, out); break;
+        case EPI_STORE: k_splitk_epi<ACT, EPI_STORE, S><<<blocks, 256, 0, s>>>(partial, m, n, e, out); break;
+        case EPI_RESIDUAL: k_splitk_epi<ACT, EPI_RESIDUAL, S><<<blocks, 256, 0, s>>>(partial, m, n, e, out); break;
+        default: k_splitk_epi<ACT, EPI_GATED, S><<<blocks, 256, 0, s>>>(partial, m, n, e, out); break;
+    }
+}
+
+template <int ACT>
+void launch_splitk_epi(int mode, const float* partial, int splits, int64_t m, int64_t n, const Epi& e,
+                       bf16_t* out, hipStream_t s) {
+    switch (splits) {
+        case 2: launch_splitk_epi_s<ACT, 2>(mode, partial, m, n, e, out, s); break;
+        case 3: launch_splitk_epi_s<ACT, 3>(mode, partial, m, n, e, out, s); break;
+        case 4: launch_splitk_epi_s<ACT, 4>(mode, partial, m, n, e, out, s); break;
+        case 5: launch_splitk_epi_s<ACT, 5>(mode, partial, m, n, e, out, s); break;
+        case 6: launch_splitk_epi_s<ACT, 6>(mode, partial, m, n, e, out, s); break;
+        case 7: launch_splitk_epi_s<ACT, 7>(mode, partial, m, n, e, out, s); break;
+        default: launch_splitk_epi_s<ACT, 8>(mode, partial, m, n, e, out, s); break;   // 2..8 slices
     }
 }
 
@@ -623,7 +653,7 @@ void launch_gemm_bf16(const bf16_t* a, const bf16_t* b, const bf16_t* bias, bf16
             "gemm: M, N, the gate's row count and the row-add period must be below 2^31");
     const int splits = ep.splitk > 0 ? ep.splitk : gemm_splits(m, n, k, ep);
     if (splits > 1) {
-        require(k % (BK * splits) == 0 && !ep.vt && mode != EPI_ROW_ADD && splits <= 16,
+        require(k % (BK * splits) == 0 && !ep.vt && mode != EPI_ROW_ADD && splits <= 8,
                 "gemm split-K: " + std::to_string(splits) + " slices of K = " + std::to_string(k) +
                     " (whole 64-wide k-tiles, plain, residual or gated store only)");
         const int64_t floats = static_cast<int64_t>(splits) * m * n;
@@ -721,7 +751,16 @@ void launch_gemm_splitk_residual(const bf16_t* a, const bf16_t* b, float* partia
     ProfileScope ps(K_ELEMENTWISE, s, static_cast<double>(m) * n * (4.0 * splits + 4.0));
     const int64_t mn = m * n;
     const int64_t blocks = std::min<int64_t>((mn / 4 + 255) / 256, 8192);
-    k_splitk_residual<<<static_cast<int>(blocks), 256, 0, s>>>(partial, splits, residual, out, mn);
+    const int g = static_cast<int>(blocks);
+    switch (splits) {
+        case 2: k_splitk_residual<2><<<g, 256, 0, s>>>(partial, residual, out, mn); break;
+        case 3: k_splitk_residual<3><<<g, 256, 0, s>>>(partial, residual, out, mn); break;
+        case 4: k_splitk_residual<4><<<g, 256, 0, s>>>(partial, residual, out, mn); break;
+        case 5: k_splitk_residual<5><<<g, 256, 0, s>>>(partial, residual, out, mn); break;
+        case 6: k_splitk_residual<6><<<g, 256, 0, s>>>(partial, residual, out, mn); break;
+        case 7: k_splitk_residual<7><<<g, 256, 0, s>>>(partial, residual, out, mn); break;
+        default: k_splitk_residual<8><<<g, 256, 0, s>>>(partial, residual, out, mn); break;
+    }
     launch_check("gemm (split-K reduce)");
 }
 
