@@ -381,7 +381,7 @@ void launch_flash72(const bf16_t* q, int64_t ld_q, const bf16_t* k, int64_t ld_k
 // one launch (cross_fused.hip): ctx = attention(bf16(x wq^T + bq), K, V^T, mask), bit-identical
 // with launch_gemm_bf16 followed by launch_flash72. x is [batch * tokens, heads * 72]; K rows of
 // stride ld_k at [batch, kv_len]; V^T as launch_flash72 reads it. Supported when tokens % 256 == 0,
-// the head count is even, kv_len <= 448 and the 256 x 144 tiles fill the chip.
+// the head count is even, kv_len <= 448 and the 256 x 144 tiles fill more than half the CUs.
 bool cross_fused_supported(int64_t batch, int64_t tokens, int64_t heads, int64_t head_dim, int64_t kv_len);
 void launch_cross_fused(const bf16_t* x, const bf16_t* wq, const bf16_t* bq, int64_t batch,
                         int64_t tokens, int64_t heads, const bf16_t* k, int64_t ld_k, const bf16_t* vt,

@@ -237,9 +237,13 @@ bool cross_fused_supported(int64_t batch, int64_t tokens, int64_t heads, int64_t
     hip_check(hipGetDevice(&dev), "hipGetDevice");
     hip_check(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev), "hipDeviceGetAttribute");
     const int64_t tiles = batch * tokens / G::BM * (heads * head_dim / gk::BN);
-    // one tile per workgroup and CU: worth it only when the tiles fill the chip
+    // One tile per workgroup and CU, so a launch of up to one round takes about one tile's time
+    // whatever its tile count, while the separate projection and attention shrink with the rows:
+    // fused when the tiles fill more than half the chip. 768px (144 tiles on 256 CUs) measured
+    // 9.26 -> 8.94 ms per step fused; 512px (64 tiles) keeps the pair (13 + 14.5 us against a
+    // ~40 us tile).
     return head_dim == fk::D && heads % kHeadsPerTile == 0 && tokens % G::BM == 0 && kv_len > 0 &&
-           kv_len <= fk::kResidentBlocks * fk::kKV && tiles >= cus;
+           kv_len <= fk::kResidentBlocks * fk::kKV && tiles * 2 > cus;
 }
 
 void launch_cross_fused(const bf16_t* x, const bf16_t* wq, const bf16_t* bq, int64_t batch,

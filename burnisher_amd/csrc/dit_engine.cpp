@@ -129,7 +129,8 @@ struct bh_dit {
     bool vt72 = false;
     int64_t qkv_ld = 0;               // row stride of qkv: 2d when V goes to V^T, else 3d
     // The cross-attention's Q projection fused into its attention (cross_fused.hip), for launches
-    // of at least cross_fused_min_rows batch rows (its 256 x 144 tiles must fill the chip).
+    // of at least cross_fused_min_rows batch rows (its 256 x 144 tiles must fill more than half
+    // the CUs).
     bool cross_fused = false;
     int64_t cross_fused_min_rows = 0;
     int64_t workspace = 0;
