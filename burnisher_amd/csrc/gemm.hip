@@ -398,11 +398,42 @@ int gemm_tile_mt(int64_t m, int64_t n) {
     return best;
 }
 
+// Split-K plans in the tile chooser's units (one operand row loaded per k-tile, ~2.75 ns): a
+// launch of S slices on BM-row tiles costs ceil(tiles * S / CUs) rounds of K / S / 64 k-tiles of
+// BM + 144 rows each, plus its fp32 partials, S * M * N * 4 bytes written and read again by the
+// summing epilogue at ~4.7 TB/s (one unit per 12,800 bytes). Fewer slices on shorter tiles can
+// win: at 512px ff2 (2048 x 1152 x 4608) 2 slices of 128-row tiles instead of 4 of 256 rows
+// halve the partial traffic (gemm_ff2 1.217 -> 1.149 ms per step, interleaved A/B).
+int64_t splitk_cost(int64_t m, int64_t n, int64_t k, int mt, int splits) {
+    const int64_t bm = 64 * mt, cus = device_cus();
+    const int64_t tiles = ((m + bm - 1) / bm) * ((n + BN - 1) / BN);
+    const int64_t rounds = (tiles * splits + cus - 1) / cus;
+    const int64_t loop = rounds * (k / BK / splits) * (bm + BN);
+    const int64_t partials = splits > 1 ? static_cast<int64_t>(splits) * m * n * 8 / 12800 : 0;
+    return loop + partials;
+}
+
+// The tile height of an S-slice launch: the cheapest by splitk_cost (ties keep the taller tile).
+// The height does not change any sum; the slice count does, and is decided on the full batch.
+int splitk_tile_mt(int64_t m, int64_t n, int64_t k, int splits) {
+    int best = kMaxMT;
+    int64_t best_cost = -1;
+    for (int mt = kMaxMT; mt >= 1; --mt) {
+        const int64_t c = splitk_cost(m, n, k, mt, splits);
+        if (best_cost < 0 || c < best_cost) {
+            best = mt;
+            best_cost = c;
+        }
+    }
+    return best;
+}
+
 // Split-K partials: `splits` slices of K in one launch (grid.y = slice), each persistent
 // workgroup set over the same output tiles, slice s writing fp32 partial[s][m][n].
+template <int MT = kMaxMT>
 void launch_tn_splitk(const bf16_t* a, const bf16_t* b, float* partial, int64_t m, int64_t n, int64_t k,
                       int splits, hipStream_t s) {
-    constexpr int BM = Geom<kMaxMT>::BM;
+    constexpr int BM = Geom<MT>::BM;
     const int tiles_m = static_cast<int>((m + BM - 1) / BM);
     const int tiles_n = static_cast<int>((n + BN - 1) / BN);
     const int tiles = tiles_m * tiles_n;
@@ -413,8 +444,8 @@ void launch_tn_splitk(const bf16_t* a, const bf16_t* b, float* partial, int64_t 
     e.ld_out = n;
     e.ld_k = k;
     e.vt_dim = 72;
-    k_gemm_tn<0, EPI_F32, false><<<dim3(grid, splits), kWgThreads, 0, s>>>(
-        a, b, reinterpret_cast<bf16_t*>(partial), m, n, k / splits, e, tiles_m, tiles_n, 4, ConvGeom{});
+    k_gemm_tn<0, EPI_F32, false, MT><<<dim3(grid, splits), kWgThreads, 0, s>>>(
+        a, b, reinterpret_cast<bf16_t*>(partial), m, n, k / splits, e, tiles_m, tiles_n, 16 / MT, ConvGeom{});
 }
 
 // The split-K reductions below take the slice count S as a template argument, so a thread issues
@@ -666,7 +697,12 @@ void launch_gemm_bf16(const bf16_t* a, const bf16_t* b, const bf16_t* bias, bf16
             partial = splitk_workspace(floats);
         }
         ProfileScope ps(K_GEMM, s, flops, gemm_subclass());
-        launch_tn_splitk(a, b, partial, m, n, k, splits, s);
+        switch (splitk_tile_mt(m, n, k, splits)) {
+            case 1: launch_tn_splitk<1>(a, b, partial, m, n, k, splits, s); break;
+            case 2: launch_tn_splitk<2>(a, b, partial, m, n, k, splits, s); break;
+            case 3: launch_tn_splitk<3>(a, b, partial, m, n, k, splits, s); break;
+            default: launch_tn_splitk<kMaxMT>(a, b, partial, m, n, k, splits, s); break;
+        }
         launch_check("gemm (split-K partials)");
         switch (ep.act) {
             case 1: launch_splitk_epi<1>(mode, partial, splits, m, n, e, out, s); break;
@@ -732,7 +768,19 @@ int gemm_splits(int64_t m, int64_t n, int64_t k, const GemmEpilogue& ep) {
     if (k / BK < kSplitKMinKTiles) return 1;
     const int64_t tiles = ((m + Geom<kMaxMT>::BM - 1) / Geom<kMaxMT>::BM) * ((n + BN - 1) / BN);
     if (tiles * 2 > device_cus()) return 1;
-    return gemm_splitk_choice(m, n, k);
+    // the slice count (2..8, whole k-tiles, at least 4 per slice) whose best tile height gives the
+    // cheapest plan; against the whole GEMM at its own best height
+    int best = 1;
+    int64_t best_cost = -1;
+    for (int sp = 1; sp <= 8; ++sp) {
+        if (sp > 1 && (k % (BK * sp) != 0 || k / sp < 4 * BK)) continue;
+        const int64_t c = splitk_cost(m, n, k, splitk_tile_mt(m, n, k, sp), sp);
+        if (best_cost < 0 || c < best_cost) {
+            best = sp;
+            best_cost = c;
+        }
+    }
+    return best;
 }
 
 void launch_gemm_splitk_residual(const bf16_t* a, const bf16_t* b, float* partial, int splits,
