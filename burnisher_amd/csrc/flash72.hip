@@ -474,9 +474,13 @@ int flash72_splits(int64_t batch, int64_t heads, int64_t q_len, int64_t kv_len, 
     hip_check(hipGetDevice(&dev), "hipGetDevice");
     hip_check(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev), "hipDeviceGetAttribute");
     if (wgs * 2 > cus) return 1;
+    // As many splits as fit in one round, each of at least four key blocks: with two, a
+    // workgroup's fixed work (Q load, pipeline fill, the 164 KB partial) and the combine's traffic
+    // outweighed the CUs gained (512px at batch 1: 8 splits of 2 blocks 0.80 ms of self-attention
+    // per step, 4 of 4 0.75 ms, 2 of 8 0.84 ms; interleaved A/B).
     int best = 1;
     for (int sp = 2; sp <= 8; ++sp)
-        if (wgs * sp <= cus && nblk >= 2 * sp) best = sp;
+        if (wgs * sp <= cus && nblk >= 4 * sp) best = sp;
     return best;
 }
 
