@@ -319,9 +319,11 @@ void launch_gemm_bf16(const bf16_t* a, const bf16_t* b, const bf16_t* bias, bf16
 // that keeps every slice's workgroups resident at once.
 int gemm_splitk_choice(int64_t m, int64_t n, int64_t k);
 // The K slices launch_gemm_bf16 uses for this shape and epilogue when ep.splitk is 0 (1: none):
-// gemm_splitk_choice when K holds at least 48 k-tiles, at most half the CUs would hold a tile, the
+// considered when K holds at least 48 k-tiles, at most half the CUs would hold a 256-row tile, the
 // MFMA kernel applies and the epilogue is a plain, residual or gated store (no row add, no
-// transposed V).
+// transposed V); then the slice count (up to 8) whose best tile height gives the least estimated
+// time, the fp32 partials' traffic included. The tile height of the split launch is chosen per
+// launch and changes no sum.
 int gemm_splits(int64_t m, int64_t n, int64_t k, const GemmEpilogue& ep);
 // out = bf16(residual + bf16(A . B^T)) through `splits` fp32 partials (partial holds
 // splits * m * n floats) summed in slice order; out may alias residual.
