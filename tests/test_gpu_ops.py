@@ -110,6 +110,26 @@ def test_gemm_tile_heights_agree(hip, act):
         assert np.array_equal(host(part, want[:rows]), want[:rows]), f"{rows} rows differ from {M}"
 
 
+def test_gemm_tile_heights_agree_gated_residual(hip):
+    # The same for the gated-residual store (x + gate[row / tokens] * bf16(A . B^T + bias), in
+    # place), the epilogue of the out-projection and ff2: 4608 rows run 192-row tiles, 8192 rows
+    # 256-row tiles, 2048 rows 64-row tiles.
+    import burnisher_amd as bh
+    import ctypes
+    M, N, K, tokens = 8192, 1152, 1152, 256
+    a, b, bias = randn_bf16(RNG, (M, K)), randn_bf16(RNG, (N, K), 0.02), randn_bf16(RNG, (N,), 0.02)
+    x, gate = randn_bf16(RNG, (M, N)), randn_bf16(RNG, (M // tokens, N), 0.5)
+    da, db, dbias, dgate = dev(a), dev(b), dev(bias), dev(gate)
+    results = {}
+    for rows in (M, 4608, 2048):
+        dx = dev(x[:rows])
+        f = bh.GemmFused(epilogue=0, round_mid=1, residual=P(dx), gate=P(dgate), gate_rows=tokens, ld_out=N)
+        call("bh_gemm_fused_run", P(da), P(db), P(dbias), P(dx), rows, N, K, ctypes.byref(f), None)
+        results[rows] = host(dx, x[:rows])
+    for rows in (4608, 2048):
+        assert np.array_equal(results[rows], results[M][:rows]), f"{rows} rows differ from {M}"
+
+
 def test_gemm_unaligned_k_and_plain_layouts(hip):
     # K % 8 != 0, B as [K, N], and fp32: the reference-order kernel, bit-exact with the oracle
     M, N, K = 9, 7, 13
