@@ -266,7 +266,7 @@ def denoise(args) -> int:
     line = {
         "metric": f"denoise loop ms/image @{args.resolution}px bf16, {steps} steps (1 GPU)",
         "value": round(graph_ms, 3), "unit": "ms", "n_gpus": 1, "steps": reps, "warmup": 1,
-        "higher_is_better": False, "dtype": "bf16",
+        "ms_per_step": round(graph_ms, 3), "higher_is_better": False, "dtype": "bf16",
         "data": "synthetic: seeded N(0,0.02) bf16 weights, N(0,1) caption and initial latent",
         "config": {"workload": f"PixArt-Sigma denoise loop {args.resolution}px, CFG 4.5, "
                                f"{steps} DPM-Solver++ 2M steps, caption {wl.caption_len}",
@@ -276,6 +276,7 @@ def denoise(args) -> int:
         "eager_ms_per_step": round(eager_ms / steps, 4),
         "graph_capture_s": round(capture_s, 3),
         "step_tflops_graph": round(flops / (graph_ms / steps * 1e-3) / 1e12, 2),
+        "output_stats": tensor_stats(latent.view(torch.bfloat16)),
     }
     bh.lib().bh_denoiser_destroy(den)
     bh.lib().bh_sched_destroy(sched)
@@ -323,6 +324,7 @@ def vae(args) -> int:
     ms = a.elapsed_time(b) / steps
     img = image.float()
     assert torch.isfinite(img).all() and img.std() > 1e-3, "degenerate decoded image"
+    output_stats = tensor_stats(image)
     # one profiled decode for the breakdown
     bh.check(bh.lib().bh_profile_enable((1 << bh.K_GEMM_QKV + 1) - 1), "bh_profile_enable")
     bh.call("bh_vae_decode", h, latent.data_ptr(), image.data_ptr(), sp)
@@ -435,6 +437,7 @@ def t5(args) -> int:
     ms = a.elapsed_time(b) / steps
     o = out.float()
     assert torch.isfinite(o).all() and o.std() > 1e-3, "degenerate encoder output"
+    output_stats = tensor_stats(out)
     bh.check(bh.lib().bh_profile_enable((1 << bh.K_GEMM_QKV + 1) - 1), "bh_profile_enable")
     bh.call("bh_t5_encode", h, wl.ids.ctypes.data, out.data_ptr(), sp)
     torch.cuda.synchronize()
@@ -535,6 +538,14 @@ def reference_stock_block(wl):
             "equals_port": bool(np.array_equal(out, port)),
             "sample": "BASELINE configs[0]: one block at 512px, batch 1, caption 120, the reference's "
                       "stock PixArtDiT::forward (oracle/_ref/libref_stock.so), one thread"}
+
+
+def tensor_stats(t) -> dict:
+    """Mean, standard deviation and largest magnitude of a timed output, as the reference's bench
+    line carries them (burnisher_main.cpp:478-480)."""
+    f = t.detach().double().cpu()
+    return {"mean": float(f.mean()), "std": float(f.std(unbiased=False)), "absmax": float(f.abs().max()),
+            "finite": bool(f.isfinite().all())}
 
 
 def parity(got, want) -> dict:

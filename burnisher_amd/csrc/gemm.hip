@@ -448,6 +448,17 @@ void launch_tn_splitk(const bf16_t* a, const bf16_t* b, float* partial, int64_t 
         a, b, reinterpret_cast<bf16_t*>(partial), m, n, k / splits, e, tiles_m, tiles_n, 16 / MT, ConvGeom{});
 }
 
+// The partials of an S-slice split on the tile height splitk_tile_mt picks for it.
+void launch_splitk_partials(const bf16_t* a, const bf16_t* b, float* partial, int64_t m, int64_t n,
+                            int64_t k, int splits, hipStream_t s) {
+    switch (splitk_tile_mt(m, n, k, splits)) {
+        case 1: launch_tn_splitk<1>(a, b, partial, m, n, k, splits, s); break;
+        case 2: launch_tn_splitk<2>(a, b, partial, m, n, k, splits, s); break;
+        case 3: launch_tn_splitk<3>(a, b, partial, m, n, k, splits, s); break;
+        default: launch_tn_splitk<kMaxMT>(a, b, partial, m, n, k, splits, s); break;
+    }
+}
+
 // The split-K reductions below take the slice count S as a template argument, so a thread issues
 // the loads of all S slices (and of the residual and gate) before the first addition: with a
 // run-time count each slice's load waited for the previous slice's sum, S + 1 memory round trips
@@ -697,12 +708,7 @@ void launch_gemm_bf16(const bf16_t* a, const bf16_t* b, const bf16_t* bias, bf16
             partial = splitk_workspace(floats);
         }
         ProfileScope ps(K_GEMM, s, flops, gemm_subclass());
-        switch (splitk_tile_mt(m, n, k, splits)) {
-            case 1: launch_tn_splitk<1>(a, b, partial, m, n, k, splits, s); break;
-            case 2: launch_tn_splitk<2>(a, b, partial, m, n, k, splits, s); break;
-            case 3: launch_tn_splitk<3>(a, b, partial, m, n, k, splits, s); break;
-            default: launch_tn_splitk<kMaxMT>(a, b, partial, m, n, k, splits, s); break;
-        }
+        launch_splitk_partials(a, b, partial, m, n, k, splits, s);
         launch_check("gemm (split-K partials)");
         switch (ep.act) {
             case 1: launch_splitk_epi<1>(mode, partial, splits, m, n, e, out, s); break;
@@ -793,7 +799,7 @@ void launch_gemm_splitk_residual(const bf16_t* a, const bf16_t* b, float* partia
             "gemm split-K: operands must be 16-byte aligned");
     {
         ProfileScope ps(K_GEMM, s, 2.0 * static_cast<double>(m) * n * k);
-        launch_tn_splitk(a, b, partial, m, n, k, splits, s);
+        launch_splitk_partials(a, b, partial, m, n, k, splits, s);
         launch_check("gemm (split-K partials)");
     }
     ProfileScope ps(K_ELEMENTWISE, s, static_cast<double>(m) * n * (4.0 * splits + 4.0));
