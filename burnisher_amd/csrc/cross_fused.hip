@@ -33,7 +33,7 @@ using G = gk::Geom<4>;
 constexpr int kHeadsPerTile = gk::BN / fk::D;           // 2
 constexpr int kChunk = 3;                               // live key blocks per head resident at once
 constexpr int kKeyStages = kHeadsPerTile * kChunk;      // 6 x 21 KiB
-constexpr int kCtileBytes = G::BM * gk::kCRow * 4;      // the parked fp32 tile
+constexpr int kCtileBytes = G::BM * gk::kCRow<gk::kNT> * 4;      // the parked fp32 tile
 constexpr int kBitsOff = kCtileBytes;                   // key-block validity words (after the tile)
 constexpr int kLiveOff = kBitsOff + fk::kResidentBlocks * 8;
 constexpr int kCountOff = kLiveOff + fk::kResidentBlocks * 4;
@@ -103,8 +103,8 @@ k_cross_fused(const bf16_t* __restrict__ X, const bf16_t* __restrict__ Wq, gk::E
                 bf16x8_t f = {};
                 if (d0 < fk::D) {
                     const int col = hh * fk::D + d0;
-                    const f32x4_t lo = *reinterpret_cast<const f32x4_t*>(ctile + gk::ctile_at(row, col));
-                    const f32x4_t hi = *reinterpret_cast<const f32x4_t*>(ctile + gk::ctile_at(row, col + 4));
+                    const f32x4_t lo = *reinterpret_cast<const f32x4_t*>(ctile + gk::ctile_at<>(row, col));
+                    const f32x4_t hi = *reinterpret_cast<const f32x4_t*>(ctile + gk::ctile_at<>(row, col + 4));
                     float bv[8];
                     if (e.bias) {
                         gk::unpack8(*reinterpret_cast<const uint4*>(bias_lds + col), bv);

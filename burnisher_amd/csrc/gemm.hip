@@ -44,11 +44,11 @@ namespace {
 #include "gemm_tile.inc"
 using namespace gk;
 
-template <int ACT, int MODE, bool CONV, int MT = kMaxMT>
+template <int ACT, int MODE, bool CONV, int MT = kMaxMT, int NT = kNT>
 __global__ void __launch_bounds__(kWgThreads, 1)
 k_gemm_tn(const bf16_t* __restrict__ A, const bf16_t* __restrict__ B, bf16_t* out, int64_t M,
           int64_t N, int64_t K, Epi e, int tiles_m, int tiles_n, int group_m, ConvGeom cv) {
-    __shared__ __attribute__((aligned(1024))) char smem[Geom<MT>::kSmemBytes];
+    __shared__ __attribute__((aligned(1024))) char smem[Geom<MT, NT>::kSmemBytes];
     const int T = tiles_m * tiles_n;
     const int my_tiles = (T - static_cast<int>(blockIdx.x) + static_cast<int>(gridDim.x) - 1) /
                          static_cast<int>(gridDim.x);
@@ -64,15 +64,15 @@ k_gemm_tn(const bf16_t* __restrict__ A, const bf16_t* __restrict__ B, bf16_t* ou
         out += static_cast<int64_t>(blockIdx.y) * M * e.ld_out * 2;   // float elements
     }
     if (wave >= kConsumers) {
-        produce<MT, CONV>(smem, Operands{A, B, M, N, K, cv, ldk, e.bias}, KT, my_tiles, tiles_m,
-                          tiles_n, group_m, wave - kConsumers, lane);
+        produce<MT, CONV, NT>(smem, Operands{A, B, M, N, K, cv, ldk, e.bias}, KT, my_tiles, tiles_m,
+                              tiles_n, group_m, wave - kConsumers, lane);
     } else {
-        consume<MT, ACT, MODE>(smem, e, out, M, N, KT, my_tiles, tiles_m, tiles_n, group_m, wave, lane);
+        consume<MT, ACT, MODE, NT>(smem, e, out, M, N, KT, my_tiles, tiles_m, tiles_n, group_m, wave, lane);
     }
     wait_and_join<63>();   // the parked tile is complete and visible
     int64_t m0, n0;
-    tile_origin<MT>(blockIdx.x + (my_tiles - 1) * gridDim.x, tiles_m, tiles_n, group_m, m0, n0);
-    store_staged<MT, ACT, MODE>(smem, e, out, M, N, m0, n0, bias_slot<MT>(smem, my_tiles - 1));
+    tile_origin<MT, NT>(blockIdx.x + (my_tiles - 1) * gridDim.x, tiles_m, tiles_n, group_m, m0, n0);
+    store_staged<MT, ACT, MODE, NT>(smem, e, out, M, N, m0, n0, bias_slot<MT, NT>(smem, my_tiles - 1));
 }
 
 // ---- small M: one wave per output column, both operands read with 16-byte loads ----
@@ -359,19 +359,19 @@ bool aligned(const void* p, int bytes) {
     return (reinterpret_cast<uintptr_t>(p) % bytes) == 0;
 }
 
-template <int ACT, int MODE, bool CONV = false, int MT = kMaxMT>
+template <int ACT, int MODE, bool CONV = false, int MT = kMaxMT, int NT = kNT>
 void launch_tn(const bf16_t* a, const bf16_t* b, bf16_t* out, int64_t m, int64_t n, int64_t k,
                const Epi& e, hipStream_t s, const ConvGeom& cv = ConvGeom{}) {
-    constexpr int BM = Geom<MT>::BM;
+    constexpr int BM = Geom<MT, NT>::BM;
     const int tiles_m = static_cast<int>((m + BM - 1) / BM);
-    const int tiles_n = static_cast<int>((n + BN - 1) / BN);
+    const int tiles_n = static_cast<int>((n + kBN<NT> - 1) / kBN<NT>);
     const int tiles = tiles_m * tiles_n;
     // One persistent workgroup per CU (the LDS stages allow no second one); with the tile count
     // a multiple of 8, so is the grid, which the XCD banding relies on. An XCD's band is walked
     // 16 / MT M-tiles (1024 rows; 960 at the 192-row tile) at a time whatever the tile height.
     int grid = min(tiles, device_cus() & ~7);
     if (grid < 8) grid = min(tiles, device_cus());
-    k_gemm_tn<ACT, MODE, CONV, MT><<<grid, kWgThreads, 0, s>>>(a, b, out, m, n, k, e, tiles_m, tiles_n,
+    k_gemm_tn<ACT, MODE, CONV, MT, NT><<<grid, kWgThreads, 0, s>>>(a, b, out, m, n, k, e, tiles_m, tiles_n,
                                                                16 / MT, cv);
 }
 
@@ -747,8 +747,16 @@ void launch_conv3x3_bf16(const ConvGeom& cv, const bf16_t* wr, const bf16_t* bia
           ep.ld_out > 0 ? ep.ld_out : c_out, 0, nullptr, 0, 0, 0, 0, 0, 72};
     require(ep.act == 0, "conv3x3: no activation epilogue (the decoder's SiLU follows a GroupNorm)");
     ProfileScope ps(K_GEMM, s, 2.0 * static_cast<double>(m) * c_out * k);
-    if (ep.residual) launch_tn<0, EPI_RESIDUAL, true>(cv.in, wr, out, m, c_out, k, e, s, cv);
-    else launch_tn<0, EPI_STORE, true>(cv.in, wr, out, m, c_out, k, e, s, cv);
+    // The decoder's channel counts are powers of two: 128-wide tiles cover them exactly, where
+    // 144-wide ones would pad every tile row by 16 columns (11% of the MFMAs).
+    const bool narrow = c_out % 128 == 0 && c_out % 144 != 0;
+    if (ep.residual) {
+        if (narrow) launch_tn<0, EPI_RESIDUAL, true, kMaxMT, 8>(cv.in, wr, out, m, c_out, k, e, s, cv);
+        else launch_tn<0, EPI_RESIDUAL, true>(cv.in, wr, out, m, c_out, k, e, s, cv);
+    } else {
+        if (narrow) launch_tn<0, EPI_STORE, true, kMaxMT, 8>(cv.in, wr, out, m, c_out, k, e, s, cv);
+        else launch_tn<0, EPI_STORE, true>(cv.in, wr, out, m, c_out, k, e, s, cv);
+    }
     launch_check("conv3x3 (mfma)");
 }
 
