@@ -375,24 +375,36 @@ void launch_tn(const bf16_t* a, const bf16_t* b, bf16_t* out, int64_t m, int64_t
                                                                16 / MT, cv);
 }
 
-// The tile height of a GEMM that runs whole (no split-K): the one with the least estimated time,
-// rounds x (rows a k-tile loads), where rounds = ceil(tiles / CUs) and a k-tile of a BM-row tile
-// loads BM + 144 rows of 128 bytes. The k-loop runs at the rate its operand stream is delivered,
-// not at the MFMA rate (~2,100 cycles per 256-row k-tile against 1,152 of MFMA issue), so a
-// shorter tile's k-tile is proportionally shorter. Ties keep the taller tile. Every height sums
-// each output's k-tiles in the same order with the same MFMAs, so results do not depend on it.
-int gemm_tile_mt(int64_t m, int64_t n) {
+// The tile shape of a GEMM that runs whole (no split-K): the height (64 MT rows) and width (16 NT
+// columns: 144, or 128 for widths that are multiples of 128) with the least
+// estimated time, rounds x (rows a k-tile loads), where rounds = ceil(tiles / CUs) and a k-tile of
+// a BM x BN tile loads BM + BN rows of 128 bytes. The k-loop runs at the rate its operand stream
+// is delivered, not at the MFMA rate (~2,100 cycles per 256 x 144 k-tile against 1,152 of MFMA
+// issue), so a smaller tile's k-tile is proportionally shorter. Ties keep the taller and the
+// 144-wide tile. Every shape sums each output's k-tiles in the same order with the same MFMAs, so
+// results do not depend on it.
+struct TileShape {
+    int mt, nt;
+};
+TileShape gemm_tile_shape(int64_t m, int64_t n) {
     const int64_t cus = device_cus();
-    const int64_t tiles_n = (n + BN - 1) / BN;
-    int best = kMaxMT;
+    TileShape best{kMaxMT, kNT};
     int64_t best_cost = -1;
-    for (int mt = kMaxMT; mt >= 1; --mt) {
-        const int64_t bm = 64 * mt;
-        const int64_t rounds = (((m + bm - 1) / bm) * tiles_n + cus - 1) / cus;
-        const int64_t cost = rounds * (bm + BN);
-        if (best_cost < 0 || cost < best_cost) {
-            best = mt;
-            best_cost = cost;
+    for (int nt : {kNT, 8}) {
+        if (nt == 8 && n % 128 != 0) continue;
+        const int64_t bn = 16 * nt, tiles_n = (n + bn - 1) / bn;
+        for (int mt = kMaxMT; mt >= 1; --mt) {
+            const int64_t bm = 64 * mt, tiles = ((m + bm - 1) / bm) * tiles_n;
+            // Over several rounds the XCD banding (tile_origin) needs a tile count divisible by
+            // 8; without it an XCD's tiles scatter over the operand panels. 1152px ff2 on 486
+            // 192 x 128 tiles measured 23% slower than on 432 of 192 x 144.
+            if (tiles > cus && tiles % 8 != 0 && !(mt == kMaxMT && nt == kNT)) continue;
+            const int64_t rounds = (tiles + cus - 1) / cus;
+            const int64_t cost = rounds * (bm + bn);
+            if (best_cost < 0 || cost < best_cost) {
+                best = {mt, nt};
+                best_cost = cost;
+            }
         }
     }
     return best;
@@ -591,21 +603,30 @@ void launch_splitk_epi(int mode, const float* partial, int splits, int64_t m, in
     }
 }
 
-template <int ACT, int MT>
+template <int ACT, int MT, int NT = kNT>
 void launch_tn_mode(int mode, const bf16_t* a, const bf16_t* b, bf16_t* out, int64_t m, int64_t n,
                     int64_t k, const Epi& e, hipStream_t s) {
     switch (mode) {
-        case EPI_STORE: launch_tn<ACT, EPI_STORE, false, MT>(a, b, out, m, n, k, e, s); break;
-        case EPI_ROW_ADD: launch_tn<ACT, EPI_ROW_ADD, false, MT>(a, b, out, m, n, k, e, s); break;
-        case EPI_RESIDUAL: launch_tn<ACT, EPI_RESIDUAL, false, MT>(a, b, out, m, n, k, e, s); break;
-        default: launch_tn<ACT, EPI_GATED, false, MT>(a, b, out, m, n, k, e, s); break;
+        case EPI_STORE: launch_tn<ACT, EPI_STORE, false, MT, NT>(a, b, out, m, n, k, e, s); break;
+        case EPI_ROW_ADD: launch_tn<ACT, EPI_ROW_ADD, false, MT, NT>(a, b, out, m, n, k, e, s); break;
+        case EPI_RESIDUAL: launch_tn<ACT, EPI_RESIDUAL, false, MT, NT>(a, b, out, m, n, k, e, s); break;
+        default: launch_tn<ACT, EPI_GATED, false, MT, NT>(a, b, out, m, n, k, e, s); break;
     }
 }
 
 template <int ACT>
-void launch_tn_mt(int mt, int mode, const bf16_t* a, const bf16_t* b, bf16_t* out, int64_t m, int64_t n,
+void launch_tn_mt(TileShape sh, int mode, const bf16_t* a, const bf16_t* b, bf16_t* out, int64_t m, int64_t n,
                   int64_t k, const Epi& e, hipStream_t s) {
-    switch (mt) {
+    if (sh.nt == 8) {
+        switch (sh.mt) {
+            case 1: launch_tn_mode<ACT, 1, 8>(mode, a, b, out, m, n, k, e, s); break;
+            case 2: launch_tn_mode<ACT, 2, 8>(mode, a, b, out, m, n, k, e, s); break;
+            case 3: launch_tn_mode<ACT, 3, 8>(mode, a, b, out, m, n, k, e, s); break;
+            default: launch_tn_mode<ACT, kMaxMT, 8>(mode, a, b, out, m, n, k, e, s); break;
+        }
+        return;
+    }
+    switch (sh.mt) {
         case 1: launch_tn_mode<ACT, 1>(mode, a, b, out, m, n, k, e, s); break;
         case 2: launch_tn_mode<ACT, 2>(mode, a, b, out, m, n, k, e, s); break;
         case 3: launch_tn_mode<ACT, 3>(mode, a, b, out, m, n, k, e, s); break;
@@ -719,7 +740,8 @@ void launch_gemm_bf16(const bf16_t* a, const bf16_t* b, const bf16_t* bias, bf16
         return;
     }
     ProfileScope ps(K_GEMM, s, flops, gemm_subclass());
-    const int mt = ep.vt ? kMaxMT : gemm_tile_mt(m, n);   // the transposed V store: 256-row tiles
+    // the transposed V store: 256 x 144 tiles
+    const TileShape mt = ep.vt ? TileShape{kMaxMT, kNT} : gemm_tile_shape(m, n);
     switch (ep.act) {
         case 1: launch_tn_mt<1>(mt, mode, a, b, out, m, n, k, e, s); break;
         case 2: launch_tn_mt<2>(mt, mode, a, b, out, m, n, k, e, s); break;
