@@ -411,30 +411,38 @@ TileShape gemm_tile_shape(int64_t m, int64_t n) {
 }
 
 // Split-K plans in the tile chooser's units (one operand row loaded per k-tile, ~2.75 ns): a
-// launch of S slices on BM-row tiles costs ceil(tiles * S / CUs) rounds of K / S / 64 k-tiles of
-// BM + 144 rows each, plus its fp32 partials, S * M * N * 4 bytes written and read again by the
+// launch of S slices on BM x BN tiles costs ceil(tiles * S / CUs) rounds of K / S / 64 k-tiles of
+// BM + BN rows each, plus its fp32 partials, S * M * N * 4 bytes written and read again by the
 // summing epilogue at ~4.7 TB/s (one unit per 12,800 bytes). Fewer slices on shorter tiles can
 // win: at 512px ff2 (2048 x 1152 x 4608) 2 slices of 128-row tiles instead of 4 of 256 rows
 // halve the partial traffic (gemm_ff2 1.217 -> 1.149 ms per step, interleaved A/B).
-int64_t splitk_cost(int64_t m, int64_t n, int64_t k, int mt, int splits) {
-    const int64_t bm = 64 * mt, cus = device_cus();
-    const int64_t tiles = ((m + bm - 1) / bm) * ((n + BN - 1) / BN);
+int64_t splitk_cost(int64_t m, int64_t n, int64_t k, TileShape sh, int splits) {
+    const int64_t bm = 64 * sh.mt, bn = 16 * sh.nt, cus = device_cus();
+    const int64_t tiles = ((m + bm - 1) / bm) * ((n + bn - 1) / bn);
     const int64_t rounds = (tiles * splits + cus - 1) / cus;
-    const int64_t loop = rounds * (k / BK / splits) * (bm + BN);
+    const int64_t loop = rounds * (k / BK / splits) * (bm + bn);
     const int64_t partials = splits > 1 ? static_cast<int64_t>(splits) * m * n * 8 / 12800 : 0;
     return loop + partials;
 }
 
-// The tile height of an S-slice launch: the cheapest by splitk_cost (ties keep the taller tile).
-// The height does not change any sum; the slice count does, and is decided on the full batch.
-int splitk_tile_mt(int64_t m, int64_t n, int64_t k, int splits) {
-    int best = kMaxMT;
+// The tile shape of an S-slice launch: the cheapest by splitk_cost (ties keep the taller and the
+// 144-wide tile; 128-wide for widths that are multiples of 128, with the XCD banding's tile count
+// kept whole over several rounds). The shape does not change any sum; the slice count does, and
+// is decided on the full batch.
+TileShape splitk_tile_shape(int64_t m, int64_t n, int64_t k, int splits) {
+    const int64_t cus = device_cus();
+    TileShape best{kMaxMT, kNT};
     int64_t best_cost = -1;
-    for (int mt = kMaxMT; mt >= 1; --mt) {
-        const int64_t c = splitk_cost(m, n, k, mt, splits);
-        if (best_cost < 0 || c < best_cost) {
-            best = mt;
-            best_cost = c;
+    for (int nt : {kNT, 8}) {
+        if (nt == 8 && n % 128 != 0) continue;
+        for (int mt = kMaxMT; mt >= 1; --mt) {
+            const int64_t bm = 64 * mt, bn = 16 * nt, tiles = ((m + bm - 1) / bm) * ((n + bn - 1) / bn);
+            if (tiles * splits > cus && tiles % 8 != 0 && !(mt == kMaxMT && nt == kNT)) continue;
+            const int64_t c = splitk_cost(m, n, k, TileShape{mt, nt}, splits);
+            if (best_cost < 0 || c < best_cost) {
+                best = {mt, nt};
+                best_cost = c;
+            }
         }
     }
     return best;
@@ -442,12 +450,12 @@ int splitk_tile_mt(int64_t m, int64_t n, int64_t k, int splits) {
 
 // Split-K partials: `splits` slices of K in one launch (grid.y = slice), each persistent
 // workgroup set over the same output tiles, slice s writing fp32 partial[s][m][n].
-template <int MT = kMaxMT>
+template <int MT = kMaxMT, int NT = kNT>
 void launch_tn_splitk(const bf16_t* a, const bf16_t* b, float* partial, int64_t m, int64_t n, int64_t k,
                       int splits, hipStream_t s) {
-    constexpr int BM = Geom<MT>::BM;
+    constexpr int BM = Geom<MT, NT>::BM;
     const int tiles_m = static_cast<int>((m + BM - 1) / BM);
-    const int tiles_n = static_cast<int>((n + BN - 1) / BN);
+    const int tiles_n = static_cast<int>((n + kBN<NT> - 1) / kBN<NT>);
     const int tiles = tiles_m * tiles_n;
     const int grid = max(1, min(tiles, device_cus() / splits));
     Epi e{};
@@ -456,14 +464,24 @@ void launch_tn_splitk(const bf16_t* a, const bf16_t* b, float* partial, int64_t 
     e.ld_out = n;
     e.ld_k = k;
     e.vt_dim = 72;
-    k_gemm_tn<0, EPI_F32, false, MT><<<dim3(grid, splits), kWgThreads, 0, s>>>(
+    k_gemm_tn<0, EPI_F32, false, MT, NT><<<dim3(grid, splits), kWgThreads, 0, s>>>(
         a, b, reinterpret_cast<bf16_t*>(partial), m, n, k / splits, e, tiles_m, tiles_n, 16 / MT, ConvGeom{});
 }
 
-// The partials of an S-slice split on the tile height splitk_tile_mt picks for it.
+// The partials of an S-slice split on the tile shape splitk_tile_shape picks for it.
 void launch_splitk_partials(const bf16_t* a, const bf16_t* b, float* partial, int64_t m, int64_t n,
                             int64_t k, int splits, hipStream_t s) {
-    switch (splitk_tile_mt(m, n, k, splits)) {
+    const TileShape sh = splitk_tile_shape(m, n, k, splits);
+    if (sh.nt == 8) {
+        switch (sh.mt) {
+            case 1: launch_tn_splitk<1, 8>(a, b, partial, m, n, k, splits, s); break;
+            case 2: launch_tn_splitk<2, 8>(a, b, partial, m, n, k, splits, s); break;
+            case 3: launch_tn_splitk<3, 8>(a, b, partial, m, n, k, splits, s); break;
+            default: launch_tn_splitk<kMaxMT, 8>(a, b, partial, m, n, k, splits, s); break;
+        }
+        return;
+    }
+    switch (sh.mt) {
         case 1: launch_tn_splitk<1>(a, b, partial, m, n, k, splits, s); break;
         case 2: launch_tn_splitk<2>(a, b, partial, m, n, k, splits, s); break;
         case 3: launch_tn_splitk<3>(a, b, partial, m, n, k, splits, s); break;
@@ -810,7 +828,7 @@ int gemm_splits(int64_t m, int64_t n, int64_t k, const GemmEpilogue& ep) {
     int64_t best_cost = -1;
     for (int sp = 1; sp <= 8; ++sp) {
         if (sp > 1 && (k % (BK * sp) != 0 || k / sp < 4 * BK)) continue;
-        const int64_t c = splitk_cost(m, n, k, splitk_tile_mt(m, n, k, sp), sp);
+        const int64_t c = splitk_cost(m, n, k, splitk_tile_shape(m, n, k, sp), sp);
         if (best_cost < 0 || c < best_cost) {
             best = sp;
             best_cost = c;
