@@ -322,8 +322,8 @@ int gemm_splitk_choice(int64_t m, int64_t n, int64_t k);
 // considered when K holds at least 48 k-tiles, at most half the CUs would hold a 256-row tile, the
 // MFMA kernel applies and the epilogue is a plain, residual or gated store (no row add, no
 // transposed V); then the slice count (up to 8) whose best tile height gives the least estimated
-// time, the fp32 partials' traffic included. The tile height of the split launch is chosen per
-// launch and changes no sum.
+// time, the fp32 partials' traffic included. The tile shape (height and width) of the split
+// launch is chosen per launch and changes no sum.
 int gemm_splits(int64_t m, int64_t n, int64_t k, const GemmEpilogue& ep);
 // out = bf16(residual + bf16(A . B^T)) through `splits` fp32 partials (partial holds
 // splits * m * n floats) summed in slice order; out may alias residual.
